@@ -1,0 +1,64 @@
+// Composite operators built from the primitive launchers:
+//  * SwiGlu (reference/swiglu.rs:40-84): gate and up projections, the fused
+//    silu(g)*u epilogue, then the down projection. The reference avoids an
+//    [rows, inter] temporary by accumulating rank-1 updates; on the GPU the
+//    intermediate goes to the device workspace (row chunks when it does not
+//    fit), which turns the three products into plain streaming GEMV/GEMMs.
+//  * RmsNormMatMul (reference/fused.rs:41-90): the normalised rows go to the
+//    workspace, then one matmul.
+#include "common.h"
+#include "kernels.h"
+
+namespace slhip {
+
+hipError_t launch_linear(const float* a, const WeightRef& w, float* out, uint64_t rows, uint64_t n,
+                         uint64_t k, float* workspace, uint64_t workspace_floats, hipStream_t s) {
+    if (w.quantized()) return launch_qmatmul(a, w.quant, out, rows, workspace, workspace_floats, s);
+    return launch_matmul(a, w.dense, out, 1, 1, 1, rows, k, n, true, s);
+}
+
+hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up, const WeightRef& down,
+                         float* out, uint64_t rows, uint64_t hidden, uint64_t inter, float* workspace,
+                         uint64_t workspace_floats, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    // Keep half of the workspace for the projections' own scratch.
+    const uint64_t budget = workspace_floats / 2;
+    uint64_t chunk = budget / (2 * inter);
+    if (chunk == 0) return hipErrorOutOfMemory;
+    if (chunk > rows) chunk = rows;
+    float* g = workspace;
+    float* u = workspace + chunk * inter;
+    float* rest = workspace + budget;
+    const uint64_t rest_floats = workspace_floats - budget;
+    for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
+        const uint64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
+        hipError_t e = launch_linear(x + r0 * hidden, gate, g, rc, inter, hidden, rest, rest_floats, s);
+        if (e == hipSuccess) e = launch_linear(x + r0 * hidden, up, u, rc, inter, hidden, rest, rest_floats, s);
+        if (e == hipSuccess) e = launch_silu_mul(g, u, g, rc * inter, s);
+        if (e == hipSuccess) e = launch_linear(g, down, out + r0 * hidden, rc, hidden, inter, rest, rest_floats, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_rms_norm_matmul(const float* x, const float* weight, const WeightRef& w, float* out,
+                                  uint64_t rows, uint64_t hidden, uint64_t out_features, float eps,
+                                  float* workspace, uint64_t workspace_floats, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    const uint64_t budget = workspace_floats / 2;
+    uint64_t chunk = budget / hidden;
+    if (chunk == 0) return hipErrorOutOfMemory;
+    if (chunk > rows) chunk = rows;
+    float* y = workspace;
+    for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
+        const uint64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
+        hipError_t e = launch_rms_norm(x + r0 * hidden, weight, y, rc, hidden, eps, s);
+        if (e == hipSuccess)
+            e = launch_linear(y, w, out + r0 * out_features, rc, out_features, hidden, workspace + budget,
+                              workspace_floats - budget, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace slhip

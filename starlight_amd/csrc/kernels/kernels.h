@@ -1,0 +1,92 @@
+// Host-side launchers of the gfx950 kernels. Every launcher enqueues on
+// `stream` and returns the launch status; shapes have already been validated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace slhip {
+
+// ---- elementwise (reference/elementwise.rs) ----
+hipError_t launch_add(const float* a, const float* b, float* out, uint64_t n, hipStream_t s);
+hipError_t launch_mul(const float* a, const float* b, float* out, uint64_t n, hipStream_t s);
+hipError_t launch_scale(const float* x, float* out, uint64_t n, float factor, hipStream_t s);
+hipError_t launch_silu(const float* x, float* out, uint64_t n, hipStream_t s);
+hipError_t launch_fill_zero(float* out, uint64_t n, hipStream_t s);
+
+// ---- norm / softmax (reference/norm.rs, reference/softmax.rs) ----
+hipError_t launch_rms_norm(const float* x, const float* w, float* out, uint64_t rows, uint64_t hidden,
+                           float eps, hipStream_t s);
+hipError_t launch_softmax(const float* x, float* out, uint64_t rows, uint64_t cols, bool causal,
+                          uint64_t seq, uint64_t past_len, hipStream_t s);
+
+// ---- rope (reference/rope.rs) ----
+hipError_t launch_rope(const float* x, const uint32_t* positions, float* out, uint64_t batch,
+                       uint64_t heads, uint64_t seq, uint64_t head_dim, float theta, bool interleaved,
+                       hipStream_t s);
+
+// ---- layout (reference/layout.rs, attention.rs kv_append) ----
+hipError_t launch_gather(const float* table, const uint32_t* ids, float* out, uint64_t rows,
+                         uint64_t hidden, hipStream_t s);
+hipError_t launch_last_token(const float* in, float* out, uint64_t batch, uint64_t seq, uint64_t hidden,
+                             uint64_t seq_len, hipStream_t s);
+hipError_t launch_heads_permute(const float* in, float* out, uint64_t batch, uint64_t seq,
+                                uint64_t heads, uint64_t head_dim, bool split, hipStream_t s);
+hipError_t launch_kv_append(const float* k, const float* v, float* cache, uint64_t batch,
+                            uint64_t layers, uint64_t layer, uint64_t kv_heads, uint64_t head_dim,
+                            uint64_t max_seq, uint64_t past_len, uint64_t seq, hipStream_t s);
+
+// ---- attention (reference/attention.rs causal_attention, after kv_append) ----
+struct AttentionArgs {
+    const float* q;
+    const float* cache;
+    float* out;
+    uint64_t batch, layers, layer, heads, kv_heads, seq, past_len, head_dim, max_seq;
+    float scale;
+};
+// `workspace` holds split-K partials; `workspace_floats` bounds the split.
+hipError_t launch_attention(const AttentionArgs& a, float* workspace, uint64_t workspace_floats,
+                            hipStream_t s);
+
+// ---- dense f32 matmul (reference/matmul.rs) ----
+// out[b] = a[b or 0] x op(b[b or 0]); op = transpose when `nt`.
+hipError_t launch_matmul(const float* a, const float* b, float* out, uint64_t batch, uint64_t batch_a,
+                         uint64_t batch_b, uint64_t m, uint64_t k, uint64_t n, bool nt, hipStream_t s);
+
+// ---- group-quantized weights (device-private tile layout) ----
+struct QuantWeight {
+    const uint8_t* tiles;  // repacked codes, see qmatmul.hip
+    const float* scales;   // [n, k / group]
+    uint32_t format;       // sl_qformat
+    uint32_t group;
+    uint64_t n, k;
+};
+// Repacks the row-major payload into the device tile layout.
+hipError_t launch_quant_repack(const uint8_t* payload, uint8_t* tiles, uint32_t format, uint64_t n,
+                               uint64_t k, hipStream_t s);
+uint64_t quant_tile_bytes(uint32_t format, uint64_t n, uint64_t k);
+// out[m, n] = sum_k a[m, k] * dequant(w)[n, k]  (a: [m, k] row-major)
+hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m,
+                          float* workspace, uint64_t workspace_floats, hipStream_t s);
+
+// ---- composites ----
+// Weights are dense f32 (pointer) or quantized (QuantWeight with tiles != null).
+struct WeightRef {
+    const float* dense;
+    QuantWeight quant;
+    bool quantized() const { return quant.tiles != nullptr; }
+};
+hipError_t launch_linear(const float* a, const WeightRef& w, float* out, uint64_t rows, uint64_t n,
+                         uint64_t k, float* workspace, uint64_t workspace_floats, hipStream_t s);
+// SwiGlu (reference/swiglu.rs): out = (silu(x Wg^T) * (x Wu^T)) Wd^T.
+hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up,
+                         const WeightRef& down, float* out, uint64_t rows, uint64_t hidden,
+                         uint64_t inter, float* workspace, uint64_t workspace_floats, hipStream_t s);
+// gate/up epilogue: h = silu(g) * u, elementwise over n values.
+hipError_t launch_silu_mul(const float* g, const float* u, float* h, uint64_t n, hipStream_t s);
+// RmsNormMatMul (reference/fused.rs): out = rms_norm(x, weight) W^T.
+hipError_t launch_rms_norm_matmul(const float* x, const float* weight, const WeightRef& w, float* out,
+                                  uint64_t rows, uint64_t hidden, uint64_t out_features, float eps,
+                                  float* workspace, uint64_t workspace_floats, hipStream_t s);
+
+}  // namespace slhip

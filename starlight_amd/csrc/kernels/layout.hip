@@ -1,0 +1,150 @@
+// Data movement: Gather, LastToken, SplitHeads/MergeHeads
+// (reference/layout.rs:25-166) and KvAppend (reference/attention.rs:33-83).
+//
+// All of them copy whole rows; a row is moved with 16-byte vectors when the
+// row length and both base pointers allow it. Gather ids were range-checked on
+// the host before the launch, as the reference checks every id before its
+// first write (layout.rs:207-213).
+#include "common.h"
+#include "kernels.h"
+
+namespace slhip {
+namespace {
+
+// Copies `rows` rows of `width` floats: dst row r <- src row map(r).
+// Mapping kinds: gather (src row = ids[r]), fixed stride pairs.
+__global__ __launch_bounds__(256) void gather_rows(const float* __restrict__ table, const uint32_t* __restrict__ ids,
+                                                   float* __restrict__ out, uint64_t hidden, bool vec) {
+    const uint64_t r = blockIdx.x;
+    const uint64_t src = static_cast<uint64_t>(ids[r]) * hidden;
+    const uint64_t dst = r * hidden;
+    if (vec) {
+        const float4* s4 = reinterpret_cast<const float4*>(table + src);
+        float4* d4 = reinterpret_cast<float4*>(out + dst);
+        for (uint64_t c = threadIdx.x; c < hidden / 4; c += blockDim.x) d4[c] = s4[c];
+    } else {
+        for (uint64_t c = threadIdx.x; c < hidden; c += blockDim.x) out[dst + c] = table[src + c];
+    }
+}
+
+__global__ __launch_bounds__(256) void last_token_rows(const float* __restrict__ in, float* __restrict__ out,
+                                                       uint64_t seq, uint64_t hidden, uint64_t position) {
+    const uint64_t b = blockIdx.x;
+    const float* src = in + (b * seq + position) * hidden;
+    float* dst = out + b * hidden;
+    for (uint64_t c = threadIdx.x; c < hidden; c += blockDim.x) dst[c] = src[c];
+}
+
+// [B, S, H, D] <-> [B, H, S, D]: one thread per output element group of VEC.
+template <int VEC, bool SPLIT>
+__global__ __launch_bounds__(256) void heads_permute(const float* __restrict__ in, float* __restrict__ out,
+                                                     uint64_t seq, uint64_t heads, uint64_t head_dim,
+                                                     uint64_t total) {
+    const uint64_t dv = head_dim / VEC;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+        // i enumerates the output in its own layout.
+        const uint64_t d = i % dv;
+        uint64_t rest = i / dv;
+        uint64_t b, h, t;
+        if (SPLIT) {  // out [B, H, S, D]
+            t = rest % seq; rest /= seq;
+            h = rest % heads; b = rest / heads;
+        } else {      // out [B, S, H, D]
+            h = rest % heads; rest /= heads;
+            t = rest % seq; b = rest / seq;
+        }
+        const uint64_t token_major = ((b * seq + t) * heads + h) * head_dim + d * VEC;
+        const uint64_t head_major = ((b * heads + h) * seq + t) * head_dim + d * VEC;
+        const uint64_t src = SPLIT ? token_major : head_major;
+        const uint64_t dst = SPLIT ? head_major : token_major;
+        if constexpr (VEC == 4)
+            *reinterpret_cast<float4*>(out + dst) = *reinterpret_cast<const float4*>(in + src);
+        else
+            out[dst] = in[src];
+    }
+}
+
+// k/v [B, Hkv, S, D] -> cache[b, layer, 0/1, past_len + t, h, :].
+template <int VEC>
+__global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                        float* __restrict__ cache, uint64_t kv_heads,
+                                                        uint64_t head_dim, uint64_t seq, uint64_t batch_stride,
+                                                        uint64_t layer_offset, uint64_t parity_stride,
+                                                        uint64_t past_len, uint64_t total) {
+    const uint64_t dv = head_dim / VEC;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const uint64_t d = i % dv;
+        uint64_t rest = i / dv;
+        const uint64_t t = rest % seq; rest /= seq;
+        const uint64_t h = rest % kv_heads;
+        const uint64_t b = rest / kv_heads;
+        const uint64_t src = ((b * kv_heads + h) * seq + t) * head_dim + d * VEC;
+        const uint64_t dst = b * batch_stride + layer_offset + (past_len + t) * kv_heads * head_dim +
+                             h * head_dim + d * VEC;
+        if constexpr (VEC == 4) {
+            *reinterpret_cast<float4*>(cache + dst) = *reinterpret_cast<const float4*>(k + src);
+            *reinterpret_cast<float4*>(cache + dst + parity_stride) = *reinterpret_cast<const float4*>(v + src);
+        } else {
+            cache[dst] = k[src];
+            cache[dst + parity_stride] = v[src];
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gather(const float* table, const uint32_t* ids, float* out, uint64_t rows,
+                         uint64_t hidden, hipStream_t s) {
+    if (rows == 0 || hidden == 0) return hipSuccess;
+    const bool vec = hidden % 4 == 0 && aligned16(table) && aligned16(out);
+    gather_rows<<<static_cast<unsigned>(rows), 256, 0, s>>>(table, ids, out, hidden, vec);
+    return hipGetLastError();
+}
+
+hipError_t launch_last_token(const float* in, float* out, uint64_t batch, uint64_t seq, uint64_t hidden,
+                             uint64_t seq_len, hipStream_t s) {
+    if (batch == 0 || hidden == 0) return hipSuccess;
+    last_token_rows<<<static_cast<unsigned>(batch), 256, 0, s>>>(in, out, seq, hidden, seq_len - 1);
+    return hipGetLastError();
+}
+
+hipError_t launch_heads_permute(const float* in, float* out, uint64_t batch, uint64_t seq,
+                                uint64_t heads, uint64_t head_dim, bool split, hipStream_t s) {
+    const uint64_t elements = batch * seq * heads * head_dim;
+    if (elements == 0) return hipSuccess;
+    const bool vec = head_dim % 4 == 0 && aligned16(in) && aligned16(out);
+    const uint64_t total = vec ? elements / 4 : elements;
+    const unsigned grid = grid_for(total, 256, 256 * 8);
+    if (vec) {
+        if (split) heads_permute<4, true><<<grid, 256, 0, s>>>(in, out, seq, heads, head_dim, total);
+        else heads_permute<4, false><<<grid, 256, 0, s>>>(in, out, seq, heads, head_dim, total);
+    } else {
+        if (split) heads_permute<1, true><<<grid, 256, 0, s>>>(in, out, seq, heads, head_dim, total);
+        else heads_permute<1, false><<<grid, 256, 0, s>>>(in, out, seq, heads, head_dim, total);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append(const float* k, const float* v, float* cache, uint64_t batch,
+                            uint64_t layers, uint64_t layer, uint64_t kv_heads, uint64_t head_dim,
+                            uint64_t max_seq, uint64_t past_len, uint64_t seq, hipStream_t s) {
+    const uint64_t elements = batch * kv_heads * seq * head_dim;
+    if (elements == 0) return hipSuccess;
+    const uint64_t parity_stride = max_seq * kv_heads * head_dim;
+    const uint64_t layer_stride = 2 * parity_stride;
+    const uint64_t batch_stride = layers * layer_stride;
+    const bool vec = head_dim % 4 == 0 && aligned16(k) && aligned16(v) && aligned16(cache);
+    const uint64_t total = vec ? elements / 4 : elements;
+    const unsigned grid = grid_for(total, 256, 256 * 8);
+    if (vec)
+        kv_append_kernel<4><<<grid, 256, 0, s>>>(k, v, cache, kv_heads, head_dim, seq, batch_stride,
+                                                 layer * layer_stride, parity_stride, past_len, total);
+    else
+        kv_append_kernel<1><<<grid, 256, 0, s>>>(k, v, cache, kv_heads, head_dim, seq, batch_stride,
+                                                 layer * layer_stride, parity_stride, past_len, total);
+    return hipGetLastError();
+}
+
+}  // namespace slhip

@@ -1,0 +1,102 @@
+// Dense f32 MatMulNT / MatMulNN (reference/matmul.rs:29-110) with the
+// equal-or-one batch broadcast of device.rs:1357-1407.
+//
+// LDS-tiled SGEMM: a 256-thread block computes a 64x64 output tile, each
+// thread a 4x4 register micro-tile, stepping K by 16 through LDS. Dense f32
+// weights only appear in small configurations (group-quantized weights use
+// qmatmul.hip), so this kernel favours generality: any shape, both B layouts,
+// any alignment. Products accumulate with fmaf in ascending k; the result
+// matches the reference's sequential f32 sum within the 1e-4 normwise bound.
+#include "common.h"
+#include "kernels.h"
+
+namespace slhip {
+namespace {
+
+constexpr int BM = 64, BN = 64, BK = 16;
+
+template <bool NT>
+__global__ __launch_bounds__(256) void sgemm_tiled(const float* __restrict__ a, const float* __restrict__ b,
+                                                   float* __restrict__ out, uint64_t m, uint64_t k, uint64_t n,
+                                                   uint64_t a_batch_stride, uint64_t b_batch_stride,
+                                                   uint64_t batch_base) {
+    __shared__ float as[BK][BM + 4];
+    __shared__ float bs[BK][BN + 4];
+    const uint64_t z = batch_base + blockIdx.z;
+    a += z * a_batch_stride;
+    b += z * b_batch_stride;
+    out += z * m * n;
+    const uint64_t row0 = static_cast<uint64_t>(blockIdx.y) * BM;
+    const uint64_t col0 = static_cast<uint64_t>(blockIdx.x) * BN;
+    const int tid = threadIdx.x;
+    const int ty = tid / 16, tx = tid % 16;
+    float acc[4][4] = {};
+
+    for (uint64_t k0 = 0; k0 < k; k0 += BK) {
+        // A tile: 64 rows x 16 k -> as[k][row]
+        for (int e = tid; e < BM * BK; e += 256) {
+            const int r = e / BK, c = e % BK;
+            const uint64_t gr = row0 + r, gc = k0 + c;
+            as[c][r] = (gr < m && gc < k) ? a[gr * k + gc] : 0.f;
+        }
+        // B tile: bs[k][col]
+        for (int e = tid; e < BN * BK; e += 256) {
+            if (NT) {
+                const int r = e / BK, c = e % BK;  // r: col of out, c: k
+                const uint64_t gn = col0 + r, gk = k0 + c;
+                bs[c][r] = (gn < n && gk < k) ? b[gn * k + gk] : 0.f;
+            } else {
+                const int c = e / BN, r = e % BN;  // c: k, r: col
+                const uint64_t gn = col0 + r, gk = k0 + c;
+                bs[c][r] = (gn < n && gk < k) ? b[gk * n + gn] : 0.f;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < BK; ++kk) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                av[i] = as[kk][ty * 4 + i];
+                bv[i] = bs[kk][tx * 4 + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint64_t gr = row0 + ty * 4 + i;
+        if (gr >= m) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint64_t gc = col0 + tx * 4 + j;
+            if (gc < n) out[gr * n + gc] = acc[i][j];
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_matmul(const float* a, const float* b, float* out, uint64_t batch, uint64_t batch_a,
+                         uint64_t batch_b, uint64_t m, uint64_t k, uint64_t n, bool nt, hipStream_t s) {
+    if (batch == 0 || m == 0 || n == 0) return hipSuccess;
+    const uint64_t a_stride = batch_a == 1 && batch > 1 ? 0 : m * k;
+    const uint64_t b_stride = batch_b == 1 && batch > 1 ? 0 : n * k;
+    const unsigned gx = static_cast<unsigned>((n + BN - 1) / BN);
+    const unsigned gy = static_cast<unsigned>((m + BM - 1) / BM);
+    for (uint64_t base = 0; base < batch; base += 65535) {
+        const unsigned gz = static_cast<unsigned>(batch - base < 65535 ? batch - base : 65535);
+        dim3 grid(gx, gy, gz);
+        if (nt) sgemm_tiled<true><<<grid, 256, 0, s>>>(a, b, out, m, k, n, a_stride, b_stride, base);
+        else sgemm_tiled<false><<<grid, 256, 0, s>>>(a, b, out, m, k, n, a_stride, b_stride, base);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace slhip

@@ -1,0 +1,250 @@
+// Group-quantized MatMulNT: out[m, n] = sum_k a[m, k] * (q[n, k] * s[n, k / G]).
+//
+// No reference kernel exists for this (sl-precision is absent from the
+// reference); the result must equal matmul_nt(a, dequant(q, s))
+// (reference/matmul.rs:29-59) within the normwise 1e-4 bound, and the decode
+// of each code is exact.
+//
+// Device-private layout (made by launch_quant_repack from the uploaded
+// payload): the same row-major bytes with every code stored offset-binary,
+// u = q + 8 (INT4 nibble) or u = q + 128 (INT8 byte), i.e. the payload XOR
+// 0x88 / 0x80. Offset-binary codes convert to f32 with one
+// v_cvt_f32_ubyte per element after a mask, and the offset is removed once per
+// 32-element chunk: sum_k q*x = sum_k u*x - off * sum_k x.
+//
+// Kernels
+//  * qgemv_valu — decode (small m): one wave owns 4 weight rows; lanes walk
+//    16-byte chunks of those rows, so a wave's load covers 1 KiB of one row
+//    contiguously; x chunks are shared by the 4 rows.
+//  * qgemm_tiled — large m: the SGEMM tile loop with the B tile decoded into
+//    LDS as f32.
+//  * qmm_generic — any k / group alignment (correctness path).
+#include "common.h"
+#include "kernels.h"
+#include "starlight_hip.h"
+
+namespace slhip {
+namespace {
+
+__global__ void xor_words(const uint32_t* __restrict__ in, uint32_t* __restrict__ out, uint64_t words,
+                          uint32_t mask) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words; i += stride)
+        out[i] = in[i] ^ mask;
+}
+
+__device__ __forceinline__ float ubyte(uint32_t w, int i) {
+    return static_cast<float>((w >> (8 * i)) & 0xffu);
+}
+
+// Sum of u*x over the 32 INT4 codes of one 16-byte chunk (8 per word;
+// byte j of a word holds k = 2j in its low and k = 2j + 1 in its high nibble).
+__device__ __forceinline__ float dot_chunk_int4(uint4 w, const float* x) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = words[i] & 0x0F0F0F0Fu;
+        const uint32_t hi = (words[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            d = fmaf(ubyte(lo, j), x[8 * i + 2 * j], d);
+            d = fmaf(ubyte(hi, j), x[8 * i + 2 * j + 1], d);
+        }
+    }
+    return d;
+}
+
+// Sum of u*x over the 16 INT8 codes of one 16-byte chunk.
+__device__ __forceinline__ float dot_chunk_int8(uint4 w, const float* x) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d = fmaf(ubyte(words[i], j), x[4 * i + j], d);
+    return d;
+}
+
+constexpr int kRowsPerWave = 4;
+
+// grid: (ceil(n / (4 waves * 4 rows)), m). Requires k % group == 0,
+// group % CK == 0 and 16-byte aligned rows (k % CK == 0).
+template <int BITS>
+__global__ __launch_bounds__(256) void qgemv_valu(const float* __restrict__ a, const uint8_t* __restrict__ tiles,
+                                                  const float* __restrict__ scales, float* __restrict__ out,
+                                                  uint32_t n, uint32_t k, uint32_t group) {
+    constexpr int CK = BITS == 4 ? 32 : 16;        // codes per 16-byte chunk
+    constexpr float OFF = BITS == 4 ? 8.f : 128.f;  // offset-binary bias
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t row0 = (blockIdx.x * 4 + threadIdx.x / kWave) * kRowsPerWave;
+    if (row0 >= n) return;
+    const uint64_t mrow = blockIdx.y;
+    const float* x = a + mrow * k;
+    const uint32_t chunks = k / CK;
+    const uint32_t row_bytes = BITS == 4 ? k / 2 : k;
+    const uint32_t groups = k / group;
+    float acc[kRowsPerWave] = {};
+    for (uint32_t c = lane; c < chunks; c += kWave) {
+        float xv[CK];
+        const float4* x4 = reinterpret_cast<const float4*>(x + static_cast<uint64_t>(c) * CK);
+#pragma unroll
+        for (int i = 0; i < CK / 4; ++i) {
+            const float4 v = x4[i];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+        float xs = 0.f;
+#pragma unroll
+        for (int i = 0; i < CK; ++i) xs += xv[i];
+        const uint32_t g = c * CK / group;
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r) {
+            const uint32_t row = row0 + r;
+            if (row >= n) break;
+            const uint4 w = *reinterpret_cast<const uint4*>(tiles + static_cast<uint64_t>(row) * row_bytes +
+                                                            static_cast<uint64_t>(c) * 16);
+            const float d = BITS == 4 ? dot_chunk_int4(w, xv) : dot_chunk_int8(w, xv);
+            const float part = fmaf(-OFF, xs, d);
+            acc[r] = fmaf(part, scales[static_cast<uint64_t>(row) * groups + g], acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+        const float v = wave_sum(acc[r]);
+        if (lane == 0 && row0 + r < n) out[mrow * n + row0 + r] = v;
+    }
+}
+
+__device__ __forceinline__ float decode(const uint8_t* tiles, uint32_t bits, uint64_t row_bytes, uint64_t r,
+                                        uint64_t c) {
+    if (bits == 4) {
+        const uint8_t byte = tiles[r * row_bytes + c / 2];
+        const int u = (c & 1) ? byte >> 4 : byte & 0x0F;
+        return static_cast<float>(u - 8);
+    }
+    return static_cast<float>(static_cast<int>(tiles[r * row_bytes + c]) - 128);
+}
+
+// One thread per output, any geometry.
+__global__ __launch_bounds__(256) void qmm_generic(const float* __restrict__ a, const uint8_t* __restrict__ tiles,
+                                                   const float* __restrict__ scales, float* __restrict__ out,
+                                                   uint64_t m, uint64_t n, uint64_t k, uint32_t group,
+                                                   uint32_t bits) {
+    const uint64_t total = m * n;
+    const uint64_t row_bytes = bits == 4 ? (k + 1) / 2 : k;
+    const uint64_t groups = k / group;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const uint64_t r = i / n, c = i % n;
+        float acc = 0.f;
+        for (uint64_t kk = 0; kk < k; ++kk)
+            acc = fmaf(a[r * k + kk], decode(tiles, bits, row_bytes, c, kk) * scales[c * groups + kk / group], acc);
+        out[i] = acc;
+    }
+}
+
+constexpr int BM = 64, BN = 64, BK = 16;
+
+// Large-m path: SGEMM tiles with B decoded into LDS (w = q * s in f32).
+__global__ __launch_bounds__(256) void qgemm_tiled(const float* __restrict__ a, const uint8_t* __restrict__ tiles,
+                                                   const float* __restrict__ scales, float* __restrict__ out,
+                                                   uint64_t m, uint64_t k, uint64_t n, uint32_t group,
+                                                   uint32_t bits) {
+    __shared__ float as[BK][BM + 4];
+    __shared__ float bs[BK][BN + 4];
+    const uint64_t row0 = static_cast<uint64_t>(blockIdx.y) * BM;
+    const uint64_t col0 = static_cast<uint64_t>(blockIdx.x) * BN;
+    const uint64_t row_bytes = bits == 4 ? (k + 1) / 2 : k;
+    const uint64_t groups = k / group;
+    const int tid = threadIdx.x;
+    const int ty = tid / 16, tx = tid % 16;
+    float acc[4][4] = {};
+    for (uint64_t k0 = 0; k0 < k; k0 += BK) {
+        for (int e = tid; e < BM * BK; e += 256) {
+            const int r = e / BK, c = e % BK;
+            const uint64_t gr = row0 + r, gc = k0 + c;
+            as[c][r] = (gr < m && gc < k) ? a[gr * k + gc] : 0.f;
+        }
+        for (int e = tid; e < BN * BK; e += 256) {
+            const int r = e / BK, c = e % BK;
+            const uint64_t gn = col0 + r, gk = k0 + c;
+            bs[c][r] = (gn < n && gk < k) ? decode(tiles, bits, row_bytes, gn, gk) * scales[gn * groups + gk / group]
+                                          : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < BK; ++kk) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                av[i] = as[kk][ty * 4 + i];
+                bv[i] = bs[kk][tx * 4 + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint64_t gr = row0 + ty * 4 + i;
+        if (gr >= m) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint64_t gc = col0 + tx * 4 + j;
+            if (gc < n) out[gr * n + gc] = acc[i][j];
+        }
+    }
+}
+
+}  // namespace
+
+uint64_t quant_tile_bytes(uint32_t format, uint64_t n, uint64_t k) {
+    const uint64_t bytes = format == SL_QFORMAT_INT4 ? n * ((k + 1) / 2) : n * k;
+    return (bytes + 3) / 4 * 4;
+}
+
+hipError_t launch_quant_repack(const uint8_t* payload, uint8_t* tiles, uint32_t format, uint64_t n,
+                               uint64_t k, hipStream_t s) {
+    const uint64_t words = quant_tile_bytes(format, n, k) / 4;
+    if (words == 0) return hipSuccess;
+    xor_words<<<grid_for(words, 256, 256 * 8), 256, 0, s>>>(
+        reinterpret_cast<const uint32_t*>(payload), reinterpret_cast<uint32_t*>(tiles), words,
+        format == SL_QFORMAT_INT4 ? 0x88888888u : 0x80808080u);
+    return hipGetLastError();
+}
+
+hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m, float* workspace,
+                          uint64_t workspace_floats, hipStream_t s) {
+    (void)workspace;
+    (void)workspace_floats;
+    if (m == 0 || w.n == 0) return hipSuccess;
+    if (w.k == 0) return launch_fill_zero(out, m * w.n, s);
+    const uint32_t bits = w.format == SL_QFORMAT_INT4 ? 4 : 8;
+    const uint32_t ck = bits == 4 ? 32 : 16;
+    const bool fast = w.k % ck == 0 && w.group % ck == 0 && w.k % w.group == 0 && aligned16(a) &&
+                      aligned16(w.tiles) && w.n <= 0xffffffffu && w.k <= 0xffffffffu;
+    if (fast && m <= 16) {
+        dim3 grid(static_cast<unsigned>((w.n + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave)),
+                  static_cast<unsigned>(m));
+        if (bits == 4)
+            qgemv_valu<4><<<grid, 256, 0, s>>>(a, w.tiles, w.scales, out, static_cast<uint32_t>(w.n),
+                                               static_cast<uint32_t>(w.k), w.group);
+        else
+            qgemv_valu<8><<<grid, 256, 0, s>>>(a, w.tiles, w.scales, out, static_cast<uint32_t>(w.n),
+                                               static_cast<uint32_t>(w.k), w.group);
+        return hipGetLastError();
+    }
+    if (w.k % w.group == 0 && m > 16) {
+        dim3 grid(static_cast<unsigned>((w.n + BN - 1) / BN), static_cast<unsigned>((m + BM - 1) / BM));
+        qgemm_tiled<<<grid, 256, 0, s>>>(a, w.tiles, w.scales, out, m, w.k, w.n, w.group, bits);
+        return hipGetLastError();
+    }
+    qmm_generic<<<grid_for(m * w.n, 256, 256 * 16), 256, 0, s>>>(a, w.tiles, w.scales, out, m, w.n, w.k,
+                                                                 w.group, bits);
+    return hipGetLastError();
+}
+
+}  // namespace slhip

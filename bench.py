@@ -1,0 +1,331 @@
+"""Decode benchmark: Llama-3-8B-shaped llama-dense, INT4 group-128 weights,
+batch 1, on one MI355X through the HIP device and the native engine.
+
+A step is one greedy decode step (one token): upload the token and position,
+dispatch the 516 commands of the compiled decode CommandBuffer, synchronize,
+download the 128256 logits and take the argmax. Before timing: a 1024-token
+prompt prefill and `--warmup` decode steps; the KV cache holds 4096
+positions. Weights are synthetic (N(0, 0.02) drawn on the GPU with torch,
+quantized with the same group-wise convention as starlight_amd.quant);
+embeddings and RMSNorm weights stay f32, lm_head is INT4.
+
+The JSON line also carries
+  roofline     — the INT4 q-GEMV (the decode's dominant kernel) on the
+                 [14336 x 4096] gate/up shape, timed with HIP events on the
+                 device stream over rotating weight copies (no MALL reuse):
+                 algorithmic bytes per launch / average launch time vs 8 TB/s;
+  cpu_baseline — the C oracle (scalar restatement of backend-cpu) on the
+                 host: one 8B-shaped layer decoding at 1024 cached positions
+                 plus a slice of lm_head, extrapolated to a full token.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+PROMPT_LEN = 1024
+MAX_SEQ = 4096
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------- weights ---
+
+
+def torch_quantize(w, group, qmax):
+    """The group-wise convention of starlight_amd.quant on a CUDA tensor:
+    scale = max|w| / qmax per group, q = clamp(round_half_away(w / scale))."""
+    import torch
+
+    n, k = w.shape
+    wg = w.view(n, k // group, group)
+    scales = wg.abs().amax(dim=2) / qmax
+    safe = torch.where(scales == 0, torch.ones_like(scales), scales)
+    r = wg / safe.unsqueeze(2)
+    t = torch.trunc(r)
+    frac = r - t
+    q = t + (frac >= 0.5).float() - (frac <= -0.5).float()
+    q = torch.clamp(q, -qmax, qmax)
+    q = torch.where((scales == 0).unsqueeze(2), torch.zeros_like(q), q)
+    return q.view(n, k).to(torch.int8), scales.contiguous()
+
+
+def torch_pack_int4(q):
+    import torch
+
+    nib = (q.to(torch.int16) & 0xF).to(torch.uint8)
+    packed = nib[:, 0::2] | (nib[:, 1::2] << 4)
+    return packed.contiguous().view(torch.int32).view(-1)
+
+
+def upload_synthetic_weights(dev, cfg, seed=0):
+    """Generates every weight of `cfg` on the GPU and uploads it through the
+    device contract; returns name -> BufferId."""
+    import torch
+
+    from starlight_amd.graph import weight_specs
+    from starlight_amd.ir import QuantFormat
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    bufs = {}
+    qmax = 7 if cfg.quant == QuantFormat.INT4 else 127
+    for spec in weight_specs(cfg):
+        if spec.kind == "norm":
+            bufs[spec.name] = dev.upload_new_f32(np.ones(spec.shape, np.float32))
+            continue
+        w = torch.randn(spec.shape, generator=g, device="cuda", dtype=torch.float32) * 0.02
+        if not spec.quantized:
+            bufs[spec.name] = dev.upload_new_f32(w.cpu().numpy())
+            del w
+            continue
+        q, scales = torch_quantize(w, cfg.group, qmax)
+        del w
+        if cfg.quant == QuantFormat.INT4:
+            words = torch_pack_int4(q)
+        else:
+            words = q.contiguous().view(torch.int32).view(-1)
+        pb = dev.upload_new_u32(words.cpu().numpy().view(np.uint32))
+        sb = dev.upload_new_f32(scales.cpu().numpy())
+        dev.bind_quantized(pb, sb, cfg.quant, cfg.group, spec.shape[0], spec.shape[1])
+        bufs[spec.name] = pb
+        del q, scales, words
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return bufs
+
+
+# ----------------------------------------------------------- hip events ---
+
+
+class HipTimer:
+    """hipEvent pair on a given stream (the device's own)."""
+
+    def __init__(self, stream):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.stream = ctypes.c_void_p(stream)
+        self.start, self.stop = ctypes.c_void_p(), ctypes.c_void_p()
+        assert self.hip.hipEventCreate(ctypes.byref(self.start)) == 0
+        assert self.hip.hipEventCreate(ctypes.byref(self.stop)) == 0
+
+    def begin(self):
+        assert self.hip.hipEventRecord(self.start, self.stream) == 0
+
+    def end_ms(self):
+        assert self.hip.hipEventRecord(self.stop, self.stream) == 0
+        assert self.hip.hipEventSynchronize(self.stop) == 0
+        ms = ctypes.c_float()
+        assert self.hip.hipEventElapsedTime(ctypes.byref(ms), self.start, self.stop) == 0
+        return ms.value
+
+
+def qgemv_roofline(dev, n=14336, k=4096, copies=16, launches=200):
+    """Times the INT4 g128 q-GEMV at [n x k], M = 1, over `copies` distinct
+    weight copies (16 x 31 MB > the 256 MB MALL) with HIP events."""
+    from starlight_amd import quant
+    from starlight_amd.ir import BufferRef, Op, QuantFormat, Value
+
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    words, scales = quant.quantize(w, 128, QuantFormat.INT4)
+    weights = []
+    for _ in range(copies):
+        pb = dev.upload_new_u32(words)
+        sb = dev.upload_new_f32(scales)
+        dev.bind_quantized(pb, sb, QuantFormat.INT4, 128, n, k)
+        weights.append(pb)
+    x = dev.upload_new_f32(rng.standard_normal(k).astype(np.float32))
+    outs = [dev.allocate_f32(n, 256) for _ in range(copies)]
+    wv = Value.quantized([n, k], QuantFormat.INT4, 128)
+    xv, ov = Value.f32([1, k]), Value.f32([1, n])
+
+    def run(i):
+        dev.dispatch(Op.matmul_nt(), [BufferRef(x, 0, k), BufferRef(weights[i % copies], 0, words.size)], [xv, wv],
+                     [BufferRef(outs[i % copies], 0, n)], [ov])
+
+    for i in range(copies * 2):
+        run(i)
+    dev.synchronize()
+    timer = HipTimer(dev.stream)
+    timer.begin()
+    for i in range(launches):
+        run(i)
+    ms = timer.end_ms()
+    avg_us = ms * 1000.0 / launches
+    algorithmic = n * k // 2 + n * (k // 128) * 4 + k * 4 + n * 4
+    achieved = algorithmic / (avg_us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": f"q-GEMV INT4 g128 [{n}x{k}] M=1", "bytes_per_launch": algorithmic,
+            "avg_launch_us": round(avg_us, 3)}
+
+
+# ------------------------------------------------------------ cpu leg ------
+
+
+def cpu_baseline(cfg, budget_s=25.0):
+    """Times the oracle (scalar C restatement of backend-cpu, one core) on one
+    8B-shaped layer decoding with 1024 positions already cached, plus a
+    lm_head slice, and extrapolates to a full token."""
+    import oracle
+    from oracle.cpu_device import OracleDevice
+    from starlight_amd import engine, graph
+    from starlight_amd.graph import LlamaConfig
+
+    one = LlamaConfig(layers=1, hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.kv_heads, head_dim=cfg.head_dim,
+                      ffn=cfg.ffn, vocab=8, eps=cfg.eps, theta=cfg.theta, quant=cfg.quant, group=cfg.group,
+                      quant_lm_head=False)
+    rng = np.random.default_rng(9)
+    dev = OracleDevice()
+    weights = {}
+    from starlight_amd.graph import weight_specs
+    for spec in weight_specs(one):
+        weights[spec.name] = (np.ones(spec.shape, np.float32) if spec.kind == "norm" else
+                              (rng.standard_normal(spec.shape, dtype=np.float32) * np.float32(0.02)))
+    bufs = engine.upload_weights(dev, one, weights)
+    pre = graph.lower_llama(one, 1, 1, PROMPT_LEN + 8)
+    eng = engine.Engine(dev, engine.compile_program(pre, bufs), engine.compile_program(pre, bufs), 1,
+                        PROMPT_LEN + 8)
+    kv = eng.states[pre.kv_cache]
+    dev.f32[kv][:] = rng.uniform(-1, 1, dev.f32[kv].size).astype(np.float32)
+    logits = np.zeros(8, np.float32)
+    t0 = time.perf_counter()
+    steps = 0
+    while steps < 3 and time.perf_counter() - t0 < budget_s * 0.6:
+        eng.step(eng.DECODE, [1], [PROMPT_LEN + steps], 1, PROMPT_LEN + steps, logits)
+        steps += 1
+    per_layer = (time.perf_counter() - t0) / steps
+    # lm_head: a 1/16 row slice of [vocab, hidden] through oracle matmul_nt
+    rows = cfg.vocab // 16
+    w = rng.standard_normal((rows, cfg.hidden), dtype=np.float32)
+    x = rng.standard_normal(cfg.hidden).astype(np.float32)
+    t1 = time.perf_counter()
+    oracle.matmul_nt(x, w, 1, 1, cfg.hidden, rows)
+    lm_head = (time.perf_counter() - t1) * 16
+    per_token = per_layer * cfg.layers + lm_head
+    return {"value": round(1.0 / per_token, 5), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": (f"oracle decode of one 8B-shaped layer (dequantized INT4 weights, 1024 cached positions) "
+                       f"x {steps} steps = {per_layer:.3f} s/layer, x{cfg.layers} layers + lm_head "
+                       f"(1/16 slice timed, x16) = {per_token:.2f} s/token; extrapolated")}
+
+
+# ------------------------------------------------------------------ main ---
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--int8", action="store_true", help="INT8 g128 weights instead of INT4")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU runs are not part of "
+                                   "this build (use --gpus 1)"}))
+        sys.exit(2)
+
+    import torch
+
+    from starlight_amd import engine, graph, synth
+    from starlight_amd.device import HipDevice
+    from starlight_amd.ir import QuantFormat
+
+    cfg = graph.LLAMA_8B_INT8 if args.int8 else graph.LLAMA_8B_INT4
+    assert PROMPT_LEN + args.warmup + args.steps <= MAX_SEQ
+    torch.cuda.init()
+    dev = HipDevice(0)
+    t0 = time.perf_counter()
+    bufs = upload_synthetic_weights(dev, cfg, seed=0)
+    log(f"weights generated and uploaded in {time.perf_counter() - t0:.1f} s")
+    pre = engine.compile_program(graph.lower_llama(cfg, 1, PROMPT_LEN, MAX_SEQ), bufs)
+    dec = engine.compile_program(graph.lower_llama(cfg, 1, 1, MAX_SEQ), bufs)
+    eng = engine.NativeEngine(dev, pre, dec, 1, MAX_SEQ)
+
+    prompt = synth.prompt(cfg.vocab, PROMPT_LEN, 0)
+    logits = np.zeros(cfg.vocab, np.float32)
+    t0 = time.perf_counter()
+    eng.step(eng.PREFILL, prompt, np.arange(PROMPT_LEN, dtype=np.uint32), PROMPT_LEN, 0, logits)
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {PROMPT_LEN} tokens: {prefill_s * 1000:.1f} ms")
+    token = int(np.argmax(logits))
+    past = PROMPT_LEN
+    warm = eng.decode(token, past, args.warmup)
+    token, past = int(warm[-1]) if args.warmup else token, past + args.warmup
+
+    dev.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    timed = eng.decode(token, past, args.steps)
+    dev.synchronize()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1000.0 / args.steps
+    tok_s = args.steps / elapsed
+    log(f"decode: {tok_s:.1f} tok/s ({ms_per_step:.3f} ms/step); last tokens {timed[-4:].tolist()}")
+
+    # bytes one decode step must move at least (weights + KV read at the timed positions)
+    linear = 0
+    from starlight_amd.graph import weight_specs
+    for spec in weight_specs(cfg):
+        if spec.quantized:
+            n, k = spec.shape
+            linear += n * k // (2 if cfg.quant == QuantFormat.INT4 else 1) + n * (k // cfg.group) * 4
+        elif spec.kind == "norm":
+            linear += spec.shape[0] * 4
+    avg_keys = past + (args.steps + 1) / 2
+    kv_bytes = avg_keys * cfg.layers * 2 * cfg.kv_heads * cfg.head_dim * 4
+    step_bytes = linear + cfg.hidden * 4 + kv_bytes
+    hbm_frac = step_bytes / (ms_per_step * 1e-3) / (HBM_PEAK_GBS * 1e9)
+
+    roof = qgemv_roofline(dev)
+    log(f"q-GEMV roofline: {roof}")
+    cpu = None if args.no_cpu else cpu_baseline(cfg)
+    if cpu:
+        log(f"cpu baseline: {cpu}")
+
+    quant_name = "INT8" if args.int8 else "INT4"
+    result = {
+        "metric": f"decode tok/s (8B-shape {quant_name} g128, bs=1)",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"Llama-3-8B-shaped llama-dense decode, {quant_name} g128 linear weights "
+                               f"(lm_head {quant_name}, embeddings/norms f32), batch 1, {PROMPT_LEN}-token prompt, "
+                               f"KV cache 4096 positions",
+                   "layers": cfg.layers, "hidden": cfg.hidden, "heads": cfg.heads, "kv_heads": cfg.kv_heads,
+                   "head_dim": cfg.head_dim, "ffn": cfg.ffn, "vocab": cfg.vocab, "batch": 1,
+                   "prompt_len": PROMPT_LEN, "kv_capacity": MAX_SEQ},
+        "decode_step_bytes": int(step_bytes),
+        "decode_hbm_frac": round(hbm_frac, 4),
+        "prefill_tok_s": round(PROMPT_LEN / prefill_s, 1),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    eng.close()
+    dev.close()
+
+
+if __name__ == "__main__":
+    main()

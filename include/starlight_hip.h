@@ -258,6 +258,11 @@ typedef struct sl_capabilities {
 
 void sl_hip_capabilities(sl_capabilities *out);
 
+/* The hipStream_t the device enqueues all work on (as void*), so a caller
+ * can record HIP events around its dispatches for timing. No reference
+ * counterpart (CpuDevice has no stream). */
+void *sl_hip_stream(const sl_hip_device *device);
+
 /* ABI version of the loaded library (SL_HIP_ABI_VERSION). */
 uint32_t sl_hip_abi_version(void);
 

@@ -430,6 +430,8 @@ sl_status sl_hip_bind_quantized(sl_hip_device* d, uint32_t payload, uint32_t sca
     return SL_OK;
 }
 
+void* sl_hip_stream(const sl_hip_device* d) { return d->stream; }
+
 void sl_hip_capabilities(sl_capabilities* out) {
     out->backend = "hip-gfx950";
     out->ir_version = SL_IR_VERSION;

@@ -1,0 +1,297 @@
+// Engine: restated sl-core Engine::build / Engine::step (ARCH-0007 §3.2)
+// over the C-ABI device. Everything a step needs — BufferRefs, port values,
+// scalar sources — is resolved in build(), so step() only uploads, loops
+// sl_hip_dispatch, synchronizes and downloads.
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "starlight_engine.h"
+#include "starlight_hip.h"
+
+namespace {
+
+enum class ScalarSource : uint8_t { SeqLen, PastLen };
+
+struct Resolved {
+    sl_op op;
+    sl_buffer_ref in[SL_MAX_INPUTS + 1];
+    sl_value in_vals[SL_MAX_INPUTS + 1];
+    size_t n_in = 0;
+    sl_buffer_ref out[SL_MAX_OUTPUTS];
+    sl_value out_vals[SL_MAX_OUTPUTS];
+    size_t n_out = 0;
+    ScalarSource scalars[SL_MAX_INPUTS];
+    size_t n_scalars = 0;
+};
+
+struct Program {
+    std::vector<Resolved> commands;
+    uint32_t token_buffer = UINT32_MAX, position_buffer = UINT32_MAX, logits_buffer = UINT32_MAX;
+    uint64_t token_elements = 0, position_elements = 0, logits_elements = 0;
+    uint64_t batch = 0, seq = 0;  // token_ids shape [batch, seq]
+    bool has_positions = false;
+};
+
+uint64_t element_count(const sl_value& v) {
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < v.rank && i < SL_MAX_RANK; ++i) n *= v.dims[i];
+    return n;
+}
+
+uint64_t payload_words(const sl_value& v) {
+    const uint64_t n = v.dims[0], k = v.dims[1];
+    const uint64_t bytes = v.qformat == SL_QFORMAT_INT4 ? n * ((k + 1) / 2) : n * k;
+    return (bytes + 3) / 4;
+}
+
+}  // namespace
+
+struct sl_engine {
+    sl_hip_device* device = nullptr;
+    Program programs[2];
+    uint32_t scratchpad = UINT32_MAX;
+    std::vector<std::pair<uint32_t, uint32_t>> states;  // (ValueId, BufferId)
+    std::vector<float> logits_host;
+    std::vector<uint32_t> token_host, position_host;
+    uint32_t max_batch = 0, max_context = 0;
+};
+
+namespace {
+
+struct BuildError {
+    sl_status status;
+};
+
+sl_status resolve_program(sl_engine* e, const sl_compiled_program* p, Program* out) {
+    const sl_command_buffer& ir = p->ir;
+    if (ir.ir_version != SL_IR_VERSION) return SL_ERR_EXECUTION;
+    const size_t nv = ir.n_values;
+    // ValueId -> BufferRef for every non-scalar value the commands touch.
+    std::vector<sl_buffer_ref> refs(nv);
+    std::vector<uint8_t> bound(nv, 0);
+    auto bind = [&](uint32_t vid, uint32_t buffer, uint64_t offset, uint64_t len) {
+        refs[vid] = sl_buffer_ref{buffer, 0, offset, len};
+        bound[vid] = 1;
+    };
+    for (size_t i = 0; i < p->n_weights; ++i) {
+        const uint32_t vid = p->weight_values[i];
+        if (vid >= nv) return SL_ERR_EXECUTION;
+        const sl_value& v = ir.values[vid];
+        const uint64_t len = v.encoding == SL_ENCODING_GROUPWISE_QUANTIZED ? payload_words(v) : element_count(v);
+        bind(vid, p->weight_buffers[i], 0, len);
+    }
+    for (size_t i = 0; i < ir.n_slots; ++i) {
+        const sl_slot& s = ir.slots[i];
+        if (s.value >= nv || s.offset % 4 != 0 || s.bytes % 4 != 0) return SL_ERR_EXECUTION;
+        bind(s.value, e->scratchpad, s.offset / 4, s.bytes / 4);
+    }
+    for (size_t vid = 0; vid < nv; ++vid) {
+        const sl_value& v = ir.values[vid];
+        if (bound[vid]) continue;
+        uint32_t buf = UINT32_MAX;
+        sl_status st = SL_OK;
+        switch (v.role) {
+            case SL_ROLE_STATE: {
+                for (auto& s : e->states)
+                    if (s.first == vid) buf = s.second;
+                if (buf == UINT32_MAX) {
+                    st = sl_hip_allocate_f32(e->device, element_count(v), 256, &buf);
+                    if (st != SL_OK) return st;
+                    e->states.push_back({static_cast<uint32_t>(vid), buf});
+                }
+                break;
+            }
+            case SL_ROLE_INPUT:
+                if (vid != p->token_ids && static_cast<int32_t>(vid) != p->positions) continue;
+                st = sl_hip_allocate_u32(e->device, element_count(v), 256, &buf);
+                if (st != SL_OK) return st;
+                break;
+            case SL_ROLE_OUTPUT:
+                st = sl_hip_allocate_f32(e->device, element_count(v), 256, &buf);
+                if (st != SL_OK) return st;
+                break;
+            default:
+                continue;  // scalars; unbound Params/Temps are caught per command below
+        }
+        bind(static_cast<uint32_t>(vid), buf, 0, element_count(v));
+    }
+    if (p->token_ids >= nv || !bound[p->token_ids]) return SL_ERR_EXECUTION;
+    out->token_buffer = refs[p->token_ids].buffer;
+    out->token_elements = element_count(ir.values[p->token_ids]);
+    const sl_value& tv = ir.values[p->token_ids];
+    out->batch = tv.rank >= 1 ? tv.dims[0] : 1;
+    out->seq = tv.rank >= 2 ? tv.dims[1] : 1;
+    if (p->positions >= 0) {
+        if (static_cast<size_t>(p->positions) >= nv || !bound[p->positions]) return SL_ERR_EXECUTION;
+        out->has_positions = true;
+        out->position_buffer = refs[p->positions].buffer;
+        out->position_elements = element_count(ir.values[p->positions]);
+    }
+    if (p->logits >= nv || !bound[p->logits]) return SL_ERR_EXECUTION;
+    out->logits_buffer = refs[p->logits].buffer;
+    out->logits_elements = element_count(ir.values[p->logits]);
+
+    out->commands.resize(ir.n_commands);
+    for (size_t c = 0; c < ir.n_commands; ++c) {
+        const sl_command& cmd = ir.commands[c];
+        Resolved& r = out->commands[c];
+        r.op = cmd.op;
+        if (cmd.n_inputs > SL_MAX_INPUTS || cmd.n_outputs > SL_MAX_OUTPUTS) return SL_ERR_EXECUTION;
+        for (uint32_t i = 0; i < cmd.n_inputs; ++i) {
+            const uint32_t vid = cmd.inputs[i];
+            if (vid >= nv) return SL_ERR_EXECUTION;
+            const sl_value& v = ir.values[vid];
+            if (v.role == SL_ROLE_SCALAR) {
+                if (vid == p->seq_len) r.scalars[r.n_scalars++] = ScalarSource::SeqLen;
+                else if (static_cast<int32_t>(vid) == p->past_len) r.scalars[r.n_scalars++] = ScalarSource::PastLen;
+                else return SL_ERR_EXECUTION;
+                continue;
+            }
+            if (!bound[vid]) return SL_ERR_EXECUTION;
+            r.in[r.n_in] = refs[vid];
+            r.in_vals[r.n_in] = v;
+            ++r.n_in;
+        }
+        // Stateful commands get their State as an extra input port.
+        if (cmd.effect != SL_EFFECT_NONE) {
+            if (cmd.state >= nv || !bound[cmd.state]) return SL_ERR_EXECUTION;
+            r.in[r.n_in] = refs[cmd.state];
+            r.in_vals[r.n_in] = ir.values[cmd.state];
+            ++r.n_in;
+        }
+        for (uint32_t i = 0; i < cmd.n_outputs; ++i) {
+            const uint32_t vid = cmd.outputs[i];
+            if (vid >= nv || !bound[vid]) return SL_ERR_EXECUTION;
+            r.out[r.n_out] = refs[vid];
+            r.out_vals[r.n_out] = ir.values[vid];
+            ++r.n_out;
+        }
+    }
+    return SL_OK;
+}
+
+uint32_t first_argmax(const float* v, size_t n) {
+    size_t best = 0;
+    for (size_t i = 1; i < n; ++i)
+        if (v[i] > v[best]) best = i;
+    return static_cast<uint32_t>(best);
+}
+
+}  // namespace
+
+extern "C" {
+
+sl_status sl_engine_build(sl_hip_device* device, const sl_compiled_program* prefill,
+                          const sl_compiled_program* decode, uint32_t max_batch, uint32_t max_context,
+                          sl_engine** out) {
+    *out = nullptr;
+    sl_engine* e = new (std::nothrow) sl_engine();
+    if (e == nullptr) return SL_ERR_OUT_OF_MEMORY;
+    e->device = device;
+    e->max_batch = max_batch;
+    e->max_context = max_context;
+    uint64_t scratch = prefill->ir.scratchpad_bytes;
+    if (decode->ir.scratchpad_bytes > scratch) scratch = decode->ir.scratchpad_bytes;
+    sl_status st = SL_OK;
+    if (scratch) st = sl_hip_allocate_f32(device, (scratch + 3) / 4, 256, &e->scratchpad);
+    if (st == SL_OK) st = resolve_program(e, prefill, &e->programs[SL_STEP_PREFILL]);
+    if (st == SL_OK) st = resolve_program(e, decode, &e->programs[SL_STEP_DECODE]);
+    if (st != SL_OK) {
+        delete e;
+        return st;
+    }
+    uint64_t most = 0, tok = 0, pos = 0;
+    for (auto& p : e->programs) {
+        if (p.logits_elements > most) most = p.logits_elements;
+        if (p.token_elements > tok) tok = p.token_elements;
+        if (p.position_elements > pos) pos = p.position_elements;
+    }
+    e->logits_host.resize(most);
+    e->token_host.resize(tok);
+    e->position_host.resize(pos);
+    *out = e;
+    return SL_OK;
+}
+
+sl_status sl_engine_step(sl_engine* e, uint32_t mode, const uint32_t* token_ids, size_t n_token_ids,
+                         const uint32_t* positions, size_t n_positions, uint32_t seq_len, uint32_t past_len,
+                         float* logits, size_t n_logits) {
+    if (mode > SL_STEP_DECODE) return SL_ERR_EXECUTION;
+    Program& p = e->programs[mode];
+    // step responsibility 1: inputs against the compiled capacities
+    if (n_token_ids != p.token_elements || (p.has_positions && n_positions != p.position_elements) ||
+        n_logits != p.logits_elements || seq_len == 0 || seq_len > p.seq ||
+        static_cast<uint64_t>(past_len) + seq_len > e->max_context)
+        return SL_ERR_EXECUTION;
+    // 2: upload token ids and positions
+    sl_status st = sl_hip_upload_u32(e->device, p.token_buffer, token_ids, n_token_ids);
+    if (st != SL_OK) return st;
+    if (p.has_positions) {
+        st = sl_hip_upload_u32(e->device, p.position_buffer, positions, n_positions);
+        if (st != SL_OK) return st;
+    }
+    // 3: dispatch in command order
+    uint32_t scalars[SL_MAX_INPUTS];
+    for (const Resolved& r : p.commands) {
+        for (size_t i = 0; i < r.n_scalars; ++i)
+            scalars[i] = r.scalars[i] == ScalarSource::SeqLen ? seq_len : past_len;
+        st = sl_hip_dispatch(e->device, &r.op, r.in, r.in_vals, r.n_in, r.out, r.out_vals, r.n_out, scalars,
+                             r.n_scalars);
+        if (st != SL_OK) return st;
+    }
+    // 4-5: synchronize, download logits
+    st = sl_hip_synchronize(e->device);
+    if (st != SL_OK) return st;
+    return sl_hip_download_f32(e->device, p.logits_buffer, logits, n_logits);
+}
+
+sl_status sl_engine_generate(sl_engine* e, const uint32_t* prompt, size_t prompt_len, uint32_t steps,
+                             uint32_t* tokens_out, float* logits_out, size_t vocab) {
+    Program& pf = e->programs[SL_STEP_PREFILL];
+    Program& dc = e->programs[SL_STEP_DECODE];
+    if (pf.batch != 1 || dc.batch != 1 || prompt_len != pf.seq || pf.logits_elements != vocab ||
+        dc.logits_elements != vocab || dc.seq != 1)
+        return SL_ERR_EXECUTION;
+    for (size_t i = 0; i < prompt_len; ++i) e->position_host[i] = static_cast<uint32_t>(i);
+    float* row = logits_out ? logits_out : e->logits_host.data();
+    sl_status st = sl_engine_step(e, SL_STEP_PREFILL, prompt, prompt_len, e->position_host.data(), prompt_len,
+                                  static_cast<uint32_t>(prompt_len), 0, row, vocab);
+    if (st != SL_OK) return st;
+    uint32_t token = first_argmax(row, vocab);
+    tokens_out[0] = token;
+    for (uint32_t s = 0; s < steps; ++s) {
+        const uint32_t past = static_cast<uint32_t>(prompt_len) + s;
+        row = logits_out ? logits_out + static_cast<size_t>(s + 1) * vocab : e->logits_host.data();
+        st = sl_engine_step(e, SL_STEP_DECODE, &token, 1, &past, 1, 1, past, row, vocab);
+        if (st != SL_OK) return st;
+        token = first_argmax(row, vocab);
+        tokens_out[s + 1] = token;
+    }
+    return SL_OK;
+}
+
+sl_status sl_engine_decode(sl_engine* e, uint32_t token, uint32_t past_len, uint32_t steps,
+                           uint32_t* tokens_out) {
+    Program& dc = e->programs[SL_STEP_DECODE];
+    if (dc.batch != 1 || dc.seq != 1) return SL_ERR_EXECUTION;
+    const size_t vocab = dc.logits_elements;
+    for (uint32_t s = 0; s < steps; ++s) {
+        const uint32_t past = past_len + s;
+        sl_status st = sl_engine_step(e, SL_STEP_DECODE, &token, 1, &past, 1, 1, past, e->logits_host.data(), vocab);
+        if (st != SL_OK) return st;
+        token = first_argmax(e->logits_host.data(), vocab);
+        tokens_out[s] = token;
+    }
+    return SL_OK;
+}
+
+uint32_t sl_engine_state_buffer(const sl_engine* e, uint32_t value) {
+    for (auto& s : e->states)
+        if (s.first == value) return s.second;
+    return UINT32_MAX;
+}
+
+void sl_engine_destroy(sl_engine* e) { delete e; }
+
+}  // extern "C"

@@ -157,6 +157,7 @@ def load_library() -> ctypes.CDLL:
                                       ctypes.POINTER(ir.CValue), ctypes.c_size_t, U32P, ctypes.c_size_t,
                                       ctypes.POINTER(ir.CError)], ctypes.c_int),
         "sl_hip_capabilities": ([ctypes.POINTER(ir.CCapabilities)], None),
+        "sl_hip_stream": ([P], ctypes.c_void_p),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -209,6 +210,11 @@ class HipDevice:
     @property
     def handle(self) -> ctypes.c_void_p:
         return self._h
+
+    @property
+    def stream(self) -> int:
+        """The device's hipStream_t (for HIP event timing)."""
+        return self._lib.sl_hip_stream(self._h)
 
     def _check(self, status: int) -> None:
         if status != 0:

@@ -33,6 +33,7 @@ namespace {
 
 constexpr uint64_t kMirrorMaxElements = 1ull << 22;        // host copy of u32 buffers up to 16 MiB
 constexpr uint64_t kWorkspaceBytes = 512ull << 20;          // split-K partials, SwiGlu intermediates
+constexpr uint64_t kCounterWords = 1ull << 16;              // cross-block completion counters (kept at zero)
 constexpr uint64_t kIdScratchElements = 1ull << 20;         // host scratch for unmirrored id checks
 
 struct Buffer {
@@ -44,6 +45,7 @@ struct Buffer {
     // group-quantized binding
     uint32_t scales = 0;
     uint8_t* tiles = nullptr;
+    QuantLayout layout = QuantLayout::RowMajor;
 };
 
 }  // namespace
@@ -54,6 +56,7 @@ struct Device : BufferView {
     std::vector<Buffer> buffers;
     float* workspace = nullptr;
     uint64_t workspace_floats = 0;
+    uint32_t* counters = nullptr;
     std::vector<uint32_t> id_scratch;
     Error last;
 
@@ -127,7 +130,7 @@ sl_status copy_in(Device* d, uint32_t id, const void* data, size_t len, uint32_t
     if (b.tiles) {
         // A re-uploaded quantized payload refreshes the private tile copy.
         e = launch_quant_repack(static_cast<const uint8_t*>(b.ptr), b.tiles, b.desc.qformat, b.desc.qn, b.desc.qk,
-                                d->stream);
+                                b.layout, d->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
         if (e != hipSuccess) return d->hip_fail(e);
     }
@@ -185,6 +188,7 @@ WeightRef weight_ref(Device* d, const sl_buffer_ref& r, const QuantOperand& q) {
     }
     const Buffer& b = d->buffers[r.buffer];
     w.quant.tiles = b.tiles;
+    w.quant.layout = b.layout;
     w.quant.scales = static_cast<const float*>(d->buffers[b.scales].ptr);
     w.quant.format = q.format;
     w.quant.group = q.group;
@@ -196,8 +200,7 @@ WeightRef weight_ref(Device* d, const sl_buffer_ref& r, const QuantOperand& q) {
 // Enqueues the kernels of one validated command.
 hipError_t launch(Device* d, const Plan& p, const sl_buffer_ref* in, const sl_buffer_ref* out) {
     hipStream_t s = d->stream;
-    float* ws = d->workspace;
-    const uint64_t wsf = d->workspace_floats;
+    const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
     switch (p.code) {
         case SL_OP_MATMUL_NT:
         case SL_OP_MATMUL_NN: {
@@ -205,7 +208,7 @@ hipError_t launch(Device* d, const Plan& p, const sl_buffer_ref* in, const sl_bu
             if (p.quant[1].present) {
                 // [.., M, K] x quantized [N, K]: the batch folds into rows.
                 return launch_qmatmul(fptr(d, in[0]), weight_ref(d, in[1], p.quant[1]).quant, fptr(d, out[0]),
-                                      p.batch * p.m, ws, wsf, s);
+                                      p.batch * p.m, ws, s);
             }
             return launch_matmul(fptr(d, in[0]), fptr(d, in[1]), fptr(d, out[0]), p.batch, p.batch_a, p.batch_b,
                                  p.m, p.k, p.n, p.code == SL_OP_MATMUL_NT, s);
@@ -239,21 +242,18 @@ hipError_t launch(Device* d, const Plan& p, const sl_buffer_ref* in, const sl_bu
             return launch_kv_append(fptr(d, in[0]), fptr(d, in[1]), fptr(d, in[p.state_index]), p.batch, p.layers,
                                     p.layer, p.kv_heads, p.head_dim, p.max_seq, p.past_len, p.seq, s);
         case SL_OP_CAUSAL_ATTENTION: {
-            float* cache = fptr(d, in[p.state_index]);
-            hipError_t e = launch_kv_append(fptr(d, in[1]), fptr(d, in[2]), cache, p.batch, p.layers, p.layer,
-                                            p.kv_heads, p.head_dim, p.max_seq, p.past_len, p.seq, s);
-            if (e != hipSuccess) return e;
-            AttentionArgs a{fptr(d, in[0]), cache, fptr(d, out[0]), p.batch, p.layers, p.layer, p.heads,
-                            p.kv_heads, p.seq, p.past_len, p.head_dim, p.max_seq, p.scale};
-            return launch_attention(a, ws, wsf, s);
+            AttentionArgs a{fptr(d, in[0]), fptr(d, in[1]), fptr(d, in[2]), fptr(d, in[p.state_index]),
+                            fptr(d, out[0]), p.batch, p.layers, p.layer, p.heads, p.kv_heads, p.seq,
+                            p.past_len, p.head_dim, p.max_seq, p.scale};
+            return launch_attention(a, ws, s);
         }
         case SL_OP_SWIGLU:
             return launch_swiglu(fptr(d, in[0]), weight_ref(d, in[1], p.quant[1]), weight_ref(d, in[2], p.quant[2]),
                                  weight_ref(d, in[3], p.quant[3]), fptr(d, out[0]), p.rows, p.hidden, p.inter, ws,
-                                 wsf, s);
+                                 s);
         case SL_OP_RMS_NORM_MATMUL:
             return launch_rms_norm_matmul(fptr(d, in[0]), fptr(d, in[1]), weight_ref(d, in[2], p.quant[2]),
-                                          fptr(d, out[0]), p.rows, p.hidden, p.out_features, p.eps, ws, wsf, s);
+                                          fptr(d, out[0]), p.rows, p.hidden, p.out_features, p.eps, ws, s);
         default:
             return hipErrorInvalidValue;
     }
@@ -312,6 +312,13 @@ sl_status sl_hip_device_create(int ordinal, sl_hip_device** out) {
         return SL_ERR_OUT_OF_MEMORY;
     }
     d->workspace_floats = slhip::kWorkspaceBytes / 4;
+    if (hipMalloc(reinterpret_cast<void**>(&d->counters), slhip::kCounterWords * 4) != hipSuccess ||
+        hipMemset(d->counters, 0, slhip::kCounterWords * 4) != hipSuccess) {
+        (void)hipFree(d->workspace);
+        (void)hipStreamDestroy(d->stream);
+        delete d;
+        return SL_ERR_OUT_OF_MEMORY;
+    }
     d->id_scratch.resize(slhip::kIdScratchElements);
     *out = d;
     return SL_OK;
@@ -326,6 +333,7 @@ void sl_hip_device_destroy(sl_hip_device* d) {
         if (b.tiles) (void)hipFree(b.tiles);
     }
     if (d->workspace) (void)hipFree(d->workspace);
+    if (d->counters) (void)hipFree(d->counters);
     (void)hipStreamDestroy(d->stream);
     delete d;
 }
@@ -404,7 +412,8 @@ sl_status sl_hip_bind_quantized(sl_hip_device* d, uint32_t payload, uint32_t sca
         return d->fail(Error::execution("quantized payload size does not match [n, k]"));
     if (d->buffers[scales].desc.elements != static_cast<uint64_t>(n) * (k / group_size))
         return d->fail(Error::execution("quantized scale count does not match [n, k / group_size]"));
-    const uint64_t bytes = slhip::quant_tile_bytes(qformat, n, k);
+    const slhip::QuantLayout layout = slhip::quant_layout_for(qformat, n, k, group_size);
+    const uint64_t bytes = slhip::quant_tile_bytes(qformat, n, k, layout);
     if (pb.tiles) {
         (void)hipStreamSynchronize(d->stream);
         (void)hipFree(pb.tiles);
@@ -423,7 +432,8 @@ sl_status sl_hip_bind_quantized(sl_hip_device* d, uint32_t payload, uint32_t sca
     pb.desc.qn = n;
     pb.desc.qk = k;
     pb.scales = scales;
-    hipError_t e = slhip::launch_quant_repack(static_cast<const uint8_t*>(pb.ptr), pb.tiles, qformat, n, k,
+    pb.layout = layout;
+    hipError_t e = slhip::launch_quant_repack(static_cast<const uint8_t*>(pb.ptr), pb.tiles, qformat, n, k, layout,
                                               d->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
     if (e != hipSuccess) return d->hip_fail(e);

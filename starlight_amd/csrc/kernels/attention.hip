@@ -7,12 +7,19 @@
 // maximum (online softmax): m' = max(m, s), l' = l*e^(m-m') + e^(s-m'),
 // acc' = acc*e^(m-m') + e^(s-m')*v, out = acc / l. Same mathematics, one pass.
 //
-// Two kernels:
-//  * attn_split — one wave per (b, h, t, key chunk). Lanes split head_dim,
-//    the score is a wave reduction. The chunk count is chosen so decode
-//    (seq = 1) still launches thousands of waves (flash-decoding); partial
-//    (m, l, acc) go to the workspace and attn_merge combines them. With one
-//    chunk it writes the output directly.
+// Kernels:
+//  * attn_decode — decode and short chunks (group * seq <= 16 query rows per
+//    KV head): one launch does kv_append and attention. A block owns one
+//    (batch, KV head, key chunk); all query rows sharing that KV head are
+//    served from one read of the chunk's K/V rows, staged through LDS in
+//    sub-tiles. Rows at or after past_len come from the new K/V (and the
+//    owning block writes them to the cache). The grid depends only on
+//    max_seq, the chunk length on past_len + seq, so every block has work.
+//    Partial (m, l, acc) go to the workspace; the last block of each
+//    (batch, KV head) — counted with a device-scope atomic — merges them in
+//    chunk order and writes the output.
+//  * attn_split / attn_merge — other decode shapes: one wave per
+//    (b, h, t, key chunk), score by wave reduction, then a merge kernel.
 //  * attn_tiled — prefill: a block owns 64 queries of one head, two threads
 //    per query (each half of head_dim), and streams 32-key K/V tiles through
 //    LDS, so each K/V row read from L2 serves 64 queries.
@@ -24,6 +31,10 @@ namespace {
 
 struct Geo {
     const float* q;
+    const float* k_new;
+    const float* v_new;
+    float* wcache;
+    uint32_t* counters;
     const float* cache;
     float* out;
     float* ws;
@@ -128,6 +139,171 @@ __global__ __launch_bounds__(256) void attn_merge(Geo g) {
     }
 }
 
+
+constexpr int kDecodeRows = 16;   // query rows (group * seq) per KV head
+constexpr int kDecodeChunks = 32; // key chunks per (batch, KV head)
+
+// Dynamic LDS: q [R][D], k/v sub-tile [KT][D + 1], p [R][KT].
+template <int KT>
+__global__ __launch_bounds__(256) void attn_decode(Geo g) {
+    extern __shared__ float lds[];
+    __shared__ float m_run[kDecodeRows], l_run[kDecodeRows], corr[kDecodeRows];
+    __shared__ int is_last;
+    const uint32_t D = g.head_dim, S = g.seq, G = g.group;
+    const uint32_t R = G * S;  // query rows: r = gi * S + t
+    const uint32_t c = blockIdx.x, kvh = blockIdx.y;
+    const uint64_t b = blockIdx.z;
+    const int tid = threadIdx.x;
+    float* qs = lds;                        // [R][D]
+    float* ks = qs + R * D;                 // [KT][D + 1]
+    float* vs = ks + KT * (D + 1);          // [KT][D + 1]
+    float* ps = vs + KT * (D + 1);          // [R][KT]
+
+    const uint32_t keys = g.past_len + S;   // keys visible to the last query
+    const uint32_t chunk = (keys + g.chunks - 1) / g.chunks;
+    const uint32_t j0 = min(c * chunk, keys), j1 = min(j0 + chunk, keys);
+    const uint64_t time_stride = static_cast<uint64_t>(g.kv_heads) * D;
+    float* kbase = g.wcache + b * g.batch_stride + g.layer_offset + kvh * D;
+    float* vbase = kbase + g.parity_stride;
+
+    for (uint32_t i = tid; i < R * D; i += 256) {
+        const uint32_t r = i / D, d = i % D, gi = r / S, t = r % S;
+        qs[i] = g.q[((b * g.heads + kvh * G + gi) * S + t) * D + d];
+    }
+    if (tid < kDecodeRows) {
+        m_run[tid] = -INFINITY;
+        l_run[tid] = 0.f;
+    }
+    // each thread owns output elements e = tid + 256 i of the [R][D] tile
+    constexpr int kMaxOut = kDecodeRows * 256 / 256;
+    float acc[kMaxOut];
+#pragma unroll
+    for (int i = 0; i < kMaxOut; ++i) acc[i] = 0.f;
+
+    for (uint32_t jt = j0; jt < j1; jt += KT) {
+        const uint32_t nk = min(static_cast<uint32_t>(KT), j1 - jt);
+        __syncthreads();
+        // K/V sub-tile: cached rows from the cache, new rows from k_new/v_new
+        // (and appended to the cache by this block, kv_append attention.rs:33-83)
+        for (uint32_t i = tid; i < KT * D; i += 256) {
+            const uint32_t jj = i / D, d = i % D, j = jt + jj;
+            float kv = 0.f, vv = 0.f;
+            if (jj < nk) {
+                if (j < g.past_len) {
+                    kv = kbase[j * time_stride + d];
+                    vv = vbase[j * time_stride + d];
+                } else {
+                    const uint64_t src = ((b * g.kv_heads + kvh) * S + (j - g.past_len)) * D + d;
+                    kv = g.k_new[src];
+                    vv = g.v_new[src];
+                    kbase[j * time_stride + d] = kv;
+                    vbase[j * time_stride + d] = vv;
+                }
+            }
+            ks[jj * (D + 1) + d] = kv;
+            vs[jj * (D + 1) + d] = vv;
+        }
+        __syncthreads();
+        // scores: one (row, key) pair per thread
+        for (uint32_t i = tid; i < R * KT; i += 256) {
+            const uint32_t r = i / KT, jj = i % KT;
+            const uint32_t t = r % S;
+            float dot = 0.f;
+            const float* qr = qs + r * D;
+            const float* kr = ks + jj * (D + 1);
+            for (uint32_t d = 0; d < D; ++d) dot = fmaf(qr[d], kr[d], dot);
+            const bool vis = jj < nk && jt + jj <= g.past_len + t;
+            ps[r * KT + jj] = vis ? dot * g.scale : -INFINITY;
+        }
+        __syncthreads();
+        // online-softmax update per row (one thread per row)
+        if (tid < static_cast<int>(R)) {
+            const float* pr = ps + tid * KT;
+            float mx = -INFINITY;
+            for (int jj = 0; jj < KT; ++jj) mx = fmaxf(mx, pr[jj]);
+            const float m_old = m_run[tid];
+            const float m_new = fmaxf(m_old, mx);
+            float cr = 1.f, sum = 0.f;
+            if (m_new != -INFINITY) {
+                cr = expf(m_old - m_new);
+                for (int jj = 0; jj < KT; ++jj) {
+                    const float p = expf(pr[jj] - m_new);
+                    ps[tid * KT + jj] = p;
+                    sum += p;
+                }
+            } else {
+                for (int jj = 0; jj < KT; ++jj) ps[tid * KT + jj] = 0.f;
+            }
+            corr[tid] = cr;
+            m_run[tid] = m_new;
+            l_run[tid] = l_run[tid] * cr + sum;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kMaxOut; ++i) {
+            const uint32_t e = tid + 256 * i;
+            if (e >= R * D) break;
+            const uint32_t r = e / D, d = e % D;
+            float a = acc[i] * corr[r];
+            const float* pr = ps + r * KT;
+            for (int jj = 0; jj < KT; ++jj) a = fmaf(pr[jj], vs[jj * (D + 1) + d], a);
+            acc[i] = a;
+        }
+    }
+
+    // partial of this chunk: [(b, kvh)][chunk][r][2 + D]
+    const uint64_t bk = b * g.kv_heads + kvh;
+    const uint64_t row_stride = 2 + D;
+    float* part = g.ws + (bk * g.chunks + c) * R * row_stride;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kMaxOut; ++i) {
+        const uint32_t e = tid + 256 * i;
+        if (e >= R * D) break;
+        part[(e / D) * row_stride + 2 + e % D] = acc[i];
+    }
+    if (tid < static_cast<int>(R)) {
+        part[tid * row_stride] = m_run[tid];
+        part[tid * row_stride + 1] = l_run[tid];
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&g.counters[bk], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = prev == g.chunks - 1;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    // merge the chunk partials in chunk order
+    const float* base = g.ws + bk * g.chunks * R * row_stride;
+    if (tid < static_cast<int>(R)) {
+        float mx = -INFINITY;
+        for (uint32_t cc = 0; cc < g.chunks; ++cc)
+            mx = fmaxf(mx, __builtin_nontemporal_load(&base[(cc * R + tid) * row_stride]));
+        float l = 0.f;
+        for (uint32_t cc = 0; cc < g.chunks; ++cc) {
+            const float lc = __builtin_nontemporal_load(&base[(cc * R + tid) * row_stride + 1]);
+            if (lc > 0.f) l += lc * expf(__builtin_nontemporal_load(&base[(cc * R + tid) * row_stride]) - mx);
+        }
+        m_run[tid] = mx;
+        l_run[tid] = 1.0f / l;
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < R * D; e += 256) {
+        const uint32_t r = e / D, d = e % D, gi = r / S, t = r % S;
+        float a = 0.f;
+        for (uint32_t cc = 0; cc < g.chunks; ++cc) {
+            const float* pc = base + (cc * R + r) * row_stride;
+            const float lc = __builtin_nontemporal_load(&pc[1]);
+            if (lc > 0.f) a = fmaf(__builtin_nontemporal_load(&pc[2 + d]), expf(__builtin_nontemporal_load(&pc[0]) - m_run[r]), a);
+        }
+        g.out[((b * g.heads + kvh * G + gi) * S + t) * D + d] = a * l_run[r];
+    }
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(&g.counters[bk], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 constexpr int kTileQ = 64;  // queries per block
 constexpr int kTileK = 32;  // keys per LDS tile
 
@@ -225,15 +401,18 @@ __global__ __launch_bounds__(128) void attn_tiled(Geo g) {
 
 }  // namespace
 
-hipError_t launch_attention(const AttentionArgs& a, float* workspace, uint64_t workspace_floats,
-                            hipStream_t s) {
+hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStream_t s) {
     const uint64_t queries = a.batch * a.heads * a.seq;
     if (queries == 0 || a.head_dim == 0) return hipSuccess;
     Geo g;
     g.q = a.q;
+    g.k_new = a.k_new;
+    g.v_new = a.v_new;
+    g.wcache = a.cache;
     g.cache = a.cache;
     g.out = a.out;
-    g.ws = workspace;
+    g.ws = ws.data;
+    g.counters = ws.counters;
     g.heads = static_cast<uint32_t>(a.heads);
     g.kv_heads = static_cast<uint32_t>(a.kv_heads);
     g.seq = static_cast<uint32_t>(a.seq);
@@ -245,6 +424,27 @@ hipError_t launch_attention(const AttentionArgs& a, float* workspace, uint64_t w
     g.batch_stride = a.layers * 2 * g.parity_stride;
     g.scale = a.scale;
 
+    // Fused decode path: kv_append + attention + merge in one launch.
+    const uint64_t rows = static_cast<uint64_t>(g.group) * a.seq;
+    const uint64_t pairs = a.batch * a.kv_heads;
+    if (rows <= kDecodeRows && a.head_dim <= 256 && pairs <= ws.n_counters &&
+        pairs * kDecodeChunks * rows * (a.head_dim + 2) <= ws.floats) {
+        g.chunks = kDecodeChunks;
+        g.chunk = 0;
+        dim3 grid(kDecodeChunks, g.kv_heads, static_cast<unsigned>(a.batch));
+        if (a.head_dim <= 128) {
+            const size_t lds = (rows * a.head_dim + 2 * 32 * (a.head_dim + 1) + rows * 32) * sizeof(float);
+            attn_decode<32><<<grid, 256, lds, s>>>(g);
+        } else {
+            const size_t lds = (rows * a.head_dim + 2 * 16 * (a.head_dim + 1) + rows * 16) * sizeof(float);
+            attn_decode<16><<<grid, 256, lds, s>>>(g);
+        }
+        return hipGetLastError();
+    }
+
+    hipError_t e = launch_kv_append(a.k_new, a.v_new, a.cache, a.batch, a.layers, a.layer, a.kv_heads, a.head_dim,
+                                    a.max_seq, a.past_len, a.seq, s);
+    if (e != hipSuccess) return e;
     const bool aligned = aligned16(a.q) && aligned16(a.cache) && aligned16(a.out);
     if (a.seq >= 16 && aligned && (a.head_dim == 64 || a.head_dim == 128)) {
         dim3 grid(static_cast<unsigned>((a.seq + kTileQ - 1) / kTileQ), g.heads, static_cast<unsigned>(a.batch));
@@ -262,7 +462,7 @@ hipError_t launch_attention(const AttentionArgs& a, float* workspace, uint64_t w
         chunks = (2048 + queries - 1) / queries;
         const uint64_t by_keys = (max_keys + 63) / 64;
         if (chunks > by_keys) chunks = by_keys;
-        const uint64_t by_ws = workspace_floats / (queries * (a.head_dim + 2));
+        const uint64_t by_ws = ws.floats / (queries * (a.head_dim + 2));
         if (chunks > by_ws) chunks = by_ws;
         if (chunks < 1) chunks = 1;
     }

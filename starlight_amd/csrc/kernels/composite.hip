@@ -12,30 +12,30 @@
 namespace slhip {
 
 hipError_t launch_linear(const float* a, const WeightRef& w, float* out, uint64_t rows, uint64_t n,
-                         uint64_t k, float* workspace, uint64_t workspace_floats, hipStream_t s) {
-    if (w.quantized()) return launch_qmatmul(a, w.quant, out, rows, workspace, workspace_floats, s);
+                         uint64_t k, const Workspace& ws, hipStream_t s) {
+    if (w.quantized()) return launch_qmatmul(a, w.quant, out, rows, ws, s);
     return launch_matmul(a, w.dense, out, 1, 1, 1, rows, k, n, true, s);
 }
 
 hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up, const WeightRef& down,
-                         float* out, uint64_t rows, uint64_t hidden, uint64_t inter, float* workspace,
-                         uint64_t workspace_floats, hipStream_t s) {
+                         float* out, uint64_t rows, uint64_t hidden, uint64_t inter, const Workspace& ws,
+                         hipStream_t s) {
     if (rows == 0) return hipSuccess;
     // Keep half of the workspace for the projections' own scratch.
-    const uint64_t budget = workspace_floats / 2;
-    uint64_t chunk = budget / (2 * inter);
+    const uint64_t budget = ws.floats / 2;
+    uint64_t chunk = budget > 64 ? (budget - 64) / (2 * inter) : 0;
     if (chunk == 0) return hipErrorOutOfMemory;
     if (chunk > rows) chunk = rows;
-    float* g = workspace;
-    float* u = workspace + chunk * inter;
-    float* rest = workspace + budget;
-    const uint64_t rest_floats = workspace_floats - budget;
+    const uint64_t u_off = (chunk * inter + 63) / 64 * 64;
+    float* g = ws.data;
+    float* u = ws.data + u_off;
+    const Workspace rest = ws.after(budget);
     for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
         const uint64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
-        hipError_t e = launch_linear(x + r0 * hidden, gate, g, rc, inter, hidden, rest, rest_floats, s);
-        if (e == hipSuccess) e = launch_linear(x + r0 * hidden, up, u, rc, inter, hidden, rest, rest_floats, s);
+        hipError_t e = launch_linear(x + r0 * hidden, gate, g, rc, inter, hidden, rest, s);
+        if (e == hipSuccess) e = launch_linear(x + r0 * hidden, up, u, rc, inter, hidden, rest, s);
         if (e == hipSuccess) e = launch_silu_mul(g, u, g, rc * inter, s);
-        if (e == hipSuccess) e = launch_linear(g, down, out + r0 * hidden, rc, hidden, inter, rest, rest_floats, s);
+        if (e == hipSuccess) e = launch_linear(g, down, out + r0 * hidden, rc, hidden, inter, rest, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -43,19 +43,18 @@ hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef&
 
 hipError_t launch_rms_norm_matmul(const float* x, const float* weight, const WeightRef& w, float* out,
                                   uint64_t rows, uint64_t hidden, uint64_t out_features, float eps,
-                                  float* workspace, uint64_t workspace_floats, hipStream_t s) {
+                                  const Workspace& ws, hipStream_t s) {
     if (rows == 0) return hipSuccess;
-    const uint64_t budget = workspace_floats / 2;
+    const uint64_t budget = ws.floats / 2;
     uint64_t chunk = budget / hidden;
     if (chunk == 0) return hipErrorOutOfMemory;
     if (chunk > rows) chunk = rows;
-    float* y = workspace;
+    float* y = ws.data;
     for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
         const uint64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
         hipError_t e = launch_rms_norm(x + r0 * hidden, weight, y, rc, hidden, eps, s);
         if (e == hipSuccess)
-            e = launch_linear(y, w, out + r0 * out_features, rc, out_features, hidden, workspace + budget,
-                              workspace_floats - budget, s);
+            e = launch_linear(y, w, out + r0 * out_features, rc, out_features, hidden, ws.after(budget), s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -7,6 +7,26 @@
 
 namespace slhip {
 
+// Device-owned scratch passed to kernels that need it: `data` for partial
+// results and intermediates, `counters` for cross-block completion counts.
+// Every kernel that uses a counter leaves it at zero when it finishes, so
+// the region stays zero between launches without any memset.
+struct Workspace {
+    float* data;
+    uint64_t floats;
+    uint32_t* counters;
+    uint64_t n_counters;
+
+    // The part of `data` after the first `used` floats (counters shared).
+    Workspace after(uint64_t used) const {
+        Workspace w = *this;
+        used = (used + 63) / 64 * 64;  // keep 256-byte alignment
+        w.data = used < floats ? data + used : data + floats;
+        w.floats = used < floats ? floats - used : 0;
+        return w;
+    }
+};
+
 // ---- elementwise (reference/elementwise.rs) ----
 hipError_t launch_add(const float* a, const float* b, float* out, uint64_t n, hipStream_t s);
 hipError_t launch_mul(const float* a, const float* b, float* out, uint64_t n, hipStream_t s);
@@ -36,38 +56,49 @@ hipError_t launch_kv_append(const float* k, const float* v, float* cache, uint64
                             uint64_t layers, uint64_t layer, uint64_t kv_heads, uint64_t head_dim,
                             uint64_t max_seq, uint64_t past_len, uint64_t seq, hipStream_t s);
 
-// ---- attention (reference/attention.rs causal_attention, after kv_append) ----
+// ---- attention (reference/attention.rs causal_attention, kv_append included) ----
 struct AttentionArgs {
     const float* q;
-    const float* cache;
+    const float* k_new;
+    const float* v_new;
+    float* cache;
     float* out;
     uint64_t batch, layers, layer, heads, kv_heads, seq, past_len, head_dim, max_seq;
     float scale;
 };
-// `workspace` holds split-K partials; `workspace_floats` bounds the split.
-hipError_t launch_attention(const AttentionArgs& a, float* workspace, uint64_t workspace_floats,
-                            hipStream_t s);
+// Appends k_new / v_new to the cache and computes the attention output.
+hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStream_t s);
 
 // ---- dense f32 matmul (reference/matmul.rs) ----
 // out[b] = a[b or 0] x op(b[b or 0]); op = transpose when `nt`.
 hipError_t launch_matmul(const float* a, const float* b, float* out, uint64_t batch, uint64_t batch_a,
                          uint64_t batch_b, uint64_t m, uint64_t k, uint64_t n, bool nt, hipStream_t s);
 
-// ---- group-quantized weights (device-private tile layout) ----
+// ---- group-quantized weights (device-private layouts, see qmatmul.hip) ----
+enum class QuantLayout : uint32_t {
+    RowMajor = 0,  // payload bytes with offset-binary codes
+    Mfma = 1,      // 16-row x 128-k superblocks in MFMA operand order
+};
 struct QuantWeight {
-    const uint8_t* tiles;  // repacked codes, see qmatmul.hip
+    const uint8_t* tiles;  // device-private copy of the codes
     const float* scales;   // [n, k / group]
     uint32_t format;       // sl_qformat
     uint32_t group;
     uint64_t n, k;
+    QuantLayout layout;
 };
-// Repacks the row-major payload into the device tile layout.
+QuantLayout quant_layout_for(uint32_t format, uint64_t n, uint64_t k, uint32_t group);
+uint64_t quant_tile_bytes(uint32_t format, uint64_t n, uint64_t k, QuantLayout layout);
+// Builds the private copy from the row-major payload.
 hipError_t launch_quant_repack(const uint8_t* payload, uint8_t* tiles, uint32_t format, uint64_t n,
-                               uint64_t k, hipStream_t s);
-uint64_t quant_tile_bytes(uint32_t format, uint64_t n, uint64_t k);
+                               uint64_t k, QuantLayout layout, hipStream_t s);
 // out[m, n] = sum_k a[m, k] * dequant(w)[n, k]  (a: [m, k] row-major)
-hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m,
-                          float* workspace, uint64_t workspace_floats, hipStream_t s);
+hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
+                          hipStream_t s);
+// The MFMA decode path (m <= 16, Mfma layout); returns hipErrorNotSupported
+// for shapes it does not take.
+hipError_t launch_qgemv_mfma(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
+                             hipStream_t s);
 
 // ---- composites ----
 // Weights are dense f32 (pointer) or quantized (QuantWeight with tiles != null).
@@ -77,16 +108,16 @@ struct WeightRef {
     bool quantized() const { return quant.tiles != nullptr; }
 };
 hipError_t launch_linear(const float* a, const WeightRef& w, float* out, uint64_t rows, uint64_t n,
-                         uint64_t k, float* workspace, uint64_t workspace_floats, hipStream_t s);
+                         uint64_t k, const Workspace& ws, hipStream_t s);
 // SwiGlu (reference/swiglu.rs): out = (silu(x Wg^T) * (x Wu^T)) Wd^T.
 hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up,
                          const WeightRef& down, float* out, uint64_t rows, uint64_t hidden,
-                         uint64_t inter, float* workspace, uint64_t workspace_floats, hipStream_t s);
+                         uint64_t inter, const Workspace& ws, hipStream_t s);
 // gate/up epilogue: h = silu(g) * u, elementwise over n values.
 hipError_t launch_silu_mul(const float* g, const float* u, float* h, uint64_t n, hipStream_t s);
 // RmsNormMatMul (reference/fused.rs): out = rms_norm(x, weight) W^T.
 hipError_t launch_rms_norm_matmul(const float* x, const float* weight, const WeightRef& w, float* out,
                                   uint64_t rows, uint64_t hidden, uint64_t out_features, float eps,
-                                  float* workspace, uint64_t workspace_floats, hipStream_t s);
+                                  const Workspace& ws, hipStream_t s);
 
 }  // namespace slhip

@@ -5,20 +5,25 @@
 // (reference/matmul.rs:29-59) within the normwise 1e-4 bound, and the decode
 // of each code is exact.
 //
-// Device-private layout (made by launch_quant_repack from the uploaded
-// payload): the same row-major bytes with every code stored offset-binary,
-// u = q + 8 (INT4 nibble) or u = q + 128 (INT8 byte), i.e. the payload XOR
-// 0x88 / 0x80. Offset-binary codes convert to f32 with one
-// v_cvt_f32_ubyte per element after a mask, and the offset is removed once per
-// 32-element chunk: sum_k q*x = sum_k u*x - off * sum_k x.
+// Device-private layouts (made by launch_quant_repack from the uploaded
+// payload):
+//  * Mfma (k % 128 == 0, group % 64 == 0): 16-row x 128-k superblocks in the
+//    MFMA operand order described in qgemv_mfma.hip — every shape the
+//    llama configurations use;
+//  * RowMajor (anything else): the payload bytes with every code stored
+//    offset-binary, u = q + 8 (INT4 nibble) or u = q + 128 (INT8 byte), i.e.
+//    the payload XOR 0x88 / 0x80. Offset-binary codes convert to f32 with one
+//    v_cvt_f32_ubyte per element after a mask, and the offset is removed once
+//    per 32-element chunk: sum_k q*x = sum_k u*x - off * sum_k x.
 //
 // Kernels
-//  * qgemv_valu — decode (small m): one wave owns 4 weight rows; lanes walk
-//    16-byte chunks of those rows, so a wave's load covers 1 KiB of one row
-//    contiguously; x chunks are shared by the 4 rows.
+//  * qgemv_mfma (qgemv_mfma.hip) — m <= 16 on the Mfma layout;
+//  * qgemv_valu — m <= 16 on the RowMajor layout: one wave owns 4 weight
+//    rows; lanes walk 16-byte chunks of those rows, so a wave's load covers
+//    1 KiB of one row contiguously; x chunks are shared by the 4 rows;
 //  * qgemm_tiled — large m: the SGEMM tile loop with the B tile decoded into
-//    LDS as f32.
-//  * qmm_generic — any k / group alignment (correctness path).
+//    LDS as f32 (either layout);
+//  * qmm_generic — any geometry (correctness path, either layout).
 #include "common.h"
 #include "kernels.h"
 #include "starlight_hip.h"
@@ -115,8 +120,21 @@ __global__ __launch_bounds__(256) void qgemv_valu(const float* __restrict__ a, c
     }
 }
 
+// Integer code of weight (r, c) in either private layout.
 __device__ __forceinline__ float decode(const uint8_t* tiles, uint32_t bits, uint64_t row_bytes, uint64_t r,
-                                        uint64_t c) {
+                                        uint64_t c, bool mfma, uint64_t sb_total) {
+    if (mfma) {
+        const uint64_t nt = r / 16, sb = c / 128;
+        const uint32_t s = (c % 128) / 64, lane = static_cast<uint32_t>(((c % 64) / 16) * 16 + r % 16);
+        const uint32_t j = c % 16;
+        if (bits == 4) {
+            const uint8_t byte = tiles[(nt * sb_total + sb) * 1024 + lane * 16 + s * 8 + (j < 8 ? 0 : 4) + (j & 3)];
+            const int u = (j & 4) ? byte >> 4 : byte & 0x0F;
+            return static_cast<float>(u - 8);
+        }
+        return static_cast<float>(
+            static_cast<int8_t>(tiles[(nt * sb_total + sb) * 2048 + s * 1024 + lane * 16 + j]));
+    }
     if (bits == 4) {
         const uint8_t byte = tiles[r * row_bytes + c / 2];
         const int u = (c & 1) ? byte >> 4 : byte & 0x0F;
@@ -125,12 +143,60 @@ __device__ __forceinline__ float decode(const uint8_t* tiles, uint32_t bits, uin
     return static_cast<float>(static_cast<int>(tiles[r * row_bytes + c]) - 128);
 }
 
+// Payload code (two's complement, row-major) of weight (r, c).
+__device__ __forceinline__ int payload_code(const uint8_t* payload, uint32_t bits, uint64_t k, uint64_t r,
+                                            uint64_t c) {
+    if (bits == 4) {
+        const uint8_t byte = payload[r * ((k + 1) / 2) + c / 2];
+        const int nib = (c & 1) ? byte >> 4 : byte & 0x0F;
+        return nib >= 8 ? nib - 16 : nib;
+    }
+    return static_cast<int8_t>(payload[r * k + c]);
+}
+
+// One thread per 32-bit word of the Mfma layout (see qgemv_mfma.hip).
+__global__ void repack_mfma(const uint8_t* __restrict__ payload, uint32_t* __restrict__ tiles, uint32_t bits,
+                            uint64_t n, uint64_t k, uint64_t words) {
+    const uint64_t sb_total = k / 128;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t w = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < words; w += stride) {
+        uint32_t out = 0;
+        if (bits == 4) {
+            const uint64_t tile = w / 256, within = w % 256;
+            const uint64_t nt = tile / sb_total, sb = tile % sb_total;
+            const uint32_t lane = static_cast<uint32_t>(within / 4), wi = static_cast<uint32_t>(within % 4);
+            const uint32_t s = wi / 2, half = wi % 2;
+            const uint64_t r = nt * 16 + lane % 16;
+            for (uint32_t jj = 0; jj < 8; ++jj) {
+                const uint32_t j = half * 8 + jj;
+                const uint64_t c = sb * 128 + s * 64 + (lane / 16) * 16 + j;
+                const uint32_t u = r < n ? static_cast<uint32_t>(payload_code(payload, 4, k, r, c) + 8) : 8u;
+                const uint32_t nib = jj < 4 ? 2 * jj : 2 * (jj - 4) + 1;
+                out |= (u & 0xF) << (4 * nib);
+            }
+        } else {
+            const uint64_t tile = w / 512, within = w % 512;
+            const uint64_t nt = tile / sb_total, sb = tile % sb_total;
+            const uint32_t s = static_cast<uint32_t>(within / 256);
+            const uint32_t lane = static_cast<uint32_t>((within % 256) / 4), wq = static_cast<uint32_t>(within % 4);
+            const uint64_t r = nt * 16 + lane % 16;
+            for (uint32_t b = 0; b < 4; ++b) {
+                const uint64_t c = sb * 128 + s * 64 + (lane / 16) * 16 + 4 * wq + b;
+                const uint32_t q = r < n ? static_cast<uint32_t>(payload_code(payload, 8, k, r, c)) & 0xFFu : 0u;
+                out |= q << (8 * b);
+            }
+        }
+        tiles[w] = out;
+    }
+}
+
 // One thread per output, any geometry.
 __global__ __launch_bounds__(256) void qmm_generic(const float* __restrict__ a, const uint8_t* __restrict__ tiles,
                                                    const float* __restrict__ scales, float* __restrict__ out,
                                                    uint64_t m, uint64_t n, uint64_t k, uint32_t group,
-                                                   uint32_t bits) {
+                                                   uint32_t bits, bool mfma) {
     const uint64_t total = m * n;
+    const uint64_t sb_total = k / 128;
     const uint64_t row_bytes = bits == 4 ? (k + 1) / 2 : k;
     const uint64_t groups = k / group;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
@@ -138,7 +204,8 @@ __global__ __launch_bounds__(256) void qmm_generic(const float* __restrict__ a, 
         const uint64_t r = i / n, c = i % n;
         float acc = 0.f;
         for (uint64_t kk = 0; kk < k; ++kk)
-            acc = fmaf(a[r * k + kk], decode(tiles, bits, row_bytes, c, kk) * scales[c * groups + kk / group], acc);
+            acc = fmaf(a[r * k + kk], decode(tiles, bits, row_bytes, c, kk, mfma, sb_total) *
+                                          scales[c * groups + kk / group], acc);
         out[i] = acc;
     }
 }
@@ -149,8 +216,9 @@ constexpr int BM = 64, BN = 64, BK = 16;
 __global__ __launch_bounds__(256) void qgemm_tiled(const float* __restrict__ a, const uint8_t* __restrict__ tiles,
                                                    const float* __restrict__ scales, float* __restrict__ out,
                                                    uint64_t m, uint64_t k, uint64_t n, uint32_t group,
-                                                   uint32_t bits) {
+                                                   uint32_t bits, bool mfma) {
     __shared__ float as[BK][BM + 4];
+    const uint64_t sb_total = k / 128;
     __shared__ float bs[BK][BN + 4];
     const uint64_t row0 = static_cast<uint64_t>(blockIdx.y) * BM;
     const uint64_t col0 = static_cast<uint64_t>(blockIdx.x) * BN;
@@ -168,7 +236,8 @@ __global__ __launch_bounds__(256) void qgemm_tiled(const float* __restrict__ a, 
         for (int e = tid; e < BN * BK; e += 256) {
             const int r = e / BK, c = e % BK;
             const uint64_t gn = col0 + r, gk = k0 + c;
-            bs[c][r] = (gn < n && gk < k) ? decode(tiles, bits, row_bytes, gn, gk) * scales[gn * groups + gk / group]
+            bs[c][r] = (gn < n && gk < k) ? decode(tiles, bits, row_bytes, gn, gk, mfma, sb_total) *
+                                                scales[gn * groups + gk / group]
                                           : 0.f;
         }
         __syncthreads();
@@ -201,30 +270,48 @@ __global__ __launch_bounds__(256) void qgemm_tiled(const float* __restrict__ a, 
 
 }  // namespace
 
-uint64_t quant_tile_bytes(uint32_t format, uint64_t n, uint64_t k) {
+QuantLayout quant_layout_for(uint32_t format, uint64_t n, uint64_t k, uint32_t group) {
+    (void)format;
+    (void)n;
+    if (group != 0 && k % 128 == 0 && group % 64 == 0 && k % group == 0 && group <= 4096) return QuantLayout::Mfma;
+    return QuantLayout::RowMajor;
+}
+
+uint64_t quant_tile_bytes(uint32_t format, uint64_t n, uint64_t k, QuantLayout layout) {
+    if (layout == QuantLayout::Mfma)
+        return (n + 15) / 16 * (k / 128) * (format == SL_QFORMAT_INT4 ? 1024 : 2048);
     const uint64_t bytes = format == SL_QFORMAT_INT4 ? n * ((k + 1) / 2) : n * k;
     return (bytes + 3) / 4 * 4;
 }
 
-hipError_t launch_quant_repack(const uint8_t* payload, uint8_t* tiles, uint32_t format, uint64_t n,
-                               uint64_t k, hipStream_t s) {
-    const uint64_t words = quant_tile_bytes(format, n, k) / 4;
+hipError_t launch_quant_repack(const uint8_t* payload, uint8_t* tiles, uint32_t format, uint64_t n, uint64_t k,
+                               QuantLayout layout, hipStream_t s) {
+    const uint64_t words = quant_tile_bytes(format, n, k, layout) / 4;
     if (words == 0) return hipSuccess;
+    if (layout == QuantLayout::Mfma) {
+        repack_mfma<<<grid_for(words, 256, 256 * 16), 256, 0, s>>>(payload, reinterpret_cast<uint32_t*>(tiles),
+                                                                    format == SL_QFORMAT_INT4 ? 4 : 8, n, k, words);
+        return hipGetLastError();
+    }
     xor_words<<<grid_for(words, 256, 256 * 8), 256, 0, s>>>(
         reinterpret_cast<const uint32_t*>(payload), reinterpret_cast<uint32_t*>(tiles), words,
         format == SL_QFORMAT_INT4 ? 0x88888888u : 0x80808080u);
     return hipGetLastError();
 }
 
-hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m, float* workspace,
-                          uint64_t workspace_floats, hipStream_t s) {
-    (void)workspace;
-    (void)workspace_floats;
+hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
+                          hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
     if (w.k == 0) return launch_fill_zero(out, m * w.n, s);
     const uint32_t bits = w.format == SL_QFORMAT_INT4 ? 4 : 8;
+    const bool mfma = w.layout == QuantLayout::Mfma;
+    if (mfma && m <= 16 && aligned16(a)) {
+        hipError_t e = launch_qgemv_mfma(a, w, out, m, ws, s);
+        if (e != hipErrorNotSupported) return e;
+        (void)hipGetLastError();
+    }
     const uint32_t ck = bits == 4 ? 32 : 16;
-    const bool fast = w.k % ck == 0 && w.group % ck == 0 && w.k % w.group == 0 && aligned16(a) &&
+    const bool fast = !mfma && w.k % ck == 0 && w.group % ck == 0 && w.k % w.group == 0 && aligned16(a) &&
                       aligned16(w.tiles) && w.n <= 0xffffffffu && w.k <= 0xffffffffu;
     if (fast && m <= 16) {
         dim3 grid(static_cast<unsigned>((w.n + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave)),
@@ -239,11 +326,11 @@ hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint
     }
     if (w.k % w.group == 0 && m > 16) {
         dim3 grid(static_cast<unsigned>((w.n + BN - 1) / BN), static_cast<unsigned>((m + BM - 1) / BM));
-        qgemm_tiled<<<grid, 256, 0, s>>>(a, w.tiles, w.scales, out, m, w.k, w.n, w.group, bits);
+        qgemm_tiled<<<grid, 256, 0, s>>>(a, w.tiles, w.scales, out, m, w.k, w.n, w.group, bits, mfma);
         return hipGetLastError();
     }
     qmm_generic<<<grid_for(m * w.n, 256, 256 * 16), 256, 0, s>>>(a, w.tiles, w.scales, out, m, w.n, w.k,
-                                                                 w.group, bits);
+                                                                 w.group, bits, mfma);
     return hipGetLastError();
 }
 

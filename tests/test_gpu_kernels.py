@@ -217,6 +217,10 @@ ATT_SHAPES = [
     (1, 2, 0, 32, 8, 70, 30, 64, 128),      # chunked prefill after a prefix, tiled path
     (2, 1, 0, 4, 4, 20, 5, 96, 32),         # prefill through the split path (head_dim 96)
     (1, 1, 0, 4, 2, 3, 0, 256, 8),          # head_dim 256
+    (1, 1, 0, 4, 1, 4, 10, 64, 16),         # 16 query rows per KV head (largest fused decode tile)
+    (1, 1, 0, 8, 2, 1, 4095, 128, 4096),    # decode of the last position of a 4096 context
+    (1, 1, 0, 8, 8, 1, 0, 128, 8),          # first token: one visible key
+    (3, 1, 0, 6, 2, 2, 33, 32, 40),         # batch 3, GQA 3, two-token chunk
 ]
 
 
@@ -315,7 +319,9 @@ def quant_weight(hip, w, fmt, group):
 @pytest.mark.parametrize("fmt", [QuantFormat.INT4, QuantFormat.INT8])
 @pytest.mark.parametrize("m,n,k,group", [(1, 256, 512, 128), (1, 300, 384, 128), (8, 256, 512, 128),
                                          (3, 64, 4096, 128), (17, 128, 256, 128), (64, 96, 512, 64),
-                                         (2, 33, 130, 2), (1, 1024, 4096, 128)])
+                                         (2, 33, 130, 2), (1, 1024, 4096, 128), (2, 512, 1024, 128),
+                                         (4, 48, 2048, 256), (12, 160, 1024, 128), (16, 64, 512, 64),
+                                         (1, 4096, 14336, 128), (5, 17, 896, 128)])
 def test_quantized_matmul_parity(hip, fmt, m, n, k, group):
     r = rng(m * n + k)
     w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)

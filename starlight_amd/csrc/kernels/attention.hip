@@ -8,16 +8,14 @@
 // acc' = acc*e^(m-m') + e^(s-m')*v, out = acc / l. Same mathematics, one pass.
 //
 // Kernels:
-//  * attn_decode — decode and short chunks (group * seq <= 16 query rows per
-//    KV head): one launch does kv_append and attention. A block owns one
-//    (batch, KV head, key chunk); all query rows sharing that KV head are
-//    served from one read of the chunk's K/V rows, staged through LDS in
-//    sub-tiles. Rows at or after past_len come from the new K/V (and the
-//    owning block writes them to the cache). The grid depends only on
-//    max_seq, the chunk length on past_len + seq, so every block has work.
-//    Partial (m, l, acc) go to the workspace; the last block of each
-//    (batch, KV head) — counted with a device-scope atomic — merges them in
-//    chunk order and writes the output.
+//  * attn_decode + attn_decode_merge — decode and short chunks (group * seq
+//    <= 16 query rows per KV head). A block owns one (batch, KV head, 32-key
+//    chunk); all query rows sharing that KV head are served from one read of
+//    the chunk's K/V rows through LDS. Rows at or after past_len come from the
+//    new K/V and the owning block appends them to the cache (kv_append fused).
+//    The grid depends only on max_seq; chunks past the current length exit.
+//    Partial (m, l, acc) go to the workspace and the merge kernel combines the
+//    active chunks in order.
 //  * attn_split / attn_merge — other decode shapes: one wave per
 //    (b, h, t, key chunk), score by wave reduction, then a merge kernel.
 //  * attn_tiled — prefill: a block owns 64 queries of one head, two threads
@@ -34,7 +32,6 @@ struct Geo {
     const float* k_new;
     const float* v_new;
     float* wcache;
-    uint32_t* counters;
     const float* cache;
     float* out;
     float* ws;
@@ -140,168 +137,186 @@ __global__ __launch_bounds__(256) void attn_merge(Geo g) {
 }
 
 
-constexpr int kDecodeRows = 16;   // query rows (group * seq) per KV head
-constexpr int kDecodeChunks = 32; // key chunks per (batch, KV head)
+constexpr int kDecodeRows = 16;  // query rows (group * seq) per KV head
 
-// Dynamic LDS: q [R][D], k/v sub-tile [KT][D + 1], p [R][KT].
-template <int KT>
+// One block per (key chunk of KT keys, KV head, batch); chunks at or beyond
+// past_len + seq exit at once, so the grid (fixed by max_seq) can be replayed
+// for any length. LDS: q [R][D], k/v [KT][D + 1], p [R][KT]. Every global
+// load of a stage is issued before any is used.
+template <int KT, bool VEC>
 __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     extern __shared__ float lds[];
-    __shared__ float m_run[kDecodeRows], l_run[kDecodeRows], corr[kDecodeRows];
-    __shared__ int is_last;
+    __shared__ float m_row[kDecodeRows], l_row[kDecodeRows];
     const uint32_t D = g.head_dim, S = g.seq, G = g.group;
     const uint32_t R = G * S;  // query rows: r = gi * S + t
     const uint32_t c = blockIdx.x, kvh = blockIdx.y;
     const uint64_t b = blockIdx.z;
     const int tid = threadIdx.x;
-    float* qs = lds;                        // [R][D]
-    float* ks = qs + R * D;                 // [KT][D + 1]
-    float* vs = ks + KT * (D + 1);          // [KT][D + 1]
-    float* ps = vs + KT * (D + 1);          // [R][KT]
-
-    const uint32_t keys = g.past_len + S;   // keys visible to the last query
-    const uint32_t chunk = (keys + g.chunks - 1) / g.chunks;
-    const uint32_t j0 = min(c * chunk, keys), j1 = min(j0 + chunk, keys);
+    const uint32_t keys = g.past_len + S;
+    const uint32_t j0 = c * KT;
+    if (j0 >= keys) return;
+    const uint32_t nk = min(static_cast<uint32_t>(KT), keys - j0);
+    float* qs = lds;                 // [R][D]
+    float* ks = qs + R * D;          // [KT][D + 1]
+    float* vs = ks + KT * (D + 1);   // [KT][D + 1]
+    float* ps = vs + KT * (D + 1);   // [R][KT]
     const uint64_t time_stride = static_cast<uint64_t>(g.kv_heads) * D;
     float* kbase = g.wcache + b * g.batch_stride + g.layer_offset + kvh * D;
     float* vbase = kbase + g.parity_stride;
 
-    for (uint32_t i = tid; i < R * D; i += 256) {
-        const uint32_t r = i / D, d = i % D, gi = r / S, t = r % S;
-        qs[i] = g.q[((b * g.heads + kvh * G + gi) * S + t) * D + d];
-    }
-    if (tid < kDecodeRows) {
-        m_run[tid] = -INFINITY;
-        l_run[tid] = 0.f;
-    }
-    // each thread owns output elements e = tid + 256 i of the [R][D] tile
-    constexpr int kMaxOut = kDecodeRows * 256 / 256;
-    float acc[kMaxOut];
+    if constexpr (VEC) {
+        const uint32_t d4 = D / 4;
+        // q rows of this KV head's query group
+        constexpr int kQ = kDecodeRows * 256 / 4 / 256;  // float4 per thread, worst case
+        float4 qv[kQ];
 #pragma unroll
-    for (int i = 0; i < kMaxOut; ++i) acc[i] = 0.f;
-
-    for (uint32_t jt = j0; jt < j1; jt += KT) {
-        const uint32_t nk = min(static_cast<uint32_t>(KT), j1 - jt);
-        __syncthreads();
-        // K/V sub-tile: cached rows from the cache, new rows from k_new/v_new
-        // (and appended to the cache by this block, kv_append attention.rs:33-83)
+        for (int u = 0; u < kQ; ++u) {
+            const uint32_t i = tid + 256 * u;
+            qv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < R * d4) {
+                const uint32_t r = i / d4, dd = i % d4, gi = r / S, t = r % S;
+                qv[u] = reinterpret_cast<const float4*>(g.q + ((b * g.heads + kvh * G + gi) * S + t) * D)[dd];
+            }
+        }
+        // K/V rows: cached rows from the cache, new rows from k_new/v_new
+        constexpr int kKV = KT * 256 / 4 / 256;  // float4 per thread, worst case (D <= 256)
+        float4 kv[kKV], vv[kKV];
+#pragma unroll
+        for (int u = 0; u < kKV; ++u) {
+            const uint32_t i = tid + 256 * u;
+            kv[u] = vv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < KT * d4) {
+                const uint32_t jj = i / d4, dd = i % d4, j = j0 + jj;
+                if (jj < nk) {
+                    if (j < g.past_len) {
+                        kv[u] = reinterpret_cast<const float4*>(kbase + j * time_stride)[dd];
+                        vv[u] = reinterpret_cast<const float4*>(vbase + j * time_stride)[dd];
+                    } else {
+                        const uint64_t src = ((b * g.kv_heads + kvh) * S + (j - g.past_len)) * D;
+                        kv[u] = reinterpret_cast<const float4*>(g.k_new + src)[dd];
+                        vv[u] = reinterpret_cast<const float4*>(g.v_new + src)[dd];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kQ; ++u) {
+            const uint32_t i = tid + 256 * u;
+            if (i < R * d4) reinterpret_cast<float4*>(qs)[i] = qv[u];
+        }
+#pragma unroll
+        for (int u = 0; u < kKV; ++u) {
+            const uint32_t i = tid + 256 * u;
+            if (i < KT * d4) {
+                const uint32_t jj = i / d4, d = 4 * (i % d4), j = j0 + jj;
+                float* kr = ks + jj * (D + 1) + d;
+                float* vr = vs + jj * (D + 1) + d;
+                kr[0] = kv[u].x; kr[1] = kv[u].y; kr[2] = kv[u].z; kr[3] = kv[u].w;
+                vr[0] = vv[u].x; vr[1] = vv[u].y; vr[2] = vv[u].z; vr[3] = vv[u].w;
+                if (jj < nk && j >= g.past_len) {  // kv_append of the new rows
+                    reinterpret_cast<float4*>(kbase + j * time_stride)[i % d4] = kv[u];
+                    reinterpret_cast<float4*>(vbase + j * time_stride)[i % d4] = vv[u];
+                }
+            }
+        }
+    } else {
+        for (uint32_t i = tid; i < R * D; i += 256) {
+            const uint32_t r = i / D, d = i % D, gi = r / S, t = r % S;
+            qs[i] = g.q[((b * g.heads + kvh * G + gi) * S + t) * D + d];
+        }
         for (uint32_t i = tid; i < KT * D; i += 256) {
-            const uint32_t jj = i / D, d = i % D, j = jt + jj;
-            float kv = 0.f, vv = 0.f;
+            const uint32_t jj = i / D, d = i % D, j = j0 + jj;
+            float kx = 0.f, vx = 0.f;
             if (jj < nk) {
                 if (j < g.past_len) {
-                    kv = kbase[j * time_stride + d];
-                    vv = vbase[j * time_stride + d];
+                    kx = kbase[j * time_stride + d];
+                    vx = vbase[j * time_stride + d];
                 } else {
                     const uint64_t src = ((b * g.kv_heads + kvh) * S + (j - g.past_len)) * D + d;
-                    kv = g.k_new[src];
-                    vv = g.v_new[src];
-                    kbase[j * time_stride + d] = kv;
-                    vbase[j * time_stride + d] = vv;
+                    kx = g.k_new[src];
+                    vx = g.v_new[src];
+                    kbase[j * time_stride + d] = kx;
+                    vbase[j * time_stride + d] = vx;
                 }
             }
-            ks[jj * (D + 1) + d] = kv;
-            vs[jj * (D + 1) + d] = vv;
-        }
-        __syncthreads();
-        // scores: one (row, key) pair per thread
-        for (uint32_t i = tid; i < R * KT; i += 256) {
-            const uint32_t r = i / KT, jj = i % KT;
-            const uint32_t t = r % S;
-            float dot = 0.f;
-            const float* qr = qs + r * D;
-            const float* kr = ks + jj * (D + 1);
-            for (uint32_t d = 0; d < D; ++d) dot = fmaf(qr[d], kr[d], dot);
-            const bool vis = jj < nk && jt + jj <= g.past_len + t;
-            ps[r * KT + jj] = vis ? dot * g.scale : -INFINITY;
-        }
-        __syncthreads();
-        // online-softmax update per row (one thread per row)
-        if (tid < static_cast<int>(R)) {
-            const float* pr = ps + tid * KT;
-            float mx = -INFINITY;
-            for (int jj = 0; jj < KT; ++jj) mx = fmaxf(mx, pr[jj]);
-            const float m_old = m_run[tid];
-            const float m_new = fmaxf(m_old, mx);
-            float cr = 1.f, sum = 0.f;
-            if (m_new != -INFINITY) {
-                cr = expf(m_old - m_new);
-                for (int jj = 0; jj < KT; ++jj) {
-                    const float p = expf(pr[jj] - m_new);
-                    ps[tid * KT + jj] = p;
-                    sum += p;
-                }
-            } else {
-                for (int jj = 0; jj < KT; ++jj) ps[tid * KT + jj] = 0.f;
-            }
-            corr[tid] = cr;
-            m_run[tid] = m_new;
-            l_run[tid] = l_run[tid] * cr + sum;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < kMaxOut; ++i) {
-            const uint32_t e = tid + 256 * i;
-            if (e >= R * D) break;
-            const uint32_t r = e / D, d = e % D;
-            float a = acc[i] * corr[r];
-            const float* pr = ps + r * KT;
-            for (int jj = 0; jj < KT; ++jj) a = fmaf(pr[jj], vs[jj * (D + 1) + d], a);
-            acc[i] = a;
+            ks[jj * (D + 1) + d] = kx;
+            vs[jj * (D + 1) + d] = vx;
         }
     }
-
-    // partial of this chunk: [(b, kvh)][chunk][r][2 + D]
-    const uint64_t bk = b * g.kv_heads + kvh;
-    const uint64_t row_stride = 2 + D;
-    float* part = g.ws + (bk * g.chunks + c) * R * row_stride;
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kMaxOut; ++i) {
-        const uint32_t e = tid + 256 * i;
-        if (e >= R * D) break;
-        part[(e / D) * row_stride + 2 + e % D] = acc[i];
+    // scores: one (row, key) pair per thread
+    for (uint32_t i = tid; i < R * KT; i += 256) {
+        const uint32_t r = i / KT, jj = i % KT;
+        const float* qr = qs + r * D;
+        const float* kr = ks + jj * (D + 1);
+        float dot = 0.f;
+        for (uint32_t d = 0; d < D; ++d) dot = fmaf(qr[d], kr[d], dot);
+        const bool vis = jj < nk && j0 + jj <= g.past_len + r % S;
+        ps[i] = vis ? dot * g.scale : -INFINITY;
+    }
+    __syncthreads();
+    // chunk softmax per row: m = max, p = exp(s - m), l = sum p
+    if (tid < static_cast<int>(R)) {
+        float* pr = ps + tid * KT;
+        float mx = -INFINITY;
+        for (int jj = 0; jj < KT; ++jj) mx = fmaxf(mx, pr[jj]);
+        float sum = 0.f;
+        for (int jj = 0; jj < KT; ++jj) {
+            const float e = mx == -INFINITY ? 0.f : expf(pr[jj] - mx);
+            pr[jj] = e;
+            sum += e;
+        }
+        m_row[tid] = mx;
+        l_row[tid] = sum;
+    }
+    __syncthreads();
+    // partial of this chunk: [(b, kvh)][chunk][r][2 + D]
+    const uint64_t row_stride = 2 + D;
+    float* part = g.ws + ((b * g.kv_heads + kvh) * g.chunks + c) * R * row_stride;
+    for (uint32_t e = tid; e < R * D; e += 256) {
+        const uint32_t r = e / D, d = e % D;
+        const float* pr = ps + r * KT;
+        float a = 0.f;
+        for (int jj = 0; jj < KT; ++jj) a = fmaf(pr[jj], vs[jj * (D + 1) + d], a);
+        part[r * row_stride + 2 + d] = a;
     }
     if (tid < static_cast<int>(R)) {
-        part[tid * row_stride] = m_run[tid];
-        part[tid * row_stride + 1] = l_run[tid];
+        part[tid * row_stride] = m_row[tid];
+        part[tid * row_stride + 1] = l_row[tid];
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&g.counters[bk], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        is_last = prev == g.chunks - 1;
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    // merge the chunk partials in chunk order
-    const float* base = g.ws + bk * g.chunks * R * row_stride;
+}
+
+// Merges the chunk partials of one (batch, KV head): grid (kv_heads, batch).
+__global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t kt) {
+    __shared__ float m_row[kDecodeRows], inv_row[kDecodeRows];
+    const uint32_t D = g.head_dim, S = g.seq, G = g.group, R = G * S;
+    const uint32_t kvh = blockIdx.x;
+    const uint64_t b = blockIdx.y;
+    const uint32_t active = (g.past_len + S + kt - 1) / kt;
+    const uint64_t row_stride = 2 + D;
+    const float* base = g.ws + (b * g.kv_heads + kvh) * g.chunks * R * row_stride;
+    const int tid = threadIdx.x;
     if (tid < static_cast<int>(R)) {
         float mx = -INFINITY;
-        for (uint32_t cc = 0; cc < g.chunks; ++cc)
-            mx = fmaxf(mx, __builtin_nontemporal_load(&base[(cc * R + tid) * row_stride]));
+        for (uint32_t c = 0; c < active; ++c) mx = fmaxf(mx, base[(c * R + tid) * row_stride]);
         float l = 0.f;
-        for (uint32_t cc = 0; cc < g.chunks; ++cc) {
-            const float lc = __builtin_nontemporal_load(&base[(cc * R + tid) * row_stride + 1]);
-            if (lc > 0.f) l += lc * expf(__builtin_nontemporal_load(&base[(cc * R + tid) * row_stride]) - mx);
+        for (uint32_t c = 0; c < active; ++c) {
+            const float* pc = base + (c * R + tid) * row_stride;
+            if (pc[1] > 0.f) l += pc[1] * expf(pc[0] - mx);
         }
-        m_run[tid] = mx;
-        l_run[tid] = 1.0f / l;
+        m_row[tid] = mx;
+        inv_row[tid] = 1.0f / l;
     }
     __syncthreads();
     for (uint32_t e = tid; e < R * D; e += 256) {
         const uint32_t r = e / D, d = e % D, gi = r / S, t = r % S;
         float a = 0.f;
-        for (uint32_t cc = 0; cc < g.chunks; ++cc) {
-            const float* pc = base + (cc * R + r) * row_stride;
-            const float lc = __builtin_nontemporal_load(&pc[1]);
-            if (lc > 0.f) a = fmaf(__builtin_nontemporal_load(&pc[2 + d]), expf(__builtin_nontemporal_load(&pc[0]) - m_run[r]), a);
+        for (uint32_t c = 0; c < active; ++c) {
+            const float* pc = base + (c * R + r) * row_stride;
+            if (pc[1] > 0.f) a = fmaf(pc[2 + d], expf(pc[0] - m_row[r]), a);
         }
-        g.out[((b * g.heads + kvh * G + gi) * S + t) * D + d] = a * l_run[r];
+        g.out[((b * g.heads + kvh * G + gi) * S + t) * D + d] = a * inv_row[r];
     }
-    __syncthreads();
-    if (tid == 0) __hip_atomic_store(&g.counters[bk], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 constexpr int kTileQ = 64;  // queries per block
@@ -412,7 +427,6 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
     g.cache = a.cache;
     g.out = a.out;
     g.ws = ws.data;
-    g.counters = ws.counters;
     g.heads = static_cast<uint32_t>(a.heads);
     g.kv_heads = static_cast<uint32_t>(a.kv_heads);
     g.seq = static_cast<uint32_t>(a.seq);
@@ -424,21 +438,26 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
     g.batch_stride = a.layers * 2 * g.parity_stride;
     g.scale = a.scale;
 
-    // Fused decode path: kv_append + attention + merge in one launch.
+    // Decode path: kv_append fused into the chunk kernel, then the merge.
     const uint64_t rows = static_cast<uint64_t>(g.group) * a.seq;
-    const uint64_t pairs = a.batch * a.kv_heads;
-    if (rows <= kDecodeRows && a.head_dim <= 256 && pairs <= ws.n_counters &&
-        pairs * kDecodeChunks * rows * (a.head_dim + 2) <= ws.floats) {
-        g.chunks = kDecodeChunks;
-        g.chunk = 0;
-        dim3 grid(kDecodeChunks, g.kv_heads, static_cast<unsigned>(a.batch));
-        if (a.head_dim <= 128) {
-            const size_t lds = (rows * a.head_dim + 2 * 32 * (a.head_dim + 1) + rows * 32) * sizeof(float);
-            attn_decode<32><<<grid, 256, lds, s>>>(g);
+    const uint32_t kt = a.head_dim <= 128 ? 32 : 16;
+    const uint64_t n_chunks = (a.max_seq + kt - 1) / kt;
+    if (rows <= kDecodeRows && a.head_dim <= 256 && n_chunks <= 0xffffffffull &&
+        a.batch * a.kv_heads * n_chunks * rows * (a.head_dim + 2) <= ws.floats) {
+        g.chunks = static_cast<uint32_t>(n_chunks);
+        g.chunk = kt;
+        const bool vec = a.head_dim % 4 == 0 && aligned16(a.q) && aligned16(a.k_new) && aligned16(a.v_new) &&
+                         aligned16(a.cache);
+        dim3 grid(static_cast<unsigned>(n_chunks), g.kv_heads, static_cast<unsigned>(a.batch));
+        const size_t lds = (rows * a.head_dim + 2 * kt * (a.head_dim + 1) + rows * kt) * sizeof(float);
+        if (kt == 32) {
+            if (vec) attn_decode<32, true><<<grid, 256, lds, s>>>(g);
+            else attn_decode<32, false><<<grid, 256, lds, s>>>(g);
         } else {
-            const size_t lds = (rows * a.head_dim + 2 * 16 * (a.head_dim + 1) + rows * 16) * sizeof(float);
-            attn_decode<16><<<grid, 256, lds, s>>>(g);
+            if (vec) attn_decode<16, true><<<grid, 256, lds, s>>>(g);
+            else attn_decode<16, false><<<grid, 256, lds, s>>>(g);
         }
+        attn_decode_merge<<<dim3(g.kv_heads, static_cast<unsigned>(a.batch)), 256, 0, s>>>(g, kt);
         return hipGetLastError();
     }
 

@@ -26,11 +26,14 @@
 // for row l % 16 — identical for A and B, which is all the product needs.
 //
 // Work split: a block of 4 waves owns 4 adjacent 16-row tiles (one per wave)
-// and one split of the K superblocks; when K is split across blocks, each
-// block writes its partial tile to the workspace and the last block of a
-// tile column (counted with one device-scope atomic per column) adds the
-// partials in split order — deterministic, no extra launch, and the counter
-// is returned to zero.
+// and one split of the K superblocks. Every wave issues the loads for all of
+// its superblocks (at most kPrefetch) before converting the activations, so
+// the whole weight slice is in flight at once — a decode GEMV moves only a
+// few MB, about one memory latency's worth, so latency, not bandwidth,
+// decides it. K is split until about 1024 waves run; split partials go to the
+// workspace and qgemv_reduce adds them in split order (deterministic, and no
+// cross-block fence: on this part a device-scope release writes back the
+// XCD's L2, which costs far more than one small extra launch).
 #include "common.h"
 #include "kernels.h"
 #include "starlight_hip.h"
@@ -42,6 +45,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kWavesPerBlock = 4;
 constexpr int kLdsLimbBytes = 48 * 1024;  // 3 limbs x m x k-slice
+constexpr int kPrefetch = 8;              // INT4 superblocks in flight per wave (INT8: half)
 
 struct QgemvArgs {
     const float* a;
@@ -49,7 +53,6 @@ struct QgemvArgs {
     const float* scales;
     float* out;
     float* partial;      // [splits, m, n] when splits > 1
-    uint32_t* counters;  // one per n-block
     uint32_t m, n, k, group;
     uint32_t sb_total;   // k / 128
     uint32_t sb_per_split;
@@ -58,11 +61,11 @@ struct QgemvArgs {
 
 template <int BITS>
 __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
+    constexpr int PF = BITS == 4 ? kPrefetch : kPrefetch / 2;  // superblocks in flight per wave
     extern __shared__ __align__(16) int8_t limbs[];  // [3][m][kslice]
     __shared__ uint32_t max_bits[16];
     __shared__ int exps[16];
     __shared__ int xsum[16 * 64];    // [m][group in split]: sum of X, for the INT4 offset correction
-    __shared__ int is_last;
 
     const int tid = threadIdx.x;
     const int lane = tid % kWave, wave = tid / kWave;
@@ -74,13 +77,45 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
     const uint32_t g0 = k0 / p.group, gcount = klen / p.group;
     const uint32_t M = p.m;
 
+    // ---- the wave's weight stream: a rolling window of kPrefetch
+    // superblocks in registers, started before the prologue so the first
+    // HBM round trip overlaps the activation conversion ----
+    const uint32_t nt = blockIdx.x * kWavesPerBlock + wave;
+    const bool tile_live = nt * 16 < p.n;
+    const uint8_t* wtile = p.tiles + static_cast<uint64_t>(nt) * p.sb_total * (BITS == 4 ? 1024 : 2048) + lane * 16;
+    uint4 w0[PF], w1[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+        const uint32_t sb = sb0 + i;
+        if (tile_live && sb < sb1) {
+            if constexpr (BITS == 4) {
+                w0[i] = *reinterpret_cast<const uint4*>(wtile + static_cast<uint64_t>(sb) * 1024);
+            } else {
+                w0[i] = *reinterpret_cast<const uint4*>(wtile + static_cast<uint64_t>(sb) * 2048);
+                w1[i] = *reinterpret_cast<const uint4*>(wtile + static_cast<uint64_t>(sb) * 2048 + 1024);
+            }
+        }
+    }
+
     // ---- prologue: the activation slice as exact int8 limbs in LDS ----
+    // (float4 loads, four in flight per thread per pass)
     if (tid < 16) max_bits[tid] = 0u;
     for (uint32_t i = tid; i < M * gcount; i += 256) xsum[i] = 0;
     __syncthreads();
-    for (uint32_t idx = tid; idx < M * klen; idx += 256) {
-        const uint32_t m = idx / klen, kk = idx % klen;
-        atomicMax(&max_bits[m], __float_as_uint(fabsf(p.a[static_cast<uint64_t>(m) * p.k + k0 + kk])));
+    const uint32_t q4 = klen / 4;  // float4 per row slice
+    for (uint32_t m = 0; m < M; ++m) {
+        const float4* xr = reinterpret_cast<const float4*>(p.a + static_cast<uint64_t>(m) * p.k + k0);
+        float mx = 0.f;
+        for (uint32_t f = tid; f < q4; f += 1024) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = f + 256 * u < q4 ? xr[f + 256 * u] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+        }
+        mx = wave_max(mx);
+        if (lane == 0) atomicMax(&max_bits[m], __float_as_uint(mx));
     }
     __syncthreads();
     if (tid < 16) {
@@ -89,30 +124,52 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
         exps[tid] = e;  // max|x| < 2^e
     }
     __syncthreads();
-    for (uint32_t idx = tid; idx < M * klen; idx += 256) {
-        const uint32_t m = idx / klen, kk = idx % klen;
-        const float x = p.a[static_cast<uint64_t>(m) * p.k + k0 + kk];
-        const int X = static_cast<int>(rintf(ldexpf(x, 22 - exps[m])));
-        const int l0 = ((X + 128) & 255) - 128;
-        const int x1 = (X - l0) >> 8;
-        const int l1 = ((x1 + 128) & 255) - 128;
-        const int l2 = (x1 - l1) >> 8;
-        limbs[(0 * M + m) * kslice + kk] = static_cast<int8_t>(l0);
-        limbs[(1 * M + m) * kslice + kk] = static_cast<int8_t>(l1);
-        limbs[(2 * M + m) * kslice + kk] = static_cast<int8_t>(l2);
-        if (BITS == 4) {
-            // A wave's 64 consecutive kk share one group (group is a multiple
-            // of 64); integer sums keep the correction exact and order-free.
-            int sx = X;
+    // lanes whose 4-element runs share a group (group is a multiple of 64)
+    const int seg = p.group / 4 < kWave ? static_cast<int>(p.group / 4) : kWave;
+    for (uint32_t m = 0; m < M; ++m) {
+        const float4* xr = reinterpret_cast<const float4*>(p.a + static_cast<uint64_t>(m) * p.k + k0);
+        const int shift = 22 - exps[m];
+        for (uint32_t f0 = 0; f0 < q4; f0 += 1024) {
+            float4 v[4];
 #pragma unroll
-            for (int off = kWave / 2; off > 0; off >>= 1) sx += __shfl_xor(sx, off, kWave);
-            if (lane == 0) atomicAdd(&xsum[m * gcount + kk / p.group], sx);
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t f = f0 + tid + 256 * u;
+                v[u] = f < q4 ? xr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t f = f0 + tid + 256 * u;
+                if (f0 + (tid & ~(kWave - 1)) + 256 * u >= q4) continue;  // whole wave out of range
+                const float xe[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                int sx = 0;
+                uint32_t packed[3] = {0u, 0u, 0u};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int X = f < q4 ? static_cast<int>(rintf(ldexpf(xe[e], shift))) : 0;
+                    const int l0 = ((X + 128) & 255) - 128;
+                    const int x1 = (X - l0) >> 8;
+                    const int l1 = ((x1 + 128) & 255) - 128;
+                    const int l2 = (x1 - l1) >> 8;
+                    packed[0] |= (static_cast<uint32_t>(l0) & 0xFFu) << (8 * e);
+                    packed[1] |= (static_cast<uint32_t>(l1) & 0xFFu) << (8 * e);
+                    packed[2] |= (static_cast<uint32_t>(l2) & 0xFFu) << (8 * e);
+                    sx += X;
+                }
+                if (f < q4) {
+#pragma unroll
+                    for (int limb = 0; limb < 3; ++limb)
+                        *reinterpret_cast<uint32_t*>(limbs + (limb * M + m) * kslice + 4 * f) = packed[limb];
+                }
+                if (BITS == 4) {
+                    for (int off = seg / 2; off > 0; off >>= 1) sx += __shfl_xor(sx, off, kWave);
+                    if (f < q4 && lane % seg == 0) atomicAdd(&xsum[m * gcount + (4 * f) / p.group], sx);
+                }
+            }
         }
     }
     __syncthreads();
 
     // ---- main loop: wave `wave` owns tile nt ----
-    const uint32_t nt = blockIdx.x * kWavesPerBlock + wave;
     const uint32_t row = nt * 16 + lane % 16;
     const uint32_t kb4 = lane / 16;
     const uint32_t am = lane % 16;  // A-operand row (activation row)
@@ -120,62 +177,71 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
     const uint32_t groups_total = p.k / p.group;
     const uint32_t steps_per_group = p.group / 64;
     float total[4] = {0.f, 0.f, 0.f, 0.f};
-    const bool tile_live = nt * 16 < p.n;
     if (tile_live) {
         v4i acc0 = {0, 0, 0, 0}, acc1 = acc0, acc2 = acc0;
         const v4i zero = {0, 0, 0, 0};
         uint32_t step = 0;  // 64-k steps since the slice start
-        for (uint32_t sb = sb0; sb < sb1; ++sb) {
-            uint4 wb[2];
-            if (BITS == 4) {
-                wb[0] = *reinterpret_cast<const uint4*>(p.tiles + (static_cast<uint64_t>(nt) * p.sb_total + sb) * 1024 +
-                                                        lane * 16);
-            } else {
-                const uint8_t* base = p.tiles + (static_cast<uint64_t>(nt) * p.sb_total + sb) * 2048 + lane * 16;
-                wb[0] = *reinterpret_cast<const uint4*>(base);
-                wb[1] = *reinterpret_cast<const uint4*>(base + 1024);
-            }
+        for (uint32_t base = sb0; base < sb1; base += PF) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                v4i bv;
-                if (BITS == 4) {
-                    const uint32_t w0 = s == 0 ? wb[0].x : wb[0].z;
-                    const uint32_t w1 = s == 0 ? wb[0].y : wb[0].w;
-                    bv[0] = static_cast<int>(w0 & 0x0F0F0F0Fu);
-                    bv[1] = static_cast<int>((w0 >> 4) & 0x0F0F0F0Fu);
-                    bv[2] = static_cast<int>(w1 & 0x0F0F0F0Fu);
-                    bv[3] = static_cast<int>((w1 >> 4) & 0x0F0F0F0Fu);
-                } else {
-                    bv[0] = static_cast<int>(wb[s].x);
-                    bv[1] = static_cast<int>(wb[s].y);
-                    bv[2] = static_cast<int>(wb[s].z);
-                    bv[3] = static_cast<int>(wb[s].w);
-                }
-                const uint32_t kl = (sb - sb0) * 128 + s * 64 + kb4 * 16;
-                v4i a0 = zero, a1 = zero, a2 = zero;
-                if (a_live) {
-                    a0 = *reinterpret_cast<const v4i*>(limbs + (0 * M + am) * kslice + kl);
-                    a1 = *reinterpret_cast<const v4i*>(limbs + (1 * M + am) * kslice + kl);
-                    a2 = *reinterpret_cast<const v4i*>(limbs + (2 * M + am) * kslice + kl);
-                }
-                acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bv, acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bv, acc1, 0, 0, 0);
-                acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bv, acc2, 0, 0, 0);
-                ++step;
-                if (step % steps_per_group == 0) {
-                    const uint32_t gl = step / steps_per_group - 1;  // group within the slice
-                    const float sc = row < p.n ? p.scales[static_cast<uint64_t>(row) * groups_total + g0 + gl] : 0.f;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const uint32_t m = kb4 * 4 + r;
-                        float v = fmaf(static_cast<float>(acc2[r]), 65536.0f,
-                                       fmaf(static_cast<float>(acc1[r]), 256.0f, static_cast<float>(acc0[r])));
-                        if (BITS == 4 && m < M) v -= 8.0f * static_cast<float>(xsum[m * gcount + gl]);
-                        total[r] = fmaf(v, sc, total[r]);
+            for (int i = 0; i < PF; ++i) {
+                const uint32_t sb = base + i;
+                if (sb >= sb1) break;
+                const uint4 c0 = w0[i];
+                uint4 c1 = c0;
+                if constexpr (BITS == 8) c1 = w1[i];
+                const uint32_t nsb = sb + PF;
+                if (nsb < sb1) {
+                    if constexpr (BITS == 4) {
+                        w0[i] = *reinterpret_cast<const uint4*>(wtile + static_cast<uint64_t>(nsb) * 1024);
+                    } else {
+                        w0[i] = *reinterpret_cast<const uint4*>(wtile + static_cast<uint64_t>(nsb) * 2048);
+                        w1[i] = *reinterpret_cast<const uint4*>(wtile + static_cast<uint64_t>(nsb) * 2048 + 1024);
                     }
-                    acc0 = zero;
-                    acc1 = zero;
-                    acc2 = zero;
+                }
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    v4i bv;
+                    if (BITS == 4) {
+                        const uint32_t wa = s == 0 ? c0.x : c0.z;
+                        const uint32_t wb = s == 0 ? c0.y : c0.w;
+                        bv[0] = static_cast<int>(wa & 0x0F0F0F0Fu);
+                        bv[1] = static_cast<int>((wa >> 4) & 0x0F0F0F0Fu);
+                        bv[2] = static_cast<int>(wb & 0x0F0F0F0Fu);
+                        bv[3] = static_cast<int>((wb >> 4) & 0x0F0F0F0Fu);
+                    } else {
+                        const uint4 cw = s == 0 ? c0 : c1;
+                        bv[0] = static_cast<int>(cw.x);
+                        bv[1] = static_cast<int>(cw.y);
+                        bv[2] = static_cast<int>(cw.z);
+                        bv[3] = static_cast<int>(cw.w);
+                    }
+                    const uint32_t kl = (sb - sb0) * 128 + s * 64 + kb4 * 16;
+                    v4i a0 = zero, a1 = zero, a2 = zero;
+                    if (a_live) {
+                        a0 = *reinterpret_cast<const v4i*>(limbs + (0 * M + am) * kslice + kl);
+                        a1 = *reinterpret_cast<const v4i*>(limbs + (1 * M + am) * kslice + kl);
+                        a2 = *reinterpret_cast<const v4i*>(limbs + (2 * M + am) * kslice + kl);
+                    }
+                    acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bv, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bv, acc1, 0, 0, 0);
+                    acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bv, acc2, 0, 0, 0);
+                    ++step;
+                    if (step % steps_per_group == 0) {
+                        const uint32_t gl = step / steps_per_group - 1;  // group within the slice
+                        const float sc =
+                            row < p.n ? p.scales[static_cast<uint64_t>(row) * groups_total + g0 + gl] : 0.f;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const uint32_t m = kb4 * 4 + r;
+                            float v = fmaf(static_cast<float>(acc2[r]), 65536.0f,
+                                           fmaf(static_cast<float>(acc1[r]), 256.0f, static_cast<float>(acc0[r])));
+                            if (BITS == 4 && m < M) v -= 8.0f * static_cast<float>(xsum[m * gcount + gl]);
+                            total[r] = fmaf(v, sc, total[r]);
+                        }
+                        acc0 = zero;
+                        acc1 = zero;
+                        acc2 = zero;
+                    }
                 }
             }
         }
@@ -190,31 +256,17 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
         if (p.splits == 1) p.out[static_cast<uint64_t>(m) * p.n + row] = v;
         else p.partial[(static_cast<uint64_t>(split) * M + m) * p.n + row] = v;
     }
-    if (p.splits == 1) return;
+}
 
-    // ---- the last block of this column adds the partials in split order ----
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&p.counters[blockIdx.x], 1u, __ATOMIC_ACQ_REL,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        is_last = prev == p.splits - 1;
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    const uint32_t col0 = blockIdx.x * kWavesPerBlock * 16;
-    const uint32_t cols = min(kWavesPerBlock * 16u, p.n - col0);
-    for (uint32_t idx = tid; idx < M * cols; idx += 256) {
-        const uint32_t m = idx / cols, c = col0 + idx % cols;
+// out[i] = sum over splits (in order) of partial[split][i], i < m * n.
+__global__ __launch_bounds__(256) void qgemv_reduce(const float* __restrict__ partial, float* __restrict__ out,
+                                                    uint64_t count, uint32_t splits) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
         float sum = 0.f;
-        for (uint32_t sp = 0; sp < p.splits; ++sp)
-            sum += __builtin_nontemporal_load(&p.partial[(static_cast<uint64_t>(sp) * M + m) * p.n + c]);
-        p.out[static_cast<uint64_t>(m) * p.n + c] = sum;
+        for (uint32_t sp = 0; sp < splits; ++sp) sum += partial[sp * count + i];
+        out[i] = sum;
     }
-    __syncthreads();
-    if (tid == 0)
-        __hip_atomic_store(&p.counters[blockIdx.x], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -237,34 +289,38 @@ hipError_t launch_qgemv_mfma(const float* a, const QuantWeight& w, float* out, u
     const uint32_t n_tiles = (p.n + 15) / 16;
     const uint32_t n_blocks = (n_tiles + kWavesPerBlock - 1) / kWavesPerBlock;
 
-    // Split K so that ~512 blocks run, keeping >= 2 superblocks per split,
-    // whole groups per split, and the limb slice within the LDS budget.
+    // Split K so that each wave holds at most kPrefetch superblocks (INT8:
+    // half, two loads each), about 1024 waves run, splits cover whole
+    // groups, and the limb slice fits the LDS budget.
     const uint32_t sb_per_group = w.group >= 128 ? w.group / 128 : 1;
-    uint32_t splits = (512 + n_blocks - 1) / n_blocks;
-    splits = min(splits, max(1u, p.sb_total / 2));
+    const uint32_t pf = w.format == SL_QFORMAT_INT4 ? kPrefetch : kPrefetch / 2;  // PF of the kernel
     const uint32_t lds_sb_cap = kLdsLimbBytes / (3 * p.m * 128);
+    uint32_t per_cap = min(pf, lds_sb_cap) / sb_per_group * sb_per_group;
+    if (per_cap == 0) return hipErrorNotSupported;
+    uint32_t splits = max((p.sb_total + per_cap - 1) / per_cap, (1024 + n_tiles - 1) / n_tiles);
+    splits = min(splits, p.sb_total / sb_per_group);
     uint32_t per = (p.sb_total + splits - 1) / splits;
     per = (per + sb_per_group - 1) / sb_per_group * sb_per_group;
-    if (per > lds_sb_cap) per = lds_sb_cap / sb_per_group * sb_per_group;
-    if (per == 0) return hipErrorNotSupported;
+    if (per > per_cap) per = per_cap;
     splits = (p.sb_total + per - 1) / per;
-    const uint32_t gcount_max = per * 128 / w.group;
-    if (p.m * gcount_max > 16 * 64) return hipErrorNotSupported;
+    if (p.m * (per * 128 / w.group) > 16 * 64) return hipErrorNotSupported;
     p.sb_per_split = per;
     p.splits = splits;
     if (splits > 1) {
         const uint64_t need = static_cast<uint64_t>(splits) * p.m * p.n;
-        if (need > ws.floats || n_blocks > ws.n_counters) return hipErrorNotSupported;
+        if (need > ws.floats) return hipErrorNotSupported;
         p.partial = ws.data;
-        p.counters = ws.counters;
     } else {
         p.partial = nullptr;
-        p.counters = nullptr;
     }
     const size_t lds = static_cast<size_t>(3) * p.m * per * 128;
     dim3 grid(n_blocks, splits);
     if (w.format == SL_QFORMAT_INT4) qgemv_mfma<4><<<grid, 256, lds, s>>>(p);
     else qgemv_mfma<8><<<grid, 256, lds, s>>>(p);
+    if (splits > 1) {
+        const uint64_t count = static_cast<uint64_t>(p.m) * p.n;
+        qgemv_reduce<<<grid_for(count, 256, 1024), 256, 0, s>>>(p.partial, out, count, splits);
+    }
     return hipGetLastError();
 }
 

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SL_HIP_ABI_VERSION 1u
+#define SL_HIP_ABI_VERSION 2u
 /* sl-ir IR_VERSION this backend implements (ARCH-0004 §12). */
 #define SL_IR_VERSION 2u
 #define SL_MAX_RANK 8u
@@ -259,9 +259,36 @@ typedef struct sl_capabilities {
 void sl_hip_capabilities(sl_capabilities *out);
 
 /* The hipStream_t the device enqueues all work on (as void*), so a caller
- * can record HIP events around its dispatches for timing. No reference
+ * can record HIP events around its submissions for timing. No reference
  * counterpart (CpuDevice has no stream). */
 void *sl_hip_stream(const sl_hip_device *device);
+
+/* Submission of logged dispatches (no reference counterpart: CpuDevice
+ * executes each dispatch at once). sl_hip_dispatch validates and logs;
+ * logged commands are enqueued on the stream, in order, by sl_hip_submit and
+ * before any call that can observe their effects (synchronize, upload,
+ * download, bind_quantized, destroy). sl_hip_submit returns without waiting;
+ * a kernel launch failure is reported by it or by the next synchronize. */
+sl_status sl_hip_submit(sl_hip_device *device);
+
+/* Submission options, all on by default:
+ *   SL_HIP_OPT_FUSION: adjacent commands may run as one kernel (every
+ *     command's outputs are still written);
+ *   SL_HIP_OPT_GRAPHS: a submission identical to the previous one except for
+ *     past_len values is captured as a HIP graph and later ones replay it. */
+#define SL_HIP_OPT_FUSION 1u
+#define SL_HIP_OPT_GRAPHS 2u
+sl_status sl_hip_set_options(sl_hip_device *device, uint32_t options);
+
+/* Counters of the submission machinery since the device was created. */
+typedef struct sl_hip_stats {
+    uint64_t submissions;    /* non-empty submissions */
+    uint64_t commands;       /* commands submitted */
+    uint64_t fused_commands; /* commands that ran inside a fused launch */
+    uint64_t graph_captures; /* submissions captured as a graph */
+    uint64_t graph_replays;  /* submissions run by replaying a graph */
+} sl_hip_stats;
+void sl_hip_get_stats(const sl_hip_device *device, sl_hip_stats *out);
 
 /* ABI version of the loaded library (SL_HIP_ABI_VERSION). */
 uint32_t sl_hip_abi_version(void);

@@ -5,10 +5,21 @@
 // (crates/backends/backend-cpu/src/device.rs:31-213):
 //  * buffers are device allocations indexed by dense u32 ids, zero-filled at
 //    allocation (device.rs:55-83);
-//  * dispatch() validates exactly as CpuDevice does (validate.cpp), then
-//    enqueues the op's kernels on the device's single stream and returns;
-//  * synchronize() waits for the stream (CpuDevice's is a no-op because it is
-//    synchronous).
+//  * dispatch() validates exactly as CpuDevice does (validate.cpp) and logs
+//    the accepted command; every error a reference dispatch reports is
+//    reported here, at the same call;
+//  * the log is submitted to the device's single stream before anything can
+//    observe its effects: synchronize(), upload, download, bind_quantized
+//    (and sl_hip_submit). Submission runs the commands in order, fusing
+//    adjacent ones where one kernel can do their work (an RMSNorm into the
+//    GEMVs that read its output, q/k/v GEMVs into one launch, a GEMV into
+//    the residual Add after it, gate/up into one launch with the silu*up
+//    epilogue); every command's outputs are still written. A log that
+//    repeats the previous one (decode steps) is captured once as a HIP
+//    graph and replayed; past_len reaches its kernels through a small device
+//    array set before each submission, so one graph serves every step;
+//  * synchronize() submits, then waits for the stream (CpuDevice's is a
+//    no-op because it is synchronous); a kernel failure surfaces there.
 // Ports that share a buffer (the sl-core scratchpad) are plain base + offset
 // pointers; CpuDevice's take/restore staging (device.rs:379-706) has no GPU
 // counterpart.
@@ -22,6 +33,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <new>
+#include <utility>
 #include <vector>
 
 #include "kernels/kernels.h"
@@ -44,8 +56,29 @@ struct Buffer {
     bool mirrored = false;
     // group-quantized binding
     uint32_t scales = 0;
-    uint8_t* tiles = nullptr;
+    uint8_t* tiles = nullptr;  // private codes, then (Mfma) tile-ordered scales
+    float* tile_scales = nullptr;
     QuantLayout layout = QuantLayout::RowMajor;
+};
+
+constexpr size_t kLogFlushLength = 8192;  // submit early past this many logged commands
+constexpr size_t kGraphCacheSize = 16;
+
+// An accepted command waiting for submission.
+struct Logged {
+    Plan plan;
+    sl_buffer_ref in[kMaxInputs];
+    sl_buffer_ref out;
+    uint32_t n_in = 0;
+    int32_t dyn_slot = -1;  // index of its past_len in the device array, if it reads one
+};
+
+struct GraphEntry {
+    std::vector<uint64_t> key;
+    uint64_t hash = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    uint64_t last_use = 0;
 };
 
 }  // namespace
@@ -59,6 +92,16 @@ struct Device : BufferView {
     uint32_t* counters = nullptr;
     std::vector<uint32_t> id_scratch;
     Error last;
+    // deferred submission
+    std::vector<Logged> log;
+    uint32_t options = SL_HIP_OPT_FUSION | SL_HIP_OPT_GRAPHS;
+    uint32_t* dyn = nullptr;  // device past_len slots
+    uint32_t dyn_cap = 0;
+    std::vector<uint32_t> dyn_values;
+    std::vector<uint64_t> key, prev_key;
+    std::vector<GraphEntry> graphs;
+    uint64_t use_clock = 0;
+    sl_hip_stats stats{};
 
     size_t count() const override { return buffers.size(); }
     const sl_buffer_desc* get(uint32_t id) const override {
@@ -74,6 +117,8 @@ struct Device : BufferView {
 };
 
 namespace {
+
+sl_status flush(Device* d);
 
 float* fptr(Device* d, const sl_buffer_ref& r) {
     return static_cast<float*>(d->buffers[r.buffer].ptr) + r.offset;
@@ -120,6 +165,7 @@ sl_status allocate(Device* d, size_t elements, size_t align, uint32_t kind, uint
 
 sl_status copy_in(Device* d, uint32_t id, const void* data, size_t len, uint32_t kind) {
     if (id >= d->buffers.size() || d->buffers[id].desc.kind != kind) return d->fail(Error::invalid_buffer(id));
+    if (d->buffers[id].desc.elements == len && len != 0 && flush(d) != SL_OK) return d->last.status;
     Buffer& b = d->buffers[id];
     if (b.desc.elements != len) return d->fail(Error::invalid_range(id, 0, len));
     if (len == 0) return SL_OK;
@@ -134,11 +180,22 @@ sl_status copy_in(Device* d, uint32_t id, const void* data, size_t len, uint32_t
         if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
         if (e != hipSuccess) return d->hip_fail(e);
     }
+    if (kind == SL_BUFFER_F32) {
+        // ... and re-uploaded scales refresh every tile-ordered copy made from them.
+        for (const Buffer& p : d->buffers) {
+            if (p.tile_scales == nullptr || p.scales != id) continue;
+            e = launch_scale_repack(static_cast<const float*>(b.ptr), p.tile_scales, p.desc.qn, p.desc.qk,
+                                    p.desc.group_size, d->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+            if (e != hipSuccess) return d->hip_fail(e);
+        }
+    }
     return SL_OK;
 }
 
 sl_status copy_out(Device* d, uint32_t id, void* out, size_t len, uint32_t kind) {
     if (id >= d->buffers.size() || d->buffers[id].desc.kind != kind) return d->fail(Error::invalid_buffer(id));
+    if (d->buffers[id].desc.elements == len && len != 0 && flush(d) != SL_OK) return d->last.status;
     Buffer& b = d->buffers[id];
     if (b.desc.elements != len) return d->fail(Error::invalid_range(id, 0, len));
     if (len == 0) return SL_OK;
@@ -190,6 +247,7 @@ WeightRef weight_ref(Device* d, const sl_buffer_ref& r, const QuantOperand& q) {
     w.quant.tiles = b.tiles;
     w.quant.layout = b.layout;
     w.quant.scales = static_cast<const float*>(d->buffers[b.scales].ptr);
+    w.quant.tile_scales = b.tile_scales;
     w.quant.format = q.format;
     w.quant.group = q.group;
     w.quant.n = q.n;
@@ -197,8 +255,10 @@ WeightRef weight_ref(Device* d, const sl_buffer_ref& r, const QuantOperand& q) {
     return w;
 }
 
-// Enqueues the kernels of one validated command.
-hipError_t launch(Device* d, const Plan& p, const sl_buffer_ref* in, const sl_buffer_ref* out) {
+// Enqueues the kernels of one validated command; `dyn`, when set, is the
+// device word its kernels read past_len from.
+hipError_t launch(Device* d, const Plan& p, const sl_buffer_ref* in, const sl_buffer_ref* out,
+                  const uint32_t* dyn) {
     hipStream_t s = d->stream;
     const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
     switch (p.code) {
@@ -214,9 +274,9 @@ hipError_t launch(Device* d, const Plan& p, const sl_buffer_ref* in, const sl_bu
                                  p.m, p.k, p.n, p.code == SL_OP_MATMUL_NT, s);
         }
         case SL_OP_SOFTMAX:
-            return launch_softmax(fptr(d, in[0]), fptr(d, out[0]), p.rows, p.cols, false, 0, 0, s);
+            return launch_softmax(fptr(d, in[0]), fptr(d, out[0]), p.rows, p.cols, false, 0, 0, nullptr, s);
         case SL_OP_SOFTMAX_CAUSAL:
-            return launch_softmax(fptr(d, in[0]), fptr(d, out[0]), p.rows, p.cols, true, p.seq, p.past_len, s);
+            return launch_softmax(fptr(d, in[0]), fptr(d, out[0]), p.rows, p.cols, true, p.seq, p.past_len, dyn, s);
         case SL_OP_RMS_NORM:
             return launch_rms_norm(fptr(d, in[0]), fptr(d, in[1]), fptr(d, out[0]), p.rows, p.hidden, p.eps, s);
         case SL_OP_ROPE:
@@ -240,11 +300,11 @@ hipError_t launch(Device* d, const Plan& p, const sl_buffer_ref* in, const sl_bu
                                         p.code == SL_OP_SPLIT_HEADS, s);
         case SL_OP_KV_APPEND:
             return launch_kv_append(fptr(d, in[0]), fptr(d, in[1]), fptr(d, in[p.state_index]), p.batch, p.layers,
-                                    p.layer, p.kv_heads, p.head_dim, p.max_seq, p.past_len, p.seq, s);
+                                    p.layer, p.kv_heads, p.head_dim, p.max_seq, p.past_len, p.seq, dyn, s);
         case SL_OP_CAUSAL_ATTENTION: {
             AttentionArgs a{fptr(d, in[0]), fptr(d, in[1]), fptr(d, in[2]), fptr(d, in[p.state_index]),
                             fptr(d, out[0]), p.batch, p.layers, p.layer, p.heads, p.kv_heads, p.seq,
-                            p.past_len, p.head_dim, p.max_seq, p.scale};
+                            p.past_len, p.head_dim, p.max_seq, p.scale, dyn};
             return launch_attention(a, ws, s);
         }
         case SL_OP_SWIGLU:
@@ -276,6 +336,320 @@ bool device_limits(Device* d, const Plan& p, Error* err) {
         return false;
     }
     return true;
+}
+
+// ---- deferred submission: fusion, past_len slots, graph replay ----
+
+bool reads_past(uint32_t code) {
+    return code == SL_OP_SOFTMAX_CAUSAL || code == SL_OP_KV_APPEND || code == SL_OP_CAUSAL_ATTENTION;
+}
+
+bool overlaps(const sl_buffer_ref& a, const sl_buffer_ref& b) {
+    return a.buffer == b.buffer && a.len != 0 && b.len != 0 && a.offset < b.offset + b.len &&
+           b.offset < a.offset + a.len;
+}
+bool same_ref(const sl_buffer_ref& a, const sl_buffer_ref& b) {
+    return a.buffer == b.buffer && a.offset == b.offset && a.len == b.len;
+}
+
+// Port `port` of `c` is a quantized weight in the MFMA tile layout.
+bool mfma_weight(const Device* d, const Logged& c, size_t port) {
+    if (!c.plan.quant[port].present) return false;
+    const Buffer& b = d->buffers[c.in[port].buffer];
+    return b.layout == QuantLayout::Mfma && b.tile_scales != nullptr;
+}
+
+// An Add right after a command that wrote `o` (rows * n values), adding it to
+// another operand: returns the port of that other operand, or -1. The add's
+// output may be `o` itself (the memory plan reuses a dead value's region;
+// the fused epilogue writes o then resid + o to each element from the same
+// thread, leaving what the two commands leave) but must not otherwise
+// overlap `o`, and must not overlap the inputs the fused kernel still reads.
+int residual_port(const Logged& a, const sl_buffer_ref& o, uint64_t count, const sl_buffer_ref* reads,
+                  size_t n_reads) {
+    if (a.plan.code != SL_OP_ADD || a.plan.len != count) return -1;
+    int other = same_ref(a.in[1], o) ? 0 : same_ref(a.in[0], o) ? 1 : -1;
+    if (other < 0 || overlaps(a.in[other], o) || (overlaps(a.out, o) && !same_ref(a.out, o))) return -1;
+    for (size_t i = 0; i < n_reads; ++i)
+        if (overlaps(a.out, reads[i])) return -1;
+    return other;
+}
+
+// Tries to run log[i..] as one fused unit; returns the number of commands it
+// covered (0: nothing launched, run log[i] alone).
+size_t try_fuse(Device* d, size_t i, hipError_t* err) {
+    const size_t n = d->log.size();
+    const Logged* norm = nullptr;
+    size_t j = i;
+    if (d->log[i].plan.code == SL_OP_RMS_NORM) {
+        norm = &d->log[i];
+        j = i + 1;
+        if (j >= n || overlaps(norm->out, norm->in[0]) || overlaps(norm->out, norm->in[1])) return 0;
+    }
+    const Logged& c1 = d->log[j];
+    if (norm && !same_ref(c1.in[0], norm->out)) return 0;
+    const sl_buffer_ref a_ref = norm ? norm->in[0] : c1.in[0];  // what the fused kernel reads
+    sl_buffer_ref reads[3] = {a_ref, norm ? norm->in[1] : a_ref, norm ? norm->out : a_ref};
+    const size_t n_reads = 3;
+    QgemvFused f{};
+    f.a = fptr(d, a_ref);
+    if (norm) {
+        f.gamma = fptr(d, norm->in[1]);
+        f.normed = fptr(d, norm->out);
+        f.eps = norm->plan.eps;
+    }
+    QuantWeight w[kFusedMaxSegs];
+
+    if (c1.plan.code == SL_OP_MATMUL_NT && mfma_weight(d, c1, 1)) {
+        const uint64_t rows = c1.plan.batch * c1.plan.m, k = c1.plan.k;
+        if (rows == 0 || (norm && (norm->plan.rows != rows || norm->plan.hidden != k))) return 0;
+        sl_buffer_ref outs[kFusedMaxSegs];
+        uint32_t cnt = 0;
+        for (size_t t = j; t < n && cnt < kFusedMaxSegs; ++t) {
+            const Logged& c = d->log[t];
+            if (c.plan.code != SL_OP_MATMUL_NT || !mfma_weight(d, c, 1) || !same_ref(c.in[0], c1.in[0]) ||
+                c.plan.batch * c.plan.m != rows || c.plan.k != k)
+                break;
+            bool clash = false;
+            for (size_t r = 0; r < n_reads; ++r) clash = clash || overlaps(c.out, reads[r]);
+            for (uint32_t u = 0; u < cnt; ++u) clash = clash || overlaps(c.out, outs[u]);
+            if (clash) break;
+            w[cnt] = weight_ref(d, c.in[1], c.plan.quant[1]).quant;
+            outs[cnt] = c.out;
+            f.w[cnt] = &w[cnt];
+            f.out[cnt] = fptr(d, c.out);
+            ++cnt;
+        }
+        if (cnt == 0 || (cnt == 1 && !norm && j + 1 >= n)) return 0;
+        size_t used = (j - i) + cnt;
+        f.nseg = cnt;
+        f.m = rows;
+        f.epilogue = kFusedPlain;
+        if (cnt == 1 && j + 1 < n) {
+            const Logged& a = d->log[j + 1];
+            const int other = residual_port(a, outs[0], rows * w[0].n, reads, n_reads);
+            if (other >= 0) {
+                f.epilogue = kFusedResidual;
+                f.resid[0] = fptr(d, a.in[other]);
+                f.out2[0] = fptr(d, a.out);
+                ++used;
+            }
+        }
+        if (used == 1) return 0;
+        const hipError_t e = launch_qgemv_fused(f, d->stream);
+        if (e == hipErrorNotSupported) return 0;
+        *err = e;
+        d->stats.fused_commands += used;
+        return used;
+    }
+
+    if (c1.plan.code == SL_OP_SWIGLU && mfma_weight(d, c1, 1) && mfma_weight(d, c1, 2) &&
+        c1.plan.quant[3].present) {
+        const uint64_t rows = c1.plan.rows, hidden = c1.plan.hidden, inter = c1.plan.inter;
+        if (rows == 0 || rows * inter > d->workspace_floats / 2 ||
+            (norm && (norm->plan.rows != rows || norm->plan.hidden != hidden)))
+            return 0;
+        for (size_t r = 0; r < n_reads; ++r)
+            if (overlaps(c1.out, reads[r])) return 0;
+        // gate/up pair into the workspace (h = silu(g) * u) ...
+        float* h = d->workspace;
+        w[0] = weight_ref(d, c1.in[1], c1.plan.quant[1]).quant;
+        w[1] = weight_ref(d, c1.in[2], c1.plan.quant[2]).quant;
+        f.w[0] = &w[0];
+        f.w[1] = &w[1];
+        f.out[0] = h;
+        f.nseg = 2;
+        f.m = rows;
+        f.epilogue = kFusedPair;
+        hipError_t e = launch_qgemv_fused(f, d->stream);
+        if (e == hipErrorNotSupported) return 0;
+        if (e != hipSuccess) {
+            *err = e;
+            return 1;
+        }
+        size_t used = (j - i) + 1;
+        // ... then the down projection, with the residual Add when one follows
+        const WeightRef down = weight_ref(d, c1.in[3], c1.plan.quant[3]);
+        QgemvFused g{};
+        g.a = h;
+        w[2] = down.quant;
+        g.w[0] = &w[2];
+        g.out[0] = fptr(d, c1.out);
+        g.nseg = 1;
+        g.m = rows;
+        g.epilogue = kFusedPlain;
+        const sl_buffer_ref dreads[2] = {a_ref, norm ? norm->out : a_ref};
+        if (j + 1 < n) {
+            const Logged& a = d->log[j + 1];
+            const int other = residual_port(a, c1.out, rows * hidden, dreads, 2);
+            if (other >= 0) {
+                g.epilogue = kFusedResidual;
+                g.resid[0] = fptr(d, a.in[other]);
+                g.out2[0] = fptr(d, a.out);
+            }
+        }
+        e = mfma_weight(d, c1, 3) ? launch_qgemv_fused(g, d->stream) : hipErrorNotSupported;
+        if (e == hipErrorNotSupported) {
+            const Workspace rest = Workspace{d->workspace, d->workspace_floats, d->counters, kCounterWords}.after(
+                d->workspace_floats / 2);
+            e = launch_linear(h, down, g.out[0], rows, hidden, inter, rest, d->stream);
+        } else if (g.epilogue == kFusedResidual) {
+            ++used;
+        }
+        *err = e;
+        d->stats.fused_commands += used;
+        return used;
+    }
+    return 0;
+}
+
+const uint32_t* dyn_of(const Device* d, const Logged& c) {
+    return c.dyn_slot >= 0 ? d->dyn + c.dyn_slot : nullptr;
+}
+
+hipError_t run_log(Device* d) {
+    for (size_t i = 0; i < d->log.size();) {
+        size_t used = 0;
+        hipError_t e = hipSuccess;
+        if (d->options & SL_HIP_OPT_FUSION) used = try_fuse(d, i, &e);
+        if (e != hipSuccess) return e;
+        if (used == 0) {
+            const Logged& c = d->log[i];
+            e = launch(d, c.plan, c.in, &c.out, dyn_of(d, c));
+            if (e != hipSuccess) return e;
+            used = 1;
+        }
+        i += used;
+    }
+    return hipSuccess;
+}
+
+void drop_graphs(Device* d) {
+    for (GraphEntry& g : d->graphs) {
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        if (g.graph) (void)hipGraphDestroy(g.graph);
+    }
+    d->graphs.clear();
+    d->prev_key.clear();
+}
+
+// Everything that decides which kernels a submission launches, with what
+// arguments: the commands (past_len aside) and the submission options.
+void build_key(Device* d) {
+    std::vector<uint64_t>& k = d->key;
+    k.clear();
+    k.push_back(d->options);
+    auto f = [](float x) {
+        uint32_t u;
+        std::memcpy(&u, &x, 4);
+        return static_cast<uint64_t>(u);
+    };
+    for (const Logged& c : d->log) {
+        const Plan& p = c.plan;
+        k.insert(k.end(), {p.code, p.rows, p.cols, p.hidden, p.batch, p.batch_a, p.batch_b, p.m, p.k, p.n, p.heads,
+                           p.kv_heads, p.seq, p.head_dim, p.layers, p.layer, p.max_seq,
+                           reads_past(p.code) ? 0 : p.past_len, p.seq_len, p.vocab, p.inter, p.out_features, p.len,
+                           f(p.eps), f(p.theta), f(p.factor), f(p.scale), p.rope_variant,
+                           static_cast<uint64_t>(static_cast<int64_t>(p.state_index)), c.n_in,
+                           static_cast<uint64_t>(static_cast<int64_t>(c.dyn_slot))});
+        for (size_t i = 0; i < kMaxInputs; ++i) {
+            const QuantOperand& q = p.quant[i];
+            k.insert(k.end(), {static_cast<uint64_t>(q.present), q.format, q.group, q.n, q.k});
+        }
+        for (uint32_t i = 0; i < c.n_in; ++i) k.insert(k.end(), {c.in[i].buffer, c.in[i].offset, c.in[i].len});
+        k.insert(k.end(), {c.out.buffer, c.out.offset, c.out.len});
+    }
+}
+
+uint64_t key_hash(const std::vector<uint64_t>& k) {
+    uint64_t h = 1469598103934665603ull;
+    for (uint64_t v : k) h = (h ^ v) * 1099511628211ull;
+    return h;
+}
+
+// Enqueues the logged commands; the log is empty afterwards either way.
+hipError_t submit(Device* d) {
+    if (d->log.empty()) return hipSuccess;
+    hipError_t e = hipSuccess;
+    uint32_t slots = 0;
+    for (Logged& c : d->log) c.dyn_slot = reads_past(c.plan.code) ? static_cast<int32_t>(slots++) : -1;
+    if (slots > d->dyn_cap) {
+        // Graphs hold the old array's address.
+        e = hipStreamSynchronize(d->stream);
+        drop_graphs(d);
+        if (d->dyn) (void)hipFree(d->dyn);
+        d->dyn = nullptr;
+        d->dyn_cap = 0;
+        const uint32_t cap = (slots + 255) / 256 * 256;
+        if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&d->dyn), cap * sizeof(uint32_t));
+        if (e != hipSuccess) {
+            d->log.clear();
+            return e;
+        }
+        d->dyn_cap = cap;
+    }
+    d->dyn_values.clear();
+    for (const Logged& c : d->log)
+        if (c.dyn_slot >= 0) d->dyn_values.push_back(static_cast<uint32_t>(c.plan.past_len));
+    if (slots) e = launch_set_words(d->dyn, d->dyn_values.data(), slots, d->stream);
+
+    d->stats.submissions += 1;
+    d->stats.commands += d->log.size();
+    build_key(d);
+    const uint64_t hash = key_hash(d->key);
+    GraphEntry* hit = nullptr;
+    for (GraphEntry& g : d->graphs)
+        if (g.hash == hash && g.key == d->key) hit = &g;
+    if (e != hipSuccess) {
+        // nothing more
+    } else if (hit) {
+        hit->last_use = ++d->use_clock;
+        e = hipGraphLaunch(hit->exec, d->stream);
+        d->stats.graph_replays += 1;
+    } else if ((d->options & SL_HIP_OPT_GRAPHS) && d->key == d->prev_key) {
+        // Seen twice in a row: capture it.
+        GraphEntry g;
+        bool captured = false;
+        if (hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+            const hipError_t run = run_log(d);
+            const hipError_t end = hipStreamEndCapture(d->stream, &g.graph);
+            if (run == hipSuccess && end == hipSuccess && g.graph &&
+                hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0) == hipSuccess)
+                captured = true;
+        }
+        if (captured) {
+            if (d->graphs.size() >= kGraphCacheSize) {
+                size_t lru = 0;
+                for (size_t i = 1; i < d->graphs.size(); ++i)
+                    if (d->graphs[i].last_use < d->graphs[lru].last_use) lru = i;
+                (void)hipGraphExecDestroy(d->graphs[lru].exec);
+                (void)hipGraphDestroy(d->graphs[lru].graph);
+                d->graphs.erase(d->graphs.begin() + static_cast<std::ptrdiff_t>(lru));
+            }
+            g.key = d->key;
+            g.hash = hash;
+            g.last_use = ++d->use_clock;
+            d->graphs.push_back(g);
+            e = hipGraphLaunch(d->graphs.back().exec, d->stream);
+            d->stats.graph_captures += 1;
+        } else {
+            if (g.exec) (void)hipGraphExecDestroy(g.exec);
+            if (g.graph) (void)hipGraphDestroy(g.graph);
+            (void)hipGetLastError();
+            e = run_log(d);
+        }
+    } else {
+        e = run_log(d);
+    }
+    std::swap(d->prev_key, d->key);
+    d->log.clear();
+    return e;
+}
+
+sl_status flush(Device* d) {
+    const hipError_t e = submit(d);
+    if (e != hipSuccess) return d->hip_fail(e);
+    return SL_OK;
 }
 
 }  // namespace
@@ -327,7 +701,10 @@ sl_status sl_hip_device_create(int ordinal, sl_hip_device** out) {
 void sl_hip_device_destroy(sl_hip_device* d) {
     if (d == nullptr) return;
     (void)hipSetDevice(d->ordinal);
+    (void)slhip::flush(d);
     (void)hipStreamSynchronize(d->stream);
+    slhip::drop_graphs(d);
+    if (d->dyn) (void)hipFree(d->dyn);
     for (auto& b : d->buffers) {
         if (b.base) (void)hipFree(b.base);
         if (b.tiles) (void)hipFree(b.tiles);
@@ -374,16 +751,33 @@ sl_status sl_hip_dispatch(sl_hip_device* d, const sl_op* op, const sl_buffer_ref
     if (!slhip::device_limits(d, plan, &err)) return d->fail(err);
     if (plan.code == SL_OP_GATHER && !slhip::gather_ids_in_range(d, inputs[1], plan.vocab, &err))
         return d->fail(err);
-    hipError_t e = slhip::launch(d, plan, inputs, outputs);
-    if (e != hipSuccess) return d->hip_fail(e);
+    slhip::Logged c;
+    c.plan = plan;
+    c.n_in = static_cast<uint32_t>(n_inputs);
+    for (size_t i = 0; i < n_inputs; ++i) c.in[i] = inputs[i];
+    if (n_outputs) c.out = outputs[0];
+    d->log.push_back(c);
+    if (d->log.size() >= slhip::kLogFlushLength) return slhip::flush(d);
     return SL_OK;
 }
 
 sl_status sl_hip_synchronize(sl_hip_device* d) {
+    if (slhip::flush(d) != SL_OK) return d->last.status;
     hipError_t e = hipStreamSynchronize(d->stream);
     if (e != hipSuccess) return d->hip_fail(e);
     return SL_OK;
 }
+
+sl_status sl_hip_submit(sl_hip_device* d) { return slhip::flush(d); }
+
+sl_status sl_hip_set_options(sl_hip_device* d, uint32_t options) {
+    if (slhip::flush(d) != SL_OK) return d->last.status;
+    d->options = options & (SL_HIP_OPT_FUSION | SL_HIP_OPT_GRAPHS);
+    d->prev_key.clear();
+    return SL_OK;
+}
+
+void sl_hip_get_stats(const sl_hip_device* d, sl_hip_stats* out) { *out = d->stats; }
 
 void sl_hip_last_error(const sl_hip_device* d, sl_error* out) {
     const Error& e = d->last;
@@ -412,12 +806,19 @@ sl_status sl_hip_bind_quantized(sl_hip_device* d, uint32_t payload, uint32_t sca
         return d->fail(Error::execution("quantized payload size does not match [n, k]"));
     if (d->buffers[scales].desc.elements != static_cast<uint64_t>(n) * (k / group_size))
         return d->fail(Error::execution("quantized scale count does not match [n, k / group_size]"));
+    // Logged commands read the old binding; the graphs hold its tile address.
+    if (slhip::flush(d) != SL_OK) return d->last.status;
+    slhip::drop_graphs(d);
     const slhip::QuantLayout layout = slhip::quant_layout_for(qformat, n, k, group_size);
-    const uint64_t bytes = slhip::quant_tile_bytes(qformat, n, k, layout);
+    const uint64_t code_bytes = slhip::quant_tile_bytes(qformat, n, k, layout);
+    const uint64_t scale_offset = (code_bytes + 255) / 256 * 256;
+    const uint64_t scale_floats = slhip::quant_tile_scale_floats(n, k, group_size, layout);
+    const uint64_t bytes = scale_floats ? scale_offset + scale_floats * 4 : code_bytes;
     if (pb.tiles) {
         (void)hipStreamSynchronize(d->stream);
         (void)hipFree(pb.tiles);
         pb.tiles = nullptr;
+        pb.tile_scales = nullptr;
     }
     if (bytes != 0) {
         if (hipMalloc(reinterpret_cast<void**>(&pb.tiles), bytes) != hipSuccess) {
@@ -425,6 +826,7 @@ sl_status sl_hip_bind_quantized(sl_hip_device* d, uint32_t payload, uint32_t sca
             pb.tiles = nullptr;
             return d->fail(Error::out_of_memory(bytes / 4));
         }
+        if (scale_floats) pb.tile_scales = reinterpret_cast<float*>(pb.tiles + scale_offset);
     }
     pb.desc.quantized = 1;
     pb.desc.qformat = qformat;
@@ -435,6 +837,9 @@ sl_status sl_hip_bind_quantized(sl_hip_device* d, uint32_t payload, uint32_t sca
     pb.layout = layout;
     hipError_t e = slhip::launch_quant_repack(static_cast<const uint8_t*>(pb.ptr), pb.tiles, qformat, n, k, layout,
                                               d->stream);
+    if (e == hipSuccess && pb.tile_scales)
+        e = slhip::launch_scale_repack(static_cast<const float*>(d->buffers[scales].ptr), pb.tile_scales, n, k,
+                                       group_size, d->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
     if (e != hipSuccess) return d->hip_fail(e);
     return SL_OK;

@@ -9,13 +9,13 @@
 //
 // Kernels:
 //  * attn_decode + attn_decode_merge — decode and short chunks (group * seq
-//    <= 16 query rows per KV head). A block owns one (batch, KV head, 32-key
-//    chunk); all query rows sharing that KV head are served from one read of
-//    the chunk's K/V rows through LDS. Rows at or after past_len come from the
-//    new K/V and the owning block appends them to the cache (kv_append fused).
-//    The grid depends only on max_seq; chunks past the current length exit.
-//    Partial (m, l, acc) go to the workspace and the merge kernel combines the
-//    active chunks in order.
+//    <= 16 query rows per KV head, head_dim a multiple of 64 up to 256): a
+//    (P, kv_heads, batch) grid with P fixed by max_seq, so one launch shape
+//    serves every past_len. 16-key tiles are dealt round-robin to the blocks'
+//    waves, all query rows sharing a KV head are served from one read of
+//    each K/V row, rows at or after past_len come from the new K/V and are
+//    appended to the cache by the lane group that reads them (kv_append
+//    fused). One partial (m, l, acc) per block; the merge kernel combines P.
 //  * attn_split / attn_merge — other decode shapes: one wave per
 //    (b, h, t, key chunk), score by wave reduction, then a merge kernel.
 //  * attn_tiled — prefill: a block owns 64 queries of one head, two threads
@@ -39,7 +39,10 @@ struct Geo {
     uint32_t past_len, chunk, chunks;
     uint64_t batch_stride, layer_offset, parity_stride;  // elements
     float scale;
+    const uint32_t* dyn;  // when set, dyn[0] is past_len
 };
+
+__device__ __forceinline__ uint32_t past_of(const Geo& g) { return g.dyn != nullptr ? g.dyn[0] : g.past_len; }
 
 template <int DPL>  // head_dim <= 64 * DPL
 __global__ __launch_bounds__(256) void attn_split(Geo g, uint64_t items) {
@@ -55,7 +58,7 @@ __global__ __launch_bounds__(256) void attn_split(Geo g, uint64_t items) {
     const uint32_t t = rest % g.seq;
     const uint64_t b = rest / g.seq;
     const uint32_t h = kvh * g.group + gi;
-    const uint32_t key_count = g.past_len + t + 1;
+    const uint32_t key_count = past_of(g) + t + 1;
     const uint32_t k0 = c * g.chunk;
     const uint32_t k1 = min(k0 + g.chunk, key_count);
     const uint64_t qrow = ((b * g.heads + h) * g.seq + t) * g.head_dim;
@@ -137,185 +140,305 @@ __global__ __launch_bounds__(256) void attn_merge(Geo g) {
 }
 
 
-constexpr int kDecodeRows = 16;  // query rows (group * seq) per KV head
+// ---- decode: flash-decoding over a grid fixed by max_seq ----
+//
+// Keys are cut into tiles of 16. Tile i belongs to block i % P, wave
+// (i / P) % 4 of that block, so every block of the (P, kv_heads, batch) grid
+// gets an equal share at any length and the grid never depends on past_len.
+// Inside a wave, four groups of 16 lanes each take 4 consecutive keys of the
+// tile; a lane holds DV float4 of every key row (dims li*4 + 64*u), so a
+// group reads each K/V row as contiguous 256-byte runs and all 8*DV loads of
+// a tile are in flight together. Scores are reduced across the 16 lanes of a
+// group; each group keeps its own online-softmax state (m, l, acc) for the
+// RT query rows of this KV head, the groups and then the waves are combined,
+// and the block writes one partial [(b, kvh, p)][r][4 + D] = (m, l, -, -,
+// acc). Rows j >= past_len come from k_new / v_new and the lane group that
+// reads one also appends it to the cache.
+constexpr int kDecodeLanes = 16;                       // lanes per key
+constexpr int kDecodeKeys = 4;                         // keys per lane group per tile
+constexpr int kDecodeTile = kDecodeKeys * kWave / kDecodeLanes;  // 16 keys per wave tile
+constexpr int kDecodeMaxRows = 16;
+constexpr uint32_t kDecodePartStride = 4;              // floats before acc in a partial row
 
-// One block per (key chunk of KT keys, KV head, batch); chunks at or beyond
-// past_len + seq exit at once, so the grid (fixed by max_seq) can be replayed
-// for any length. LDS: q [R][D], k/v [KT][D + 1], p [R][KT]. Every global
-// load of a stage is issued before any is used.
-template <int KT, bool VEC>
+__device__ __forceinline__ float group_sum16(float v) { return row_sum(v); }  // a lane group is a DPP row
+
+__device__ __forceinline__ float4 f4_fma(float a, float4 x, float4 y) {
+    return make_float4(fmaf(a, x.x, y.x), fmaf(a, x.y, y.y), fmaf(a, x.z, y.z), fmaf(a, x.w, y.w));
+}
+
+__device__ __forceinline__ float4 f4_scale(float4 x, float a) { return make_float4(x.x * a, x.y * a, x.z * a, x.w * a); }
+
+// Folds state (mo, lo, ao) into (m, l, a); an empty state has m == -inf.
+template <int DV>
+__device__ __forceinline__ void fold_state(float& m, float& l, float4 (&a)[DV], float mo, float lo,
+                                           const float4 (&ao)[DV]) {
+    const float mn = fmaxf(m, mo);
+    if (mn == -INFINITY) return;
+    const float ca = m == -INFINITY ? 0.f : expf(m - mn);
+    const float cb = mo == -INFINITY ? 0.f : expf(mo - mn);
+    l = l * ca + lo * cb;
+#pragma unroll
+    for (int u = 0; u < DV; ++u) a[u] = f4_fma(cb, ao[u], f4_scale(a[u], ca));
+    m = mn;
+}
+
+template <int DV, int RT>
 __global__ __launch_bounds__(256) void attn_decode(Geo g) {
-    extern __shared__ float lds[];
-    __shared__ float m_row[kDecodeRows], l_row[kDecodeRows];
-    const uint32_t D = g.head_dim, S = g.seq, G = g.group;
-    const uint32_t R = G * S;  // query rows: r = gi * S + t
-    const uint32_t c = blockIdx.x, kvh = blockIdx.y;
+    constexpr int D4 = 16 * DV;  // float4 per row
+    __shared__ float4 qs[RT * D4];
+    __shared__ float4 wacc[4][RT][D4];
+    __shared__ float wml[4][RT][2];
+    const uint32_t S = g.seq, G = g.group, R = G * S;
+    const uint32_t P = gridDim.x, p = blockIdx.x, kvh = blockIdx.y;
     const uint64_t b = blockIdx.z;
-    const int tid = threadIdx.x;
-    const uint32_t keys = g.past_len + S;
-    const uint32_t j0 = c * KT;
-    if (j0 >= keys) return;
-    const uint32_t nk = min(static_cast<uint32_t>(KT), keys - j0);
-    float* qs = lds;                 // [R][D]
-    float* ks = qs + R * D;          // [KT][D + 1]
-    float* vs = ks + KT * (D + 1);   // [KT][D + 1]
-    float* ps = vs + KT * (D + 1);   // [R][KT]
-    const uint64_t time_stride = static_cast<uint64_t>(g.kv_heads) * D;
-    float* kbase = g.wcache + b * g.batch_stride + g.layer_offset + kvh * D;
-    float* vbase = kbase + g.parity_stride;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int grp = lane / kDecodeLanes, li = lane % kDecodeLanes;
+    const uint32_t past = past_of(g), keys = past + S;
+    const uint32_t ntiles = (keys + kDecodeTile - 1) / kDecodeTile;
 
-    if constexpr (VEC) {
-        const uint32_t d4 = D / 4;
-        // q rows of this KV head's query group
-        constexpr int kQ = kDecodeRows * 256 / 4 / 256;  // float4 per thread, worst case
-        float4 qv[kQ];
+    const uint64_t time_stride = static_cast<uint64_t>(g.kv_heads) * (4 * D4);
+    float* kbase = g.wcache + b * g.batch_stride + g.layer_offset + kvh * (4 * D4);
+    float* vbase = kbase + g.parity_stride;
+    // K/V rows of a tile for this lane: cached rows from the cache, new rows
+    // from k_new / v_new, zeros past the end.
+    auto load_tile = [&](uint32_t tile, float4 (&kx)[kDecodeKeys][DV], float4 (&vx)[kDecodeKeys][DV]) {
+        const uint32_t j0 = tile * kDecodeTile + grp * kDecodeKeys;
 #pragma unroll
-        for (int u = 0; u < kQ; ++u) {
-            const uint32_t i = tid + 256 * u;
-            qv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (i < R * d4) {
-                const uint32_t r = i / d4, dd = i % d4, gi = r / S, t = r % S;
-                qv[u] = reinterpret_cast<const float4*>(g.q + ((b * g.heads + kvh * G + gi) * S + t) * D)[dd];
+        for (int kb = 0; kb < kDecodeKeys; ++kb) {
+            // Every lane loads (keys past the end re-read the last row; their
+            // scores are masked to -inf, so they weigh exactly 0), so the
+            // loads carry no branch and the waits before their use are exact.
+            const uint32_t j = min(j0 + kb, keys - 1);
+            const float* kr = kbase + static_cast<uint64_t>(j) * time_stride;
+            const float* vr = vbase + static_cast<uint64_t>(j) * time_stride;
+            if (j >= past) {
+                const uint64_t src = ((b * g.kv_heads + kvh) * S + (j - past)) * (4 * D4);
+                kr = g.k_new + src;
+                vr = g.v_new + src;
+            }
+#pragma unroll
+            for (int u = 0; u < DV; ++u) {
+                kx[kb][u] = reinterpret_cast<const float4*>(kr)[li + 16 * u];
+                vx[kb][u] = reinterpret_cast<const float4*>(vr)[li + 16 * u];
             }
         }
-        // K/V rows: cached rows from the cache, new rows from k_new/v_new
-        constexpr int kKV = KT * 256 / 4 / 256;  // float4 per thread, worst case (D <= 256)
-        float4 kv[kKV], vv[kKV];
+    };
+    // The first tile's loads go out before the query rows are staged, and
+    // each iteration starts the next tile's loads before computing.
+    // query rows: loaded first (rows past R re-read row 0 and are zeroed),
+    // staged in LDS after the first tile's loads have gone out
+    constexpr int QPT = (RT * D4 + 255) / 256;
+    float4 qv[QPT];
 #pragma unroll
-        for (int u = 0; u < kKV; ++u) {
-            const uint32_t i = tid + 256 * u;
-            kv[u] = vv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (i < KT * d4) {
-                const uint32_t jj = i / d4, dd = i % d4, j = j0 + jj;
-                if (jj < nk) {
-                    if (j < g.past_len) {
-                        kv[u] = reinterpret_cast<const float4*>(kbase + j * time_stride)[dd];
-                        vv[u] = reinterpret_cast<const float4*>(vbase + j * time_stride)[dd];
-                    } else {
-                        const uint64_t src = ((b * g.kv_heads + kvh) * S + (j - g.past_len)) * D;
-                        kv[u] = reinterpret_cast<const float4*>(g.k_new + src)[dd];
-                        vv[u] = reinterpret_cast<const float4*>(g.v_new + src)[dd];
-                    }
+    for (int u = 0; u < QPT; ++u) {
+        const uint32_t i = min(static_cast<uint32_t>(tid + 256 * u), static_cast<uint32_t>(RT * D4 - 1));
+        const uint32_t r = min(i / D4, R - 1), c = i % D4, gi = r / S, t = r % S;
+        qv[u] = reinterpret_cast<const float4*>(g.q + ((b * g.heads + kvh * G + gi) * S + t) * (4 * D4))[c];
+    }
+    uint32_t tile = p + P * wave;
+    float4 kv[kDecodeKeys][DV], vv[kDecodeKeys][DV];
+    load_tile(min(tile, ntiles - 1), kv, vv);  // unconditional: a wave with no tile loads and ignores one
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        const uint32_t i = tid + 256 * u;
+        if (i < RT * D4) qs[i] = i / D4 < R ? qv[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
+
+    float m[RT], l[RT];
+    float4 acc[RT][DV];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+#pragma unroll
+        for (int u = 0; u < DV; ++u) acc[r][u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    for (; tile < ntiles; tile += 4 * P) {
+        const uint32_t j0 = tile * kDecodeTile + grp * kDecodeKeys;
+        float4 kn[kDecodeKeys][DV], vn[kDecodeKeys][DV];
+        const bool more = tile + 4 * P < ntiles;
+        load_tile(min(tile + 4 * P, ntiles - 1), kn, vn);
+#pragma unroll
+        for (int kb = 0; kb < kDecodeKeys; ++kb) {
+            const uint32_t j = j0 + kb;
+            if (j >= past && j < keys) {
+#pragma unroll
+                for (int u = 0; u < DV; ++u) {
+                    reinterpret_cast<float4*>(kbase + j * time_stride)[li + 16 * u] = kv[kb][u];
+                    reinterpret_cast<float4*>(vbase + j * time_stride)[li + 16 * u] = vv[kb][u];
                 }
             }
         }
 #pragma unroll
-        for (int u = 0; u < kQ; ++u) {
-            const uint32_t i = tid + 256 * u;
-            if (i < R * d4) reinterpret_cast<float4*>(qs)[i] = qv[u];
-        }
+        for (int r = 0; r < RT; ++r) {
+            if (r >= static_cast<int>(R)) continue;
+            float4 qv[DV];
 #pragma unroll
-        for (int u = 0; u < kKV; ++u) {
-            const uint32_t i = tid + 256 * u;
-            if (i < KT * d4) {
-                const uint32_t jj = i / d4, d = 4 * (i % d4), j = j0 + jj;
-                float* kr = ks + jj * (D + 1) + d;
-                float* vr = vs + jj * (D + 1) + d;
-                kr[0] = kv[u].x; kr[1] = kv[u].y; kr[2] = kv[u].z; kr[3] = kv[u].w;
-                vr[0] = vv[u].x; vr[1] = vv[u].y; vr[2] = vv[u].z; vr[3] = vv[u].w;
-                if (jj < nk && j >= g.past_len) {  // kv_append of the new rows
-                    reinterpret_cast<float4*>(kbase + j * time_stride)[i % d4] = kv[u];
-                    reinterpret_cast<float4*>(vbase + j * time_stride)[i % d4] = vv[u];
+            for (int u = 0; u < DV; ++u) qv[u] = qs[r * D4 + li + 16 * u];
+            const uint32_t limit = past + r % S;  // last visible key of this row
+            float s[kDecodeKeys];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < kDecodeKeys; ++kb) {
+                float dot = 0.f;
+#pragma unroll
+                for (int u = 0; u < DV; ++u) {
+                    dot = fmaf(qv[u].x, kv[kb][u].x, dot);
+                    dot = fmaf(qv[u].y, kv[kb][u].y, dot);
+                    dot = fmaf(qv[u].z, kv[kb][u].z, dot);
+                    dot = fmaf(qv[u].w, kv[kb][u].w, dot);
+                }
+                dot = group_sum16(dot);
+                s[kb] = j0 + kb <= limit ? dot * g.scale : -INFINITY;
+                tmax = fmaxf(tmax, s[kb]);
+            }
+            const float mn = fmaxf(m[r], tmax);
+            if (mn == -INFINITY) continue;
+            const float corr = m[r] == -INFINITY ? 0.f : expf(m[r] - mn);
+            float lsum = l[r] * corr;
+#pragma unroll
+            for (int u = 0; u < DV; ++u) acc[r][u] = f4_scale(acc[r][u], corr);
+#pragma unroll
+            for (int kb = 0; kb < kDecodeKeys; ++kb) {
+                const float pk = s[kb] == -INFINITY ? 0.f : expf(s[kb] - mn);
+                lsum += pk;
+#pragma unroll
+                for (int u = 0; u < DV; ++u) acc[r][u] = f4_fma(pk, vv[kb][u], acc[r][u]);
+            }
+            l[r] = lsum;
+            m[r] = mn;
+        }
+        if (more) {
+#pragma unroll
+            for (int kb = 0; kb < kDecodeKeys; ++kb) {
+#pragma unroll
+                for (int u = 0; u < DV; ++u) {
+                    kv[kb][u] = kn[kb][u];
+                    vv[kb][u] = vn[kb][u];
                 }
             }
         }
-    } else {
-        for (uint32_t i = tid; i < R * D; i += 256) {
-            const uint32_t r = i / D, d = i % D, gi = r / S, t = r % S;
-            qs[i] = g.q[((b * g.heads + kvh * G + gi) * S + t) * D + d];
-        }
-        for (uint32_t i = tid; i < KT * D; i += 256) {
-            const uint32_t jj = i / D, d = i % D, j = j0 + jj;
-            float kx = 0.f, vx = 0.f;
-            if (jj < nk) {
-                if (j < g.past_len) {
-                    kx = kbase[j * time_stride + d];
-                    vx = vbase[j * time_stride + d];
-                } else {
-                    const uint64_t src = ((b * g.kv_heads + kvh) * S + (j - g.past_len)) * D + d;
-                    kx = g.k_new[src];
-                    vx = g.v_new[src];
-                    kbase[j * time_stride + d] = kx;
-                    vbase[j * time_stride + d] = vx;
-                }
+    }
+
+    // combine the four lane groups of the wave, then the four waves
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        if (r >= static_cast<int>(R)) continue;
+#pragma unroll
+        for (int off = kDecodeLanes; off < kWave; off <<= 1) {
+            const float mo = __shfl_xor(m[r], off, kWave), lo = __shfl_xor(l[r], off, kWave);
+            float4 ao[DV];
+#pragma unroll
+            for (int u = 0; u < DV; ++u) {
+                ao[u].x = __shfl_xor(acc[r][u].x, off, kWave);
+                ao[u].y = __shfl_xor(acc[r][u].y, off, kWave);
+                ao[u].z = __shfl_xor(acc[r][u].z, off, kWave);
+                ao[u].w = __shfl_xor(acc[r][u].w, off, kWave);
             }
-            ks[jj * (D + 1) + d] = kx;
-            vs[jj * (D + 1) + d] = vx;
+            fold_state<DV>(m[r], l[r], acc[r], mo, lo, ao);
+        }
+        if (grp == 0) {
+#pragma unroll
+            for (int u = 0; u < DV; ++u) wacc[wave][r][li + 16 * u] = acc[r][u];
+            if (li == 0) {
+                wml[wave][r][0] = m[r];
+                wml[wave][r][1] = l[r];
+            }
         }
     }
     __syncthreads();
-    // scores: one (row, key) pair per thread
-    for (uint32_t i = tid; i < R * KT; i += 256) {
-        const uint32_t r = i / KT, jj = i % KT;
-        const float* qr = qs + r * D;
-        const float* kr = ks + jj * (D + 1);
-        float dot = 0.f;
-        for (uint32_t d = 0; d < D; ++d) dot = fmaf(qr[d], kr[d], dot);
-        const bool vis = jj < nk && j0 + jj <= g.past_len + r % S;
-        ps[i] = vis ? dot * g.scale : -INFINITY;
-    }
-    __syncthreads();
-    // chunk softmax per row: m = max, p = exp(s - m), l = sum p
-    if (tid < static_cast<int>(R)) {
-        float* pr = ps + tid * KT;
-        float mx = -INFINITY;
-        for (int jj = 0; jj < KT; ++jj) mx = fmaxf(mx, pr[jj]);
-        float sum = 0.f;
-        for (int jj = 0; jj < KT; ++jj) {
-            const float e = mx == -INFINITY ? 0.f : expf(pr[jj] - mx);
-            pr[jj] = e;
-            sum += e;
+    const uint64_t row_stride = kDecodePartStride + 4 * D4;
+    float* part = g.ws + ((b * g.kv_heads + kvh) * P + p) * R * row_stride;
+    for (uint32_t i = tid; i < R * D4; i += 256) {
+        const uint32_t r = i / D4, c = i % D4;
+        float mm = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) mm = fmaxf(mm, wml[w][r][0]);
+        float ll = 0.f;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (mm != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float mw = wml[w][r][0];
+                const float cw = mw == -INFINITY ? 0.f : expf(mw - mm);
+                ll = fmaf(wml[w][r][1], cw, ll);
+                a = f4_fma(cw, wacc[w][r][c], a);
+            }
         }
-        m_row[tid] = mx;
-        l_row[tid] = sum;
-    }
-    __syncthreads();
-    // partial of this chunk: [(b, kvh)][chunk][r][2 + D]
-    const uint64_t row_stride = 2 + D;
-    float* part = g.ws + ((b * g.kv_heads + kvh) * g.chunks + c) * R * row_stride;
-    for (uint32_t e = tid; e < R * D; e += 256) {
-        const uint32_t r = e / D, d = e % D;
-        const float* pr = ps + r * KT;
-        float a = 0.f;
-        for (int jj = 0; jj < KT; ++jj) a = fmaf(pr[jj], vs[jj * (D + 1) + d], a);
-        part[r * row_stride + 2 + d] = a;
-    }
-    if (tid < static_cast<int>(R)) {
-        part[tid * row_stride] = m_row[tid];
-        part[tid * row_stride + 1] = l_row[tid];
+        reinterpret_cast<float4*>(part + r * row_stride + kDecodePartStride)[c] = a;
+        if (c == 0) {
+            part[r * row_stride] = mm;
+            part[r * row_stride + 1] = ll;
+        }
     }
 }
 
-// Merges the chunk partials of one (batch, KV head): grid (kv_heads, batch).
-__global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t kt) {
-    __shared__ float m_row[kDecodeRows], inv_row[kDecodeRows];
-    const uint32_t D = g.head_dim, S = g.seq, G = g.group, R = G * S;
+// Merges the P partials of one (KV head, batch): grid (kv_heads, batch).
+// Each wave turns the (m, l) of a query row over all partials into weights
+// exp(m_p - max) / sum; then threads own float4 output slots, several threads
+// per slot when there are few, and sum their share of the partials with all
+// loads of a batch of eight in flight.
+constexpr int kMergeMaxParts = 64;
+
+__global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
+    __shared__ float coef[kMergeMaxParts][kDecodeMaxRows];
+    __shared__ float4 red[256];
+    const uint32_t D4 = g.head_dim / 4, S = g.seq, G = g.group, R = G * S;
     const uint32_t kvh = blockIdx.x;
     const uint64_t b = blockIdx.y;
-    const uint32_t active = (g.past_len + S + kt - 1) / kt;
-    const uint64_t row_stride = 2 + D;
-    const float* base = g.ws + (b * g.kv_heads + kvh) * g.chunks * R * row_stride;
-    const int tid = threadIdx.x;
-    if (tid < static_cast<int>(R)) {
-        float mx = -INFINITY;
-        for (uint32_t c = 0; c < active; ++c) mx = fmaxf(mx, base[(c * R + tid) * row_stride]);
-        float l = 0.f;
-        for (uint32_t c = 0; c < active; ++c) {
-            const float* pc = base + (c * R + tid) * row_stride;
-            if (pc[1] > 0.f) l += pc[1] * expf(pc[0] - mx);
-        }
-        m_row[tid] = mx;
-        inv_row[tid] = 1.0f / l;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const uint64_t row_stride = kDecodePartStride + 4 * D4;
+    const float* base = g.ws + (b * g.kv_heads + kvh) * P * R * row_stride;
+    for (uint32_t r = wave; r < R; r += 4) {
+        const bool on = static_cast<uint32_t>(lane) < P;
+        const float* pr = base + (static_cast<uint64_t>(on ? lane : 0) * R + r) * row_stride;
+        const float mp = on ? pr[0] : -INFINITY;
+        const float lp = on ? pr[1] : 0.f;
+        const float mx = wave_max(mp);
+        const float e = mp == -INFINITY ? 0.f : expf(mp - mx);
+        const float total = wave_sum(lp * e);
+        if (on) coef[lane][r] = e / total;
     }
     __syncthreads();
-    for (uint32_t e = tid; e < R * D; e += 256) {
-        const uint32_t r = e / D, d = e % D, gi = r / S, t = r % S;
-        float a = 0.f;
-        for (uint32_t c = 0; c < active; ++c) {
-            const float* pc = base + (c * R + r) * row_stride;
-            if (pc[1] > 0.f) a = fmaf(pc[2 + d], expf(pc[0] - m_row[r]), a);
+    const uint32_t slots = R * D4;
+    const uint32_t T = slots >= 256 ? 1 : 256 / slots;  // threads per slot
+    const uint32_t q = tid / slots;
+    for (uint32_t slot = tid % slots; slot < slots; slot += 256) {
+        const uint32_t r = slot / D4, c = slot % D4;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (q < T) {
+            for (uint32_t p0 = q; p0 < P; p0 += 8 * T) {
+                float4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t pp = p0 + u * T;
+                    v[u] = pp < P ? reinterpret_cast<const float4*>(base + (pp * R + r) * row_stride +
+                                                                    kDecodePartStride)[c]
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t pp = p0 + u * T;
+                    if (pp < P) a = f4_fma(coef[pp][r], v[u], a);
+                }
+            }
         }
-        g.out[((b * g.heads + kvh * G + gi) * S + t) * D + d] = a * inv_row[r];
+        if (T > 1) {
+            red[tid] = a;
+            __syncthreads();
+            if (q == 0) {
+                for (uint32_t o = 1; o < T; ++o) {
+                    const float4 x = red[tid + o * slots];
+                    a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
+                }
+            }
+        }
+        if (q == 0 || T == 1) {
+            const uint32_t gi = r / S, t = r % S;
+            reinterpret_cast<float4*>(g.out + ((b * g.heads + kvh * G + gi) * S + t) * (4 * D4))[c] = a;
+        }
     }
 }
 
@@ -333,9 +456,10 @@ __global__ __launch_bounds__(128) void attn_tiled(Geo g) {
     const int r = threadIdx.x / 2, half = threadIdx.x % 2;
     const uint32_t t = blockIdx.x * kTileQ + r;
     const bool valid = t < g.seq;
-    const uint32_t key_count = g.past_len + t + 1;
+    const uint32_t past = past_of(g);
+    const uint32_t key_count = past + t + 1;
     const uint32_t last_t = min(g.seq, (blockIdx.x + 1) * kTileQ) - 1;
-    const uint32_t block_keys = g.past_len + last_t + 1;
+    const uint32_t block_keys = past + last_t + 1;
 
     const uint64_t qrow = ((b * g.heads + h) * g.seq + (valid ? t : 0)) * D + half * H;
     float qv[H], acc[H];
@@ -437,34 +561,41 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
     g.layer_offset = a.layer * 2 * g.parity_stride;
     g.batch_stride = a.layers * 2 * g.parity_stride;
     g.scale = a.scale;
+    g.dyn = a.dyn;
 
-    // Decode path: kv_append fused into the chunk kernel, then the merge.
+    // Decode path: kv_append fused into the tile kernel, then the merge.
     const uint64_t rows = static_cast<uint64_t>(g.group) * a.seq;
-    const uint32_t kt = a.head_dim <= 128 ? 32 : 16;
-    const uint64_t n_chunks = (a.max_seq + kt - 1) / kt;
-    if (rows <= kDecodeRows && a.head_dim <= 256 && n_chunks <= 0xffffffffull &&
-        a.batch * a.kv_heads * n_chunks * rows * (a.head_dim + 2) <= ws.floats) {
-        g.chunks = static_cast<uint32_t>(n_chunks);
-        g.chunk = kt;
-        const bool vec = a.head_dim % 4 == 0 && aligned16(a.q) && aligned16(a.k_new) && aligned16(a.v_new) &&
-                         aligned16(a.cache);
-        dim3 grid(static_cast<unsigned>(n_chunks), g.kv_heads, static_cast<unsigned>(a.batch));
-        const size_t lds = (rows * a.head_dim + 2 * kt * (a.head_dim + 1) + rows * kt) * sizeof(float);
-        if (kt == 32) {
-            if (vec) attn_decode<32, true><<<grid, 256, lds, s>>>(g);
-            else attn_decode<32, false><<<grid, 256, lds, s>>>(g);
-        } else {
-            if (vec) attn_decode<16, true><<<grid, 256, lds, s>>>(g);
-            else attn_decode<16, false><<<grid, 256, lds, s>>>(g);
+    const uint64_t dv = a.head_dim / 64;
+    const uint64_t rt = rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
+    uint64_t parts = (a.max_seq + 127) / 128;
+    if (parts > kMergeMaxParts) parts = kMergeMaxParts;
+    const bool aligned = aligned16(a.q) && aligned16(a.k_new) && aligned16(a.v_new) && aligned16(a.cache) &&
+                         aligned16(a.out);
+    if (rows <= kDecodeMaxRows && a.head_dim % 64 == 0 && dv >= 1 && dv <= 4 && rt * dv <= 32 && aligned &&
+        a.batch * a.kv_heads * parts * rows * (kDecodePartStride + a.head_dim) <= ws.floats) {
+        g.chunks = static_cast<uint32_t>(parts);
+        g.chunk = kDecodeTile;
+        const dim3 grid(static_cast<unsigned>(parts), g.kv_heads, static_cast<unsigned>(a.batch));
+        switch (dv * 100 + rt) {
+            case 104: attn_decode<1, 4><<<grid, 256, 0, s>>>(g); break;
+            case 108: attn_decode<1, 8><<<grid, 256, 0, s>>>(g); break;
+            case 116: attn_decode<1, 16><<<grid, 256, 0, s>>>(g); break;
+            case 204: attn_decode<2, 4><<<grid, 256, 0, s>>>(g); break;
+            case 208: attn_decode<2, 8><<<grid, 256, 0, s>>>(g); break;
+            case 216: attn_decode<2, 16><<<grid, 256, 0, s>>>(g); break;
+            case 304: attn_decode<3, 4><<<grid, 256, 0, s>>>(g); break;
+            case 308: attn_decode<3, 8><<<grid, 256, 0, s>>>(g); break;
+            case 404: attn_decode<4, 4><<<grid, 256, 0, s>>>(g); break;
+            default: attn_decode<4, 8><<<grid, 256, 0, s>>>(g); break;
         }
-        attn_decode_merge<<<dim3(g.kv_heads, static_cast<unsigned>(a.batch)), 256, 0, s>>>(g, kt);
+        attn_decode_merge<<<dim3(g.kv_heads, static_cast<unsigned>(a.batch)), 256, 0, s>>>(
+            g, static_cast<uint32_t>(parts));
         return hipGetLastError();
     }
 
     hipError_t e = launch_kv_append(a.k_new, a.v_new, a.cache, a.batch, a.layers, a.layer, a.kv_heads, a.head_dim,
-                                    a.max_seq, a.past_len, a.seq, s);
+                                    a.max_seq, a.past_len, a.seq, a.dyn, s);
     if (e != hipSuccess) return e;
-    const bool aligned = aligned16(a.q) && aligned16(a.cache) && aligned16(a.out);
     if (a.seq >= 16 && aligned && (a.head_dim == 64 || a.head_dim == 128)) {
         dim3 grid(static_cast<unsigned>((a.seq + kTileQ - 1) / kTileQ), g.heads, static_cast<unsigned>(a.batch));
         if (a.head_dim == 64) attn_tiled<64><<<grid, 128, 0, s>>>(g);
@@ -473,9 +604,11 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
     }
     if (a.head_dim > 256) return hipErrorInvalidValue;
 
-    // Split the longest key range so that about 2048 waves run, each chunk
-    // holding at least 64 keys, within the workspace.
-    const uint64_t max_keys = a.past_len + a.seq;
+    // Split the longest possible key range (max_seq, so the launch does not
+    // depend on past_len) so that about 2048 waves run, each chunk holding
+    // at least 64 keys, within the workspace; chunks past the current length
+    // leave empty partials.
+    const uint64_t max_keys = a.max_seq;
     uint64_t chunks = 1;
     if (queries < 2048) {
         chunks = (2048 + queries - 1) / queries;

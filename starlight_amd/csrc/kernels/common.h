@@ -8,16 +8,58 @@ namespace slhip {
 
 constexpr int kWave = 64;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+// Cross-lane reductions on the DPP network: within each 16-lane row,
+// xor 1 and xor 2 (quad_perm), then the half-row and row mirrors, leave the
+// row's total in every lane of the row (the same bits in each, the
+// operations being commutative); readlane then combines the four rows into
+// a wave-uniform value. No LDS round trips, unlike ds_bpermute shuffles.
+// All 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+__device__ __forceinline__ float row_sum(float v) {
+    v += dpp_f<kDppXor1>(v);
+    v += dpp_f<kDppXor2>(v);
+    v += dpp_f<kDppHalfMirror>(v);
+    v += dpp_f<kDppMirror>(v);
     return v;
+}
+__device__ __forceinline__ int row_sum(int v) {
+    v += dpp_i<kDppXor1>(v);
+    v += dpp_i<kDppXor2>(v);
+    v += dpp_i<kDppHalfMirror>(v);
+    v += dpp_i<kDppMirror>(v);
+    return v;
+}
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    return v;
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    const float r = row_sum(v);
+    return (lane_value(r, 0) + lane_value(r, 16)) + (lane_value(r, 32) + lane_value(r, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
+    const float r = row_max(v);
+    return fmaxf(fmaxf(lane_value(r, 0), lane_value(r, 16)), fmaxf(lane_value(r, 32), lane_value(r, 48)));
 }
 
 // Block-wide sum/max for blocks of up to 1024 threads; every thread gets the
@@ -47,6 +89,35 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Compute units of the current device (all devices of a process are taken
+// to be the same part).
+inline unsigned compute_units() {
+    static unsigned cus = 0;
+    if (cus == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            cus = static_cast<unsigned>(v);
+        else
+            cus = 256;
+    }
+    return cus;
+}
+
+// Largest LDS allocation one workgroup may make on the current device.
+inline size_t max_lds_per_block() {
+    static size_t bytes = 0;
+    if (bytes == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
+            bytes = static_cast<size_t>(v);
+        else
+            bytes = 64 * 1024;
+    }
+    return bytes;
+}
 
 inline unsigned grid_for(uint64_t work, unsigned per_block, unsigned cap) {
     uint64_t g = (work + per_block - 1) / per_block;

@@ -30,6 +30,20 @@ hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef&
     float* g = ws.data;
     float* u = ws.data + u_off;
     const Workspace rest = ws.after(budget);
+    if (rows <= 16 && gate.quantized() && up.quantized()) {
+        // gate and up tiles in one launch with the silu * up epilogue
+        QgemvFused f{};
+        f.a = x;
+        f.w[0] = &gate.quant;
+        f.w[1] = &up.quant;
+        f.out[0] = g;
+        f.nseg = 2;
+        f.m = rows;
+        f.epilogue = kFusedPair;
+        hipError_t e = launch_qgemv_fused(f, s);
+        if (e == hipSuccess) return launch_linear(g, down, out, rows, hidden, inter, rest, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
         const uint64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
         hipError_t e = launch_linear(x + r0 * hidden, gate, g, rc, inter, hidden, rest, s);
@@ -50,6 +64,20 @@ hipError_t launch_rms_norm_matmul(const float* x, const float* weight, const Wei
     if (chunk == 0) return hipErrorOutOfMemory;
     if (chunk > rows) chunk = rows;
     float* y = ws.data;
+    if (rows <= 16 && w.quantized()) {
+        // the normalisation runs as the GEMV's prologue
+        QgemvFused f{};
+        f.a = x;
+        f.gamma = weight;
+        f.eps = eps;
+        f.w[0] = &w.quant;
+        f.out[0] = out;
+        f.nseg = 1;
+        f.m = rows;
+        f.epilogue = kFusedPlain;
+        hipError_t e = launch_qgemv_fused(f, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
         const uint64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
         hipError_t e = launch_rms_norm(x + r0 * hidden, weight, y, rc, hidden, eps, s);

@@ -92,6 +92,31 @@ hipError_t launch_silu(const float* x, float* out, uint64_t n, hipStream_t s) {
 hipError_t launch_silu_mul(const float* g, const float* u, float* h, uint64_t n, hipStream_t s) {
     return launch_ew<Ew::SiluMul>(g, u, h, n, 0.f, s);
 }
+namespace {
+constexpr uint32_t kSetWords = 240;
+struct Words {
+    uint32_t v[kSetWords];
+};
+// dst[i] = w.v[i], i < count: the values travel in the kernel arguments, so
+// the host array may change as soon as the launch returns.
+__global__ void set_words(uint32_t* __restrict__ dst, Words w, uint32_t count) {
+    const uint32_t i = threadIdx.x;
+    if (i < count) dst[i] = w.v[i];
+}
+}  // namespace
+
+hipError_t launch_set_words(uint32_t* dst, const uint32_t* values, uint64_t count, hipStream_t s) {
+    for (uint64_t done = 0; done < count; done += kSetWords) {
+        const uint32_t n = static_cast<uint32_t>(count - done < kSetWords ? count - done : kSetWords);
+        Words w{};
+        for (uint32_t i = 0; i < n; ++i) w.v[i] = values[done + i];
+        set_words<<<1, 256, 0, s>>>(dst + done, w, n);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_fill_zero(float* out, uint64_t n, hipStream_t s) {
     return launch_ew<Ew::Zero>(nullptr, nullptr, out, n, 0.f, s);
 }

@@ -34,11 +34,20 @@ hipError_t launch_scale(const float* x, float* out, uint64_t n, float factor, hi
 hipError_t launch_silu(const float* x, float* out, uint64_t n, hipStream_t s);
 hipError_t launch_fill_zero(float* out, uint64_t n, hipStream_t s);
 
+// dst[0..count) = values, through kernel arguments (no host buffer lifetime,
+// no memset node when captured).
+hipError_t launch_set_words(uint32_t* dst, const uint32_t* values, uint64_t count, hipStream_t s);
+
+// Launchers whose kernels read past_len also take `dyn`: when set, the
+// kernels read past_len from dyn[0] at run time instead of the argument.
+// Their launch geometry never depends on past_len, so a captured launch is
+// valid for any length.
+
 // ---- norm / softmax (reference/norm.rs, reference/softmax.rs) ----
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, uint64_t rows, uint64_t hidden,
                            float eps, hipStream_t s);
 hipError_t launch_softmax(const float* x, float* out, uint64_t rows, uint64_t cols, bool causal,
-                          uint64_t seq, uint64_t past_len, hipStream_t s);
+                          uint64_t seq, uint64_t past_len, const uint32_t* dyn, hipStream_t s);
 
 // ---- rope (reference/rope.rs) ----
 hipError_t launch_rope(const float* x, const uint32_t* positions, float* out, uint64_t batch,
@@ -54,7 +63,8 @@ hipError_t launch_heads_permute(const float* in, float* out, uint64_t batch, uin
                                 uint64_t heads, uint64_t head_dim, bool split, hipStream_t s);
 hipError_t launch_kv_append(const float* k, const float* v, float* cache, uint64_t batch,
                             uint64_t layers, uint64_t layer, uint64_t kv_heads, uint64_t head_dim,
-                            uint64_t max_seq, uint64_t past_len, uint64_t seq, hipStream_t s);
+                            uint64_t max_seq, uint64_t past_len, uint64_t seq, const uint32_t* dyn,
+                            hipStream_t s);
 
 // ---- attention (reference/attention.rs causal_attention, kv_append included) ----
 struct AttentionArgs {
@@ -65,6 +75,7 @@ struct AttentionArgs {
     float* out;
     uint64_t batch, layers, layer, heads, kv_heads, seq, past_len, head_dim, max_seq;
     float scale;
+    const uint32_t* dyn;  // device copy of past_len read by the kernels, or null
 };
 // Appends k_new / v_new to the cache and computes the attention output.
 hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStream_t s);
@@ -86,12 +97,19 @@ struct QuantWeight {
     uint32_t group;
     uint64_t n, k;
     QuantLayout layout;
+    const float* tile_scales;  // Mfma: scales in wave order (quant_tile_scale_floats), else null
 };
 QuantLayout quant_layout_for(uint32_t format, uint64_t n, uint64_t k, uint32_t group);
 uint64_t quant_tile_bytes(uint32_t format, uint64_t n, uint64_t k, QuantLayout layout);
 // Builds the private copy from the row-major payload.
 hipError_t launch_quant_repack(const uint8_t* payload, uint8_t* tiles, uint32_t format, uint64_t n,
                                uint64_t k, QuantLayout layout, hipStream_t s);
+// Scales in wave order for the Mfma layout: [ceil(n/16)][k/128][16][gps]
+// with gps = 2 for group 64 (both groups of a superblock), else 1 (the group
+// containing the superblock); rows past n zero.
+uint64_t quant_tile_scale_floats(uint64_t n, uint64_t k, uint32_t group, QuantLayout layout);
+hipError_t launch_scale_repack(const float* scales, float* tile_scales, uint64_t n, uint64_t k, uint32_t group,
+                               hipStream_t s);
 // out[m, n] = sum_k a[m, k] * dequant(w)[n, k]  (a: [m, k] row-major)
 hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
                           hipStream_t s);
@@ -101,6 +119,30 @@ hipError_t launch_qgemv_mfma(const float* a, const QuantWeight& w, float* out, u
                              hipStream_t s);
 
 // ---- composites ----
+// Decode GEMV with the K reduction inside one workgroup and its fusions
+// (qgemv_fused.hip). Needs QuantLayout::Mfma weights of one format, group
+// and k, m <= 16, m * k <= 16384, k % 256 == 0, group 64/128/256 or a
+// multiple of 256, 16-byte aligned a / gamma / normed; otherwise returns
+// hipErrorNotSupported before launching anything.
+constexpr uint32_t kFusedMaxSegs = 3;
+constexpr uint32_t kFusedPlain = 0;     // out[i] = a x w[i]^T
+constexpr uint32_t kFusedResidual = 1;  // ... and out2[i] = resid[i] + out[i]
+constexpr uint32_t kFusedPair = 2;      // out[0] = silu(a x w[0]^T) * (a x w[1]^T)
+struct QgemvFused {
+    const float* a;       // [m, k]
+    const float* gamma;   // RMSNorm weight [k] applied to a first, or null
+    float* normed;        // where the normalised a is written (gamma set), or null
+    float eps;
+    const QuantWeight* w[kFusedMaxSegs];
+    float* out[kFusedMaxSegs];
+    const float* resid[kFusedMaxSegs];
+    float* out2[kFusedMaxSegs];
+    uint32_t nseg;
+    uint64_t m;
+    uint32_t epilogue;
+};
+hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s);
+
 // Weights are dense f32 (pointer) or quantized (QuantWeight with tiles != null).
 struct WeightRef {
     const float* dense;

@@ -71,7 +71,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
                                                         float* __restrict__ cache, uint64_t kv_heads,
                                                         uint64_t head_dim, uint64_t seq, uint64_t batch_stride,
                                                         uint64_t layer_offset, uint64_t parity_stride,
-                                                        uint64_t past_len, uint64_t total) {
+                                                        uint64_t past_len, const uint32_t* __restrict__ dyn,
+                                                        uint64_t total) {
+    if (dyn != nullptr) past_len = dyn[0];
     const uint64_t dv = head_dim / VEC;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
@@ -129,7 +131,8 @@ hipError_t launch_heads_permute(const float* in, float* out, uint64_t batch, uin
 
 hipError_t launch_kv_append(const float* k, const float* v, float* cache, uint64_t batch,
                             uint64_t layers, uint64_t layer, uint64_t kv_heads, uint64_t head_dim,
-                            uint64_t max_seq, uint64_t past_len, uint64_t seq, hipStream_t s) {
+                            uint64_t max_seq, uint64_t past_len, uint64_t seq, const uint32_t* dyn,
+                            hipStream_t s) {
     const uint64_t elements = batch * kv_heads * seq * head_dim;
     if (elements == 0) return hipSuccess;
     const uint64_t parity_stride = max_seq * kv_heads * head_dim;
@@ -140,10 +143,10 @@ hipError_t launch_kv_append(const float* k, const float* v, float* cache, uint64
     const unsigned grid = grid_for(total, 256, 256 * 8);
     if (vec)
         kv_append_kernel<4><<<grid, 256, 0, s>>>(k, v, cache, kv_heads, head_dim, seq, batch_stride,
-                                                 layer * layer_stride, parity_stride, past_len, total);
+                                                 layer * layer_stride, parity_stride, past_len, dyn, total);
     else
         kv_append_kernel<1><<<grid, 256, 0, s>>>(k, v, cache, kv_heads, head_dim, seq, batch_stride,
-                                                 layer * layer_stride, parity_stride, past_len, total);
+                                                 layer * layer_stride, parity_stride, past_len, dyn, total);
     return hipGetLastError();
 }
 

@@ -66,9 +66,11 @@ __global__ __launch_bounds__(256) void rms_norm_any(const float* __restrict__ x,
 // Softmax with the row in registers: up to 256 * VPT columns.
 template <int VPT, bool CAUSAL>
 __global__ __launch_bounds__(256) void softmax_regs(const float* __restrict__ x, float* __restrict__ out,
-                                                    uint32_t cols, uint32_t seq, uint32_t past_len) {
+                                                    uint32_t cols, uint32_t seq, uint32_t past_len,
+                                                    const uint32_t* __restrict__ dyn) {
     __shared__ float scratch[4];
     const uint64_t row = blockIdx.x;
+    if (CAUSAL && dyn != nullptr) past_len = dyn[0];
     const uint32_t visible = CAUSAL ? past_len + static_cast<uint32_t>(row % seq) + 1u : cols;
     const float* xr = x + row * cols;
     float v[VPT];
@@ -100,9 +102,11 @@ __global__ __launch_bounds__(256) void softmax_regs(const float* __restrict__ x,
 // General softmax: three passes over the row for very wide rows.
 template <bool CAUSAL>
 __global__ __launch_bounds__(256) void softmax_any(const float* __restrict__ x, float* __restrict__ out,
-                                                   uint64_t cols, uint64_t seq, uint64_t past_len) {
+                                                   uint64_t cols, uint64_t seq, uint64_t past_len,
+                                                   const uint32_t* __restrict__ dyn) {
     __shared__ float scratch[4];
     const uint64_t row = blockIdx.x;
+    if (CAUSAL && dyn != nullptr) past_len = dyn[0];
     const uint64_t visible = CAUSAL ? past_len + row % seq + 1 : cols;
     const float* xr = x + row * cols;
     float* orow = out + row * cols;
@@ -139,7 +143,7 @@ hipError_t launch_rms_norm(const float* x, const float* w, float* out, uint64_t 
 }
 
 hipError_t launch_softmax(const float* x, float* out, uint64_t rows, uint64_t cols, bool causal,
-                          uint64_t seq, uint64_t past_len, hipStream_t s) {
+                          uint64_t seq, uint64_t past_len, const uint32_t* dyn, hipStream_t s) {
     if (rows == 0) return hipSuccess;
     const unsigned g = static_cast<unsigned>(rows);
     const uint32_t c = static_cast<uint32_t>(cols), q = static_cast<uint32_t>(seq),
@@ -147,8 +151,8 @@ hipError_t launch_softmax(const float* x, float* out, uint64_t rows, uint64_t co
     if (cols <= 256 * 16) {
 #define SL_SOFTMAX(V)                                                              \
     do {                                                                           \
-        if (causal) softmax_regs<V, true><<<g, 256, 0, s>>>(x, out, c, q, p);      \
-        else softmax_regs<V, false><<<g, 256, 0, s>>>(x, out, c, q, p);            \
+        if (causal) softmax_regs<V, true><<<g, 256, 0, s>>>(x, out, c, q, p, dyn); \
+        else softmax_regs<V, false><<<g, 256, 0, s>>>(x, out, c, q, p, dyn);       \
         return hipGetLastError();                                                  \
     } while (0)
         if (cols <= 256) SL_SOFTMAX(1);
@@ -158,8 +162,8 @@ hipError_t launch_softmax(const float* x, float* out, uint64_t rows, uint64_t co
         SL_SOFTMAX(16);
 #undef SL_SOFTMAX
     }
-    if (causal) softmax_any<true><<<g, 256, 0, s>>>(x, out, cols, seq, past_len);
-    else softmax_any<false><<<g, 256, 0, s>>>(x, out, cols, seq, past_len);
+    if (causal) softmax_any<true><<<g, 256, 0, s>>>(x, out, cols, seq, past_len, dyn);
+    else softmax_any<false><<<g, 256, 0, s>>>(x, out, cols, seq, past_len, dyn);
     return hipGetLastError();
 }
 

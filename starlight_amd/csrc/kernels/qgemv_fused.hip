@@ -1,0 +1,457 @@
+// Group-quantized GEMV for decode (m <= 16 activation rows, m * k <= 16384)
+// with the K reduction kept inside one workgroup, and the fusions a decoder
+// layer wants around it.
+//
+// Arithmetic is the int8-limb MFMA scheme of qgemv_mfma.hip (exact integer
+// products, one f32 combination per group; the weight tiles are the same
+// QuantLayout::Mfma superblocks). What differs is the work split:
+//  * a block of 8 waves owns one 16-row tile (or, for a gate/up pair, one
+//    tile of each with 4 waves apiece) and the whole K range; its waves take
+//    contiguous, group-aligned runs of superblocks and start their weight
+//    and scale loads (6 INT4 / 4 INT8 superblocks, rolling) before the
+//    activation prologue, then add their partial sums in LDS in wave order.
+//    No split partials in HBM, no second launch, deterministic. Blocks stay
+//    resident over several tiles (at most two per CU), so the prologue is
+//    paid once per block, and the per-tile LDS sums are double-buffered;
+//  * the activations are converted once per block from registers: every
+//    thread holds its share of the m x k input as float4, the per-row
+//    reductions (sum of squares, max |x|) go wave -> LDS -> one wave per row;
+//  * up to three weights that read the same input run as one launch (q/k/v);
+//  * prologue RMSNorm: x = (a * inv) * gamma with inv = 1/sqrt(ss/k + eps)
+//    (reference/norm.rs:27-60), block 0 also writes x as the norm's output;
+//  * epilogues: plain; residual (out2 = resid + out, reference/add.rs); pair
+//    (h = silu(g) * u over a gate and an up tile, reference/swiglu.rs:40-84).
+#include "common.h"
+#include "kernels.h"
+#include "starlight_hip.h"
+
+namespace slhip {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxF4 = 8;  // float4 of activations per thread
+constexpr uint32_t kMaxElems = kThreads * 4 * kMaxF4;
+// static LDS of the kernel: red, row_val, exps, wres
+constexpr size_t kStaticLds = sizeof(float) * (kMaxF4 * kWaves + 16 + 16 + 2 * kWaves * 16 * 16);
+
+struct Seg {
+    const uint8_t* tiles;
+    const float* tscales;  // [tile][group][16]
+    float* out;
+    const float* resid;
+    float* out2;
+    uint32_t n, tile0;
+};
+
+struct Args {
+    const float* a;
+    const float* gamma;
+    float* normed;
+    float eps;
+    Seg seg[kFusedMaxSegs];
+    uint32_t nseg;
+    uint32_t m, k, group, sb_total, groups_total, sb_per_wave;
+    uint32_t tiles_total;  // block tiles (pair mode: gate tiles)
+    uint32_t epilogue;
+};
+
+// One weight superblock of a wave's stream: codes (16 bytes per lane, INT8
+// two loads) and the scales of its groups for the lane's row.
+template <int BITS>
+struct Item {
+    uint4 c0, c1;
+    float s0, s1;
+};
+
+template <int BITS, int NT, int GPS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(Args p) {
+    constexpr int PF = BITS == 4 ? 6 : 4;  // superblocks in flight per wave
+    constexpr int WPT = kWaves / NT;  // waves per tile
+    constexpr uint32_t SB_BYTES = BITS == 4 ? 1024 : 2048;
+    extern __shared__ __align__(16) int8_t limbs[];  // [3][m][k], xsum [m][groups], tres [tiles][16][m]
+    __shared__ float red[kMaxF4][kWaves];
+    __shared__ float row_val[16];
+    __shared__ int exps[16];
+    __shared__ float wres[2][kWaves][16][16];
+
+    const int tid = threadIdx.x, lane = tid % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, kept in scalar registers
+    const uint32_t M = p.m, K = p.k, K4 = K / 4;
+    int* xsum = reinterpret_cast<int*>(limbs + 3 * M * K);
+    float* tres = reinterpret_cast<float*>(xsum + M * p.groups_total);
+
+    // ---- this wave's stream: for each block tile j (global tile
+    // blockIdx.x + j * gridDim.x) the superblocks [sbA, sbA + len); every
+    // wave has the same item count, so the per-tile barriers line up ----
+    const int slot = wave / WPT, wi = wave % WPT;
+    const uint32_t len = p.sb_per_wave;
+    const uint32_t sbA = wi * len;
+    const uint32_t my_tiles =
+        p.tiles_total > blockIdx.x ? (p.tiles_total - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    const uint32_t items = my_tiles * len;
+    constexpr uint32_t gps = GPS;  // groups per superblock: 2 for group 64, else 1
+
+    // Segment fields are read by constant index and chosen with selects: a
+    // runtime index into the argument block (or a struct copy) would turn
+    // every access into a dependent memory load.
+    auto seg_of = [&](uint32_t t, uint32_t& tile) -> uint32_t {
+        uint32_t si;
+        if (NT == 1) {
+            si = (p.nseg > 1 && t >= p.seg[1].tile0 ? 1u : 0u) + (p.nseg > 2 && t >= p.seg[2].tile0 ? 1u : 0u);
+            tile = t - (si == 0 ? 0u : si == 1 ? p.seg[1].tile0 : p.seg[2].tile0);
+        } else {
+            si = static_cast<uint32_t>(slot);
+            tile = t;
+        }
+        return si;
+    };
+#define SEG_FIELD(si, f) ((si) == 0 ? p.seg[0].f : (si) == 1 ? p.seg[1].f : p.seg[2].f)
+    // The stream is walked with cursors: the segment, tile and base address
+    // are resolved once per tile and the addresses advance by a constant per
+    // superblock, keeping the shared scalar unit's work per item small.
+    // Every item issues the same loads (the dead superblocks of a trailing
+    // wave re-read its last live one), so each wait is for one item only.
+    const uint32_t nlive = sbA < p.sb_total ? min(len, p.sb_total - sbA) : 0;
+    const uint32_t sb0 = min(sbA, p.sb_total - 1);
+    auto tile_base = [&](uint32_t j, const uint8_t*& wp, const float*& sp) {
+        uint32_t tile;
+        const uint32_t si = seg_of(blockIdx.x + j * gridDim.x, tile);
+        const uint64_t ts = static_cast<uint64_t>(tile) * p.sb_total + sb0;
+        wp = SEG_FIELD(si, tiles) + ts * SB_BYTES;
+        sp = SEG_FIELD(si, tscales) + ts * 16 * gps;
+    };
+    uint32_t pj = 0, pq = 0;  // block tile and position of the next item to fetch
+    bool pdone = false;       // the stream's last item has been fetched: stay on it
+    const uint8_t* pw;
+    const float* ps;
+    tile_base(0, pw, ps);
+    auto fetch_next = [&](Item<BITS>& it) {
+        const uint8_t* wp = pw + lane * 16;
+        it.c0 = *reinterpret_cast<const uint4*>(wp);
+        if constexpr (BITS == 8) it.c1 = *reinterpret_cast<const uint4*>(wp + 1024);
+        const float* sp = ps + (lane % 16) * gps;
+        if constexpr (GPS == 2) {
+            const float2 s2 = *reinterpret_cast<const float2*>(sp);
+            it.s0 = s2.x;
+            it.s1 = s2.y;
+        } else {
+            it.s0 = sp[0];
+            it.s1 = it.s0;
+        }
+        // The window fetches PF items past the stream's end; those re-read
+        // the last item, so the cursor never leaves this wave's last tile.
+        if (pdone) return;
+        if (++pq == len) {
+            pq = 0;
+            if (pj + 1 < my_tiles) tile_base(++pj, pw, ps);
+            else pdone = true;
+        } else if (pq < nlive) {
+            pw += SB_BYTES;
+            ps += 16 * gps;
+        }
+    };
+
+    // ---- activations first (the prologue waits for them only), then the
+    // weight window: element float4 f = tid + kThreads * u of [m][k/4] ----
+    const uint32_t total4 = M * K4;
+    float4 v[kMaxF4], gv[kMaxF4];
+#pragma unroll
+    for (int u = 0; u < kMaxF4; ++u) {
+        const uint32_t f = min(tid + kThreads * u, total4 - 1);
+        v[u] = reinterpret_cast<const float4*>(p.a)[f];
+        if (p.gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(p.gamma)[f % K4];
+    }
+    Item<BITS> win[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) fetch_next(win[i]);
+#pragma unroll
+    for (int u = 0; u < kMaxF4; ++u)
+        if (tid + kThreads * u >= total4) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t i = tid; i < M * p.groups_total; i += kThreads) xsum[i] = 0;
+
+    // Row of the wave-uniform run (u, wave): k % 256 == 0 keeps a wave's 64
+    // float4 inside one row. Each wave reduces the rows w, w + 8 over the
+    // (u, wave) partials in a fixed order.
+    auto row_reduce = [&](bool is_max) {
+        __syncthreads();
+        for (uint32_t r = wave; r < M; r += kWaves) {
+            float x = 0.f;
+            const int u = lane / kWaves, w = lane % kWaves;
+            const uint32_t fb = static_cast<uint32_t>(w) * kWave + kThreads * u;
+            if (fb < total4 && fb / K4 == r) x = red[u][w];
+            x = is_max ? wave_max(x) : wave_sum(x);
+            if (lane == 0) row_val[r] = x;
+        }
+        __syncthreads();
+    };
+
+    if (p.gamma != nullptr) {
+#pragma unroll
+        for (int u = 0; u < kMaxF4; ++u) {
+            float ss = 0.f;
+            ss = fmaf(v[u].x, v[u].x, ss);
+            ss = fmaf(v[u].y, v[u].y, ss);
+            ss = fmaf(v[u].z, v[u].z, ss);
+            ss = fmaf(v[u].w, v[u].w, ss);
+            ss = wave_sum(ss);
+            if (lane == 0) red[u][wave] = ss;
+        }
+        row_reduce(false);
+        const float kf = static_cast<float>(K);
+#pragma unroll
+        for (int u = 0; u < kMaxF4; ++u) {
+            const uint32_t f = tid + kThreads * u;
+            if (f < total4) {
+                const float inv = 1.0f / sqrtf(row_val[f / K4] / kf + p.eps);
+                const float4 g = gv[u];
+                v[u].x = (v[u].x * inv) * g.x;
+                v[u].y = (v[u].y * inv) * g.y;
+                v[u].z = (v[u].z * inv) * g.z;
+                v[u].w = (v[u].w * inv) * g.w;
+                if (blockIdx.x == 0 && p.normed != nullptr) reinterpret_cast<float4*>(p.normed)[f] = v[u];
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kMaxF4; ++u) {
+        float mx = fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w)));
+        mx = wave_max(mx);
+        if (lane == 0) red[u][wave] = mx;
+    }
+    row_reduce(true);
+    if (tid < 16) {
+        int e = 0;
+        if (tid < static_cast<int>(M) && row_val[tid] != 0.f) frexpf(row_val[tid], &e);
+        exps[tid] = e;  // max|x| < 2^e
+    }
+    __syncthreads();
+
+    // exact integers X = rint(x * 2^(22-E)) as three signed int8 limbs
+    const int seg_lanes = p.group / 4 < kWave ? static_cast<int>(p.group / 4) : kWave;
+#pragma unroll
+    for (int u = 0; u < kMaxF4; ++u) {
+        const uint32_t fb = static_cast<uint32_t>(wave) * kWave + kThreads * u;
+        if (fb >= total4) continue;  // whole wave past the end
+        const uint32_t f = tid + kThreads * u;
+        const uint32_t r = f / K4, c4 = f % K4;
+        const int shift = 22 - exps[r];
+        const float xe[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        uint32_t packed[3] = {0u, 0u, 0u};
+        int sx = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int X = static_cast<int>(rintf(ldexpf(xe[e], shift)));
+            const int l0 = ((X + 128) & 255) - 128;
+            const int x1 = (X - l0) >> 8;
+            const int l1 = ((x1 + 128) & 255) - 128;
+            const int l2 = (x1 - l1) >> 8;
+            packed[0] |= (static_cast<uint32_t>(l0) & 0xFFu) << (8 * e);
+            packed[1] |= (static_cast<uint32_t>(l1) & 0xFFu) << (8 * e);
+            packed[2] |= (static_cast<uint32_t>(l2) & 0xFFu) << (8 * e);
+            sx += X;
+        }
+#pragma unroll
+        for (int limb = 0; limb < 3; ++limb)
+            *reinterpret_cast<uint32_t*>(limbs + (limb * M + r) * K + 4 * c4) = packed[limb];
+        if (BITS == 4) {
+            // group sums of X: a group covers 16, 32 or 64 lanes (one, two
+            // or four DPP rows)
+            const int rs = row_sum(sx);
+            const int r0 = __builtin_amdgcn_readlane(rs, 0), r1 = __builtin_amdgcn_readlane(rs, 16);
+            const int r2 = __builtin_amdgcn_readlane(rs, 32), r3 = __builtin_amdgcn_readlane(rs, 48);
+            const int gsum = seg_lanes == 16 ? rs : seg_lanes == 32 ? (lane < 32 ? r0 + r1 : r2 + r3) : r0 + r1 + r2 + r3;
+            if (lane % seg_lanes == 0) atomicAdd(&xsum[r * p.groups_total + (4 * c4) / p.group], gsum);
+        }
+    }
+    __syncthreads();
+
+    // ---- main loop over the stream ----
+    const uint32_t kb4 = lane / 16;
+    const uint32_t am = min(static_cast<uint32_t>(lane % 16), M - 1);  // rows past M repeat row M - 1, unused
+    const uint32_t rm = M < 4 ? M : 4;                                 // accumulator rows worth finishing
+    const uint32_t steps_per_group = p.group / 64;
+    const uint32_t g_start = sbA * 128 / p.group;
+    const v4i zero = {0, 0, 0, 0};
+    float total[4] = {0.f, 0.f, 0.f, 0.f};
+    // integer sums of the current group (a group may span superblocks; the
+    // wave runs are group-aligned, so a group never spans two runs)
+    v4i acc0 = zero, acc1 = zero, acc2 = zero;
+    uint32_t cj = 0, q = 0;               // block tile and position of the item being consumed
+    uint32_t gstep = 0, gi = g_start;     // 64-k steps into the current group, its index
+    const int8_t* a_row = limbs + am * K + sbA * 128 + kb4 * 16;
+    for (uint32_t base = 0; base < items; base += PF) {
+#pragma unroll
+        for (int s = 0; s < PF; ++s) {
+            const uint32_t i = base + s;
+            if (i >= items) break;
+            const Item<BITS> cur = win[s];
+            fetch_next(win[s]);
+            const uint32_t j = cj;
+            if (q < nlive) {
+                const int8_t* ap = a_row + q * 128;
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    v4i bv;
+                    if (BITS == 4) {
+                        const uint32_t wa = st == 0 ? cur.c0.x : cur.c0.z;
+                        const uint32_t wb = st == 0 ? cur.c0.y : cur.c0.w;
+                        bv[0] = static_cast<int>(wa & 0x0F0F0F0Fu);
+                        bv[1] = static_cast<int>((wa >> 4) & 0x0F0F0F0Fu);
+                        bv[2] = static_cast<int>(wb & 0x0F0F0F0Fu);
+                        bv[3] = static_cast<int>((wb >> 4) & 0x0F0F0F0Fu);
+                    } else {
+                        const uint4 cw = st == 0 ? cur.c0 : cur.c1;
+                        bv[0] = static_cast<int>(cw.x);
+                        bv[1] = static_cast<int>(cw.y);
+                        bv[2] = static_cast<int>(cw.z);
+                        bv[3] = static_cast<int>(cw.w);
+                    }
+                    const v4i a0 = *reinterpret_cast<const v4i*>(ap + st * 64);
+                    const v4i a1 = *reinterpret_cast<const v4i*>(ap + M * K + st * 64);
+                    const v4i a2 = *reinterpret_cast<const v4i*>(ap + 2 * M * K + st * 64);
+                    acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bv, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bv, acc1, 0, 0, 0);
+                    acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bv, acc2, 0, 0, 0);
+                    if (++gstep == steps_per_group) {
+                        gstep = 0;
+                        const float sc = st == 1 ? cur.s1 : cur.s0;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if (static_cast<uint32_t>(r) >= rm) continue;
+                            const uint32_t m = min(kb4 * 4 + r, M - 1);
+                            float val = fmaf(static_cast<float>(acc2[r]), 65536.0f,
+                                             fmaf(static_cast<float>(acc1[r]), 256.0f, static_cast<float>(acc0[r])));
+                            if (BITS == 4) val -= 8.0f * static_cast<float>(xsum[m * p.groups_total + gi]);
+                            total[r] = fmaf(val, sc, total[r]);
+                        }
+                        ++gi;
+                        acc0 = zero;
+                        acc1 = zero;
+                        acc2 = zero;
+                    }
+                }
+            }
+            if (++q == len) {
+                q = 0;
+                ++cj;
+                gi = g_start;
+                // tile j done: wave partials -> LDS, summed in wave order
+                // into the block's result area (global writes wait until the
+                // stream is done, so the loop issues only the window's loads)
+                const uint32_t buf = j & 1;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    wres[buf][wave][kb4 * 4 + r][lane % 16] = total[r];
+                    total[r] = 0.f;
+                }
+                __syncthreads();
+                if (static_cast<uint32_t>(tid) < 16 * M) {
+                    const uint32_t m = tid / 16, col = tid % 16;
+                    float val;
+                    if (NT == 1) {
+                        float acc = 0.f;
+#pragma unroll
+                        for (int w = 0; w < kWaves; ++w) acc += wres[buf][w][m][col];
+                        val = ldexpf(acc, exps[m] - 22);
+                    } else {
+                        float g = 0.f, up = 0.f;
+#pragma unroll
+                        for (int w = 0; w < WPT; ++w) {
+                            g += wres[buf][w][m][col];
+                            up += wres[buf][WPT + w][m][col];
+                        }
+                        g = ldexpf(g, exps[m] - 22);
+                        up = ldexpf(up, exps[m] - 22);
+                        val = (g * (1.0f / (1.0f + expf(-g)))) * up;
+                    }
+                    tres[(j * 16 + col) * M + m] = val;
+                }
+            }
+        }
+    }
+
+    // ---- results of all the block's tiles ----
+    __syncthreads();
+    for (uint32_t e = tid; e < my_tiles * 16 * M; e += kThreads) {
+        const uint32_t j = e / (16 * M), col = (e / M) % 16, m = e % M;
+        uint32_t tile = blockIdx.x + j * gridDim.x, si = 0;
+        if (NT == 1) si = seg_of(tile, tile);
+        const uint32_t sn = SEG_FIELD(si, n);
+        const uint32_t orow = tile * 16 + col;
+        if (orow >= sn) continue;
+        const float val = tres[e];
+        const uint64_t o = static_cast<uint64_t>(m) * sn + orow;
+        SEG_FIELD(si, out)[o] = val;
+        if (p.epilogue == kFusedResidual) SEG_FIELD(si, out2)[o] = SEG_FIELD(si, resid)[o] + val;
+    }
+}
+#undef SEG_FIELD
+
+}  // namespace
+
+hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
+    if (f.nseg == 0 || f.nseg > kFusedMaxSegs || f.m == 0 || f.m > 16) return hipErrorNotSupported;
+    const QuantWeight& w0 = *f.w[0];
+    const uint64_t k = w0.k;
+    if (w0.layout != QuantLayout::Mfma || k % 256 != 0 || w0.group % 64 != 0 || k % w0.group != 0 ||
+        !(w0.group == 64 || w0.group == 128 || w0.group % 256 == 0) || f.m * k > kMaxElems || !aligned16(f.a) || (f.gamma != nullptr && !aligned16(f.gamma)) ||
+        (f.normed != nullptr && !aligned16(f.normed)))
+        return hipErrorNotSupported;
+    if (f.epilogue == kFusedPair && f.nseg != 2) return hipErrorNotSupported;
+    Args p;
+    p.a = f.a;
+    p.gamma = f.gamma;
+    p.normed = f.normed;
+    p.eps = f.eps;
+    p.nseg = f.nseg;
+    p.m = static_cast<uint32_t>(f.m);
+    p.k = static_cast<uint32_t>(k);
+    p.group = w0.group;
+    p.sb_total = p.k / 128;
+    p.groups_total = p.k / p.group;
+    p.epilogue = f.epilogue;
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < f.nseg; ++i) {
+        const QuantWeight& w = *f.w[i];
+        if (w.layout != QuantLayout::Mfma || w.tile_scales == nullptr || w.k != k || w.group != w0.group ||
+            w.format != w0.format || w.n > 0xffffffffull)
+            return hipErrorNotSupported;
+        if (f.epilogue == kFusedPair && w.n != w0.n) return hipErrorNotSupported;
+        p.seg[i] = Seg{w.tiles, w.tile_scales, f.out[i], f.resid[i], f.out2[i], static_cast<uint32_t>(w.n), tiles};
+        if (f.epilogue != kFusedPair) tiles += static_cast<uint32_t>((w.n + 15) / 16);
+    }
+    if (f.epilogue == kFusedPair) tiles = static_cast<uint32_t>((w0.n + 15) / 16);
+    p.tiles_total = tiles;
+    const uint32_t wpt = f.epilogue == kFusedPair ? kWaves / 2 : kWaves;
+    const uint32_t sb_per_group = p.group >= 128 ? p.group / 128 : 1;
+    uint32_t per = (p.sb_total + wpt - 1) / wpt;
+    per = (per + sb_per_group - 1) / sb_per_group * sb_per_group;
+    p.sb_per_wave = per;
+    // Resident blocks: the tiles are dealt evenly over at most two blocks
+    // per CU, so every block converts the activations once for all its
+    // tiles; the results of a block's tiles wait in LDS (at most 16 KB).
+    const uint32_t max_blocks = 2 * compute_units();
+    uint32_t per_block = (tiles + max_blocks - 1) / max_blocks;
+    const uint32_t per_cap = 4096 / (16 * p.m);
+    if (per_block > per_cap) per_block = per_cap;
+    const uint32_t blocks = (tiles + per_block - 1) / per_block;
+    const size_t lds = static_cast<size_t>(3) * p.m * p.k + sizeof(int) * p.m * p.groups_total +
+                       sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m;
+    if (lds + kStaticLds > max_lds_per_block()) return hipErrorNotSupported;
+    const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, g64 = p.group == 64;
+#define SL_QGEMV_FUSED(B, T, G) qgemv_fused<B, T, G><<<blocks, kThreads, lds, s>>>(p)
+    if (int4) {
+        if (pair) g64 ? SL_QGEMV_FUSED(4, 2, 2) : SL_QGEMV_FUSED(4, 2, 1);
+        else g64 ? SL_QGEMV_FUSED(4, 1, 2) : SL_QGEMV_FUSED(4, 1, 1);
+    } else {
+        if (pair) g64 ? SL_QGEMV_FUSED(8, 2, 2) : SL_QGEMV_FUSED(8, 2, 1);
+        else g64 ? SL_QGEMV_FUSED(8, 1, 2) : SL_QGEMV_FUSED(8, 1, 1);
+    }
+#undef SL_QGEMV_FUSED
+    return hipGetLastError();
+}
+
+}  // namespace slhip

@@ -268,6 +268,22 @@ __global__ __launch_bounds__(256) void qgemm_tiled(const float* __restrict__ a, 
     }
 }
 
+// Scales per 128-k superblock of each 16-row tile, in the order a wave reads
+// them: tile_scales[((tile * sb_total + sb) * 16 + r) * gps + j] is the scale
+// of row 16 * tile + r for the j-th group of superblock sb (gps = 2 groups
+// per superblock for group 64, else 1 and the group containing sb).
+__global__ void scale_repack(const float* __restrict__ scales, float* __restrict__ tile_scales, uint64_t n,
+                             uint64_t groups, uint64_t sb_total, uint32_t group, uint32_t gps, uint64_t total) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const uint64_t j = i % gps, r = (i / gps) % 16, sb = (i / (16 * gps)) % sb_total;
+        const uint64_t tile = i / (16 * gps * sb_total);
+        const uint64_t row = tile * 16 + r;
+        const uint64_t g = group <= 128 ? sb * gps + j : sb * 128 / group;
+        tile_scales[i] = row < n ? scales[row * groups + g] : 0.f;
+    }
+}
+
 }  // namespace
 
 QuantLayout quant_layout_for(uint32_t format, uint64_t n, uint64_t k, uint32_t group) {
@@ -299,6 +315,22 @@ hipError_t launch_quant_repack(const uint8_t* payload, uint8_t* tiles, uint32_t 
     return hipGetLastError();
 }
 
+uint64_t quant_tile_scale_floats(uint64_t n, uint64_t k, uint32_t group, QuantLayout layout) {
+    if (layout != QuantLayout::Mfma || group == 0) return 0;
+    const uint64_t gps = group < 128 ? 128 / group : 1;
+    return (n + 15) / 16 * (k / 128) * 16 * gps;
+}
+
+hipError_t launch_scale_repack(const float* scales, float* tile_scales, uint64_t n, uint64_t k, uint32_t group,
+                               hipStream_t s) {
+    const uint64_t total = quant_tile_scale_floats(n, k, group, QuantLayout::Mfma);
+    if (total == 0) return hipSuccess;
+    const uint32_t gps = group < 128 ? 128 / group : 1;
+    scale_repack<<<grid_for(total, 256, 256 * 64), 256, 0, s>>>(scales, tile_scales, n, k / group, k / 128, group,
+                                                                gps, total);
+    return hipGetLastError();
+}
+
 hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
                           hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
@@ -306,7 +338,16 @@ hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint
     const uint32_t bits = w.format == SL_QFORMAT_INT4 ? 4 : 8;
     const bool mfma = w.layout == QuantLayout::Mfma;
     if (mfma && m <= 16 && aligned16(a)) {
-        hipError_t e = launch_qgemv_mfma(a, w, out, m, ws, s);
+        QgemvFused f{};
+        f.a = a;
+        f.w[0] = &w;
+        f.out[0] = out;
+        f.nseg = 1;
+        f.m = m;
+        f.epilogue = kFusedPlain;
+        hipError_t e = launch_qgemv_fused(f, s);
+        if (e != hipErrorNotSupported) return e;
+        e = launch_qgemv_mfma(a, w, out, m, ws, s);
         if (e != hipErrorNotSupported) return e;
         (void)hipGetLastError();
     }

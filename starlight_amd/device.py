@@ -113,6 +113,19 @@ class DeviceError(Exception):
 
 _lib = None
 
+OPT_FUSION = 1
+OPT_GRAPHS = 2
+
+
+class HipStats(ctypes.Structure):
+    """sl_hip_stats: counters of the submission machinery."""
+    _fields_ = [("submissions", ctypes.c_uint64), ("commands", ctypes.c_uint64),
+                ("fused_commands", ctypes.c_uint64), ("graph_captures", ctypes.c_uint64),
+                ("graph_replays", ctypes.c_uint64)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
 
 def exported_symbols() -> list:
     """Every `sl_hip_*` function the public header declares."""
@@ -158,6 +171,9 @@ def load_library() -> ctypes.CDLL:
                                       ctypes.POINTER(ir.CError)], ctypes.c_int),
         "sl_hip_capabilities": ([ctypes.POINTER(ir.CCapabilities)], None),
         "sl_hip_stream": ([P], ctypes.c_void_p),
+        "sl_hip_submit": ([P], ctypes.c_int),
+        "sl_hip_set_options": ([P, ctypes.c_uint32], ctypes.c_int),
+        "sl_hip_get_stats": ([P, ctypes.POINTER(HipStats)], None),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -265,6 +281,20 @@ class HipDevice:
 
     def synchronize(self) -> None:
         self._check(self._lib.sl_hip_synchronize(self._h))
+
+    # -- extension: submission of logged dispatches -----------------------
+    def submit(self) -> None:
+        """Enqueues the logged dispatches without waiting."""
+        self._check(self._lib.sl_hip_submit(self._h))
+
+    def set_options(self, fusion: bool = True, graphs: bool = True) -> None:
+        self._check(self._lib.sl_hip_set_options(self._h, (OPT_FUSION if fusion else 0) |
+                                                 (OPT_GRAPHS if graphs else 0)))
+
+    def stats(self) -> dict:
+        st = HipStats()
+        self._lib.sl_hip_get_stats(self._h, ctypes.byref(st))
+        return st.as_dict()
 
     # -- extension: group-quantized weights ------------------------------
     def bind_quantized(self, payload: int, scales: int, qformat: ir.QuantFormat, group_size: int, n: int,

@@ -19,7 +19,7 @@ def test_library_exports_every_declared_symbol():
     assert len(declared) >= 14
     for name in declared:
         assert hasattr(lib, name), f"{name} is declared in starlight_hip.h but not exported"
-    assert lib.sl_hip_abi_version() == 1
+    assert lib.sl_hip_abi_version() == 2
 
 
 def test_capabilities_declare_all_ops_and_composites():

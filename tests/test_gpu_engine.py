@@ -106,3 +106,33 @@ def test_kv_cache_matches_the_oracle_after_decode(hip):
         for kv in range(2):
             assert_normwise(got[l, kv, :7], want[l, kv, :7])
     assert np.all(got[:, :, 7:] == 0)
+
+
+@pytest.mark.parametrize("fusion,graphs", [(False, False), (True, False), (False, True)])
+def test_submission_options_keep_parity(hip, fusion, graphs):
+    """Every combination of the submission options (fused launches, graph
+    replay) gives the oracle's logits on the 1B-class INT4 shapes."""
+    cfg = LlamaConfig(layers=2, hidden=2048, heads=32, kv_heads=8, head_dim=64, ffn=8192, vocab=32000,
+                      theta=500_000.0, quant=QuantFormat.INT4)
+    hip.set_options(fusion=fusion, graphs=graphs)
+    try:
+        g_tokens, g_logits, c_tokens, c_logits = run_both(hip, cfg, 8, 4, 32, seed=1)
+    finally:
+        hip.set_options()
+    check_generation(g_tokens, g_logits, c_tokens, c_logits)
+
+
+def test_8b_shaped_decode_fuses_and_replays(hip):
+    """The 8B decode shapes (hidden 4096, 32/8 heads x 128, SwiGLU 14336, INT4
+    g128), two layers and a 32000 vocabulary so the oracle keeps up: 6-token
+    prefill, 6 greedy steps. The decode submissions must run fused and, from
+    the third step, as graph replays, with the oracle's logits every step."""
+    cfg = LlamaConfig(layers=2, hidden=4096, heads=32, kv_heads=8, head_dim=128, ffn=14336, vocab=32000,
+                      theta=500_000.0, quant=QuantFormat.INT4)
+    before = hip.stats()
+    g_tokens, g_logits, c_tokens, c_logits = run_both(hip, cfg, 6, 6, 64, seed=2)
+    after = hip.stats()
+    check_generation(g_tokens, g_logits, c_tokens, c_logits)
+    assert after["fused_commands"] > before["fused_commands"]
+    assert after["graph_captures"] > before["graph_captures"]
+    assert after["graph_replays"] >= before["graph_replays"] + 3

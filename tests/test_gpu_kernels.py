@@ -221,6 +221,12 @@ ATT_SHAPES = [
     (1, 1, 0, 8, 2, 1, 4095, 128, 4096),    # decode of the last position of a 4096 context
     (1, 1, 0, 8, 8, 1, 0, 128, 8),          # first token: one visible key
     (3, 1, 0, 6, 2, 2, 33, 32, 40),         # batch 3, GQA 3, two-token chunk
+    (1, 1, 0, 32, 8, 1, 8000, 128, 8192),   # 64 key partitions, several tiles per wave
+    (1, 1, 0, 16, 16, 1, 700, 64, 16384),   # MHA, partitions capped, long max_seq
+    (1, 1, 0, 32, 4, 1, 200, 128, 256),     # 8 query rows per KV head
+    (1, 1, 0, 16, 1, 1, 50, 128, 64),       # 16 query rows per KV head, head_dim 128
+    (1, 1, 0, 4, 2, 1, 77, 192, 100),       # head_dim 192
+    (2, 1, 0, 8, 2, 3, 40, 64, 64),         # three-token chunk through the decode kernel
 ]
 
 
@@ -368,12 +374,33 @@ def test_quantized_payload_reupload_refreshes_codes(hip):
     assert_normwise(read(hip, orf), want)
 
 
+def test_quantized_scale_reupload_refreshes_tile_scales(hip):
+    # Scales uploaded again into the bound buffer must reach the decode GEMV
+    # (which reads a tile-ordered copy of them) without a new bind.
+    n, k = 96, 512
+    r = rng(12)
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    words, scales = quant.quantize(w, 128, QuantFormat.INT4)
+    pb = hip.upload_new_u32(words)
+    sb = hip.upload_new_f32(scales)
+    hip.bind_quantized(pb, sb, QuantFormat.INT4, 128, n, k)
+    scales2 = (scales * r.uniform(0.5, 2.0, scales.shape)).astype(np.float32)
+    hip.upload_f32(sb, scales2)
+    a = r.standard_normal(k).astype(np.float32)
+    _, ar = put(hip, a)
+    _, orf = out_buf(hip, n)
+    hip.dispatch(Op.matmul_nt(), [ar, BufferRef(pb, 0, words.size)],
+                 [Value.f32([1, k]), Value.quantized([n, k], QuantFormat.INT4, 128)], [orf], [Value.f32([1, n])])
+    want = oracle.matmul_nt(a, quant.dequantize(words, scales2, n, k, 128, QuantFormat.INT4), 1, 1, k, n)
+    assert_normwise(read(hip, orf), want)
+
+
 # ------------------------------------------------------------- composites --
 
 
 @pytest.mark.parametrize("quantized", [False, True])
 @pytest.mark.parametrize("rows,hidden,inter", [(1, 1, 1), (3, 5, 7), (2, 8, 4), (4, 6, 13), (1, 256, 688),
-                                               (5, 512, 1024)])
+                                               (5, 512, 1024), (1, 4096, 14336), (16, 512, 768)])
 def test_swiglu_parity(hip, quantized, rows, hidden, inter):
     if quantized and (hidden % 128 or inter % 128):
         pytest.skip("group size 128 needs hidden and inter multiples of 128")
@@ -384,9 +411,10 @@ def test_swiglu_parity(hip, quantized, rows, hidden, inter):
     d = (r.standard_normal((hidden, inter)) * 0.1).astype(np.float32)
     _, xr = put(hip, x)
     if quantized:
-        gr, gv, g = quant_weight(hip, g, QuantFormat.INT4, 128)
-        ur, uv, u = quant_weight(hip, u, QuantFormat.INT4, 128)
-        dr, dv, d = quant_weight(hip, d, QuantFormat.INT4, 128)
+        fmt = QuantFormat.INT8 if rows == 16 else QuantFormat.INT4
+        gr, gv, g = quant_weight(hip, g, fmt, 128)
+        ur, uv, u = quant_weight(hip, u, fmt, 128)
+        dr, dv, d = quant_weight(hip, d, fmt, 128)
     else:
         gr, ur, dr = put(hip, g)[1], put(hip, u)[1], put(hip, d)[1]
         gv = uv = Value.f32([inter, hidden], ValueRole.PARAM)
@@ -401,7 +429,8 @@ def test_swiglu_parity(hip, quantized, rows, hidden, inter):
 
 
 @pytest.mark.parametrize("quantized", [False, True])
-@pytest.mark.parametrize("rows,hidden,out_f", [(1, 1, 1), (3, 7, 5), (2, 33, 17), (4, 256, 384)])
+@pytest.mark.parametrize("rows,hidden,out_f", [(1, 1, 1), (3, 7, 5), (2, 33, 17), (4, 256, 384), (1, 4096, 1024),
+                                               (3, 512, 640)])
 def test_rms_norm_matmul_parity(hip, quantized, rows, hidden, out_f):
     if quantized and hidden % 128:
         pytest.skip("group size 128 needs hidden multiple of 128")

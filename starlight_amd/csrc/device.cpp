@@ -30,6 +30,7 @@
 // its first write.
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <new>
@@ -369,7 +370,9 @@ int residual_port(const Logged& a, const sl_buffer_ref& o, uint64_t count, const
                   size_t n_reads) {
     if (a.plan.code != SL_OP_ADD || a.plan.len != count) return -1;
     int other = same_ref(a.in[1], o) ? 0 : same_ref(a.in[0], o) ? 1 : -1;
-    if (other < 0 || overlaps(a.in[other], o) || (overlaps(a.out, o) && !same_ref(a.out, o))) return -1;
+    if (other < 0 || overlaps(a.in[other], o) || (overlaps(a.out, o) && !same_ref(a.out, o)) ||
+        (overlaps(a.out, a.in[other]) && !same_ref(a.out, a.in[other])))
+        return -1;
     for (size_t i = 0; i < n_reads; ++i)
         if (overlaps(a.out, reads[i])) return -1;
     return other;
@@ -478,10 +481,11 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
         g.nseg = 1;
         g.m = rows;
         g.epilogue = kFusedPlain;
-        const sl_buffer_ref dreads[2] = {a_ref, norm ? norm->out : a_ref};
+        // The down kernel reads only h (the workspace), the weights and, per
+        // element, the residual: nothing another block could overwrite.
         if (j + 1 < n) {
             const Logged& a = d->log[j + 1];
-            const int other = residual_port(a, c1.out, rows * hidden, dreads, 2);
+            const int other = residual_port(a, c1.out, rows * hidden, nullptr, 0);
             if (other >= 0) {
                 g.epilogue = kFusedResidual;
                 g.resid[0] = fptr(d, a.in[other]);
@@ -507,11 +511,154 @@ const uint32_t* dyn_of(const Device* d, const Logged& c) {
     return c.dyn_slot >= 0 ? d->dyn + c.dyn_slot : nullptr;
 }
 
+// True when every element of `r` is overwritten by commands log[from..]
+// before any of them reads it: the value is dead, and a fused unit may skip
+// writing it (the final contents are those later writes either way).
+// `skip_reads` names a command whose reads do not count (one a fused unit
+// redirects elsewhere).
+bool dead_after(const Device* d, size_t from, const sl_buffer_ref& r, size_t skip_reads = SIZE_MAX) {
+    std::vector<std::pair<uint64_t, uint64_t>> live;
+    if (r.len) live.push_back({r.offset, r.offset + r.len});
+    for (size_t j = from; j < d->log.size() && !live.empty(); ++j) {
+        const Logged& c = d->log[j];
+        for (uint32_t k = 0; k < (j == skip_reads ? 0u : c.n_in); ++k) {
+            const sl_buffer_ref& x = c.in[k];
+            if (x.buffer != r.buffer || x.len == 0) continue;
+            for (const auto& iv : live)
+                if (x.offset < iv.second && iv.first < x.offset + x.len) return false;
+        }
+        const sl_buffer_ref& o = c.out;
+        if (o.buffer != r.buffer || o.len == 0) continue;
+        std::vector<std::pair<uint64_t, uint64_t>> rest;
+        for (const auto& iv : live) {
+            if (o.offset > iv.first) rest.push_back({iv.first, o.offset < iv.second ? o.offset : iv.second});
+            if (o.offset + o.len < iv.second)
+                rest.push_back({o.offset + o.len > iv.first ? o.offset + o.len : iv.first, iv.second});
+        }
+        live.clear();
+        for (const auto& iv : rest)
+            if (iv.first < iv.second) live.push_back(iv);
+    }
+    return live.empty();
+}
+
+// SplitHeads q/k/v, Rope q/k and CausalAttention (and MergeHeads, and the
+// output projection with its residual Add) as the decode kernels with Rope
+// applied inside: the split and rotated heads are never materialised, so
+// the unit is taken only when each of them is dead (dead_after); the
+// attention output and MergeHeads result are written unless dead. The
+// projection reads a copy of the merged heads in the workspace, so its
+// outputs may reuse any scratch region. Returns the commands covered.
+size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
+    const size_t n = d->log.size();
+    if (i + 6 > n) return 0;
+    const Logged* c = &d->log[i];
+    const Logged &sq = c[0], &sk = c[1], &sv = c[2], &rq = c[3], &rk = c[4], &at = c[5];
+    if (sq.plan.code != SL_OP_SPLIT_HEADS || sk.plan.code != SL_OP_SPLIT_HEADS || sv.plan.code != SL_OP_SPLIT_HEADS ||
+        rq.plan.code != SL_OP_ROPE || rk.plan.code != SL_OP_ROPE || at.plan.code != SL_OP_CAUSAL_ATTENTION)
+        return 0;
+    const Plan& ap = at.plan;
+    const uint64_t B = ap.batch, S = ap.seq, H = ap.heads, Hkv = ap.kv_heads, D = ap.head_dim;
+    auto split_ok = [&](const Logged& x, uint64_t heads) {
+        return x.plan.batch == B && x.plan.seq == S && x.plan.heads == heads && x.plan.head_dim == D;
+    };
+    auto rope_ok = [&](const Logged& x, uint64_t heads) {
+        return x.plan.batch == B && x.plan.seq == S && x.plan.heads == heads && x.plan.head_dim == D &&
+               same_ref(x.in[1], rq.in[1]) && x.plan.theta == rq.plan.theta &&
+               x.plan.rope_variant == rq.plan.rope_variant;
+    };
+    if (!split_ok(sq, H) || !split_ok(sk, Hkv) || !split_ok(sv, Hkv) || !rope_ok(rq, H) || !rope_ok(rk, Hkv) ||
+        !same_ref(rq.in[0], sq.out) || !same_ref(rk.in[0], sk.out) || !same_ref(at.in[0], rq.out) ||
+        !same_ref(at.in[1], rk.out) || !same_ref(at.in[2], sv.out))
+        return 0;
+    size_t used = 6;
+    const Logged* mh = nullptr;
+    if (i + 6 < n && c[6].plan.code == SL_OP_MERGE_HEADS && same_ref(c[6].in[0], at.out) &&
+        c[6].plan.heads == H && c[6].plan.head_dim == D) {
+        mh = &c[6];
+        used = 7;
+    }
+    // The split and rotated heads must be dead: each is scanned from the
+    // command after its last reader inside the unit, so the unit's own later
+    // writes (the attention output, MergeHeads) count as overwrites.
+    const sl_buffer_ref skipped[5] = {sq.out, sk.out, sv.out, rq.out, rk.out};
+    const size_t after_reader[5] = {i + 4, i + 5, i + 6, i + 6, i + 6};
+    for (int x = 0; x < 5; ++x)
+        if (!dead_after(d, after_reader[x], skipped[x])) return 0;
+    const sl_buffer_ref& cache = at.in[ap.state_index];
+    const sl_buffer_ref att = at.out;
+    const bool att_dead = mh != nullptr && dead_after(d, i + used, att);
+    // the projection chained below reads the mirror, not MergeHeads' output
+    const Logged* mm = mh && i + used < n ? &d->log[i + used] : nullptr;
+    const bool chainable = mm && mm->plan.code == SL_OP_MATMUL_NT && same_ref(mm->in[0], mh->out) &&
+                           mfma_weight(d, *mm, 1) && mm->plan.batch * mm->plan.m == B * S && mm->plan.k == H * D;
+    const bool merged_needed =
+        mh != nullptr && !dead_after(d, i + used, mh->out, chainable ? i + used : SIZE_MAX);
+    // outputs of the merge kernel: no overlap with the cache, or with each other
+    if (overlaps(att, cache) || (mh && overlaps(mh->out, cache)) ||
+        (mh && !att_dead && merged_needed && overlaps(att, mh->out) && !same_ref(att, mh->out)))
+        return 0;
+
+    AttentionArgs a{fptr(d, sq.in[0]), fptr(d, sk.in[0]), fptr(d, sv.in[0]), fptr(d, cache),
+                    att_dead ? nullptr : fptr(d, att), B, ap.layers, ap.layer, H, Hkv, S, ap.past_len, D,
+                    ap.max_seq, ap.scale, dyn_of(d, at)};
+    a.positions = uptr(d, rq.in[1]);
+    a.theta = rq.plan.theta;
+    a.rope_variant = rq.plan.rope_variant;
+    a.merged = merged_needed ? fptr(d, mh->out) : nullptr;
+
+    // the output projection (and its residual Add) reading the mirror
+    const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
+    const uint64_t mirror_at = (attention_workspace_floats(a) + 63) / 64 * 64;
+    const bool chain = chainable && mirror_at + B * S * H * D <= ws.floats;
+    if (chain) a.mirror = ws.data + mirror_at;
+    hipError_t e = launch_attention_fused(a, ws, d->stream);
+    if (e == hipErrorNotSupported) return 0;
+    if (e != hipSuccess) {
+        *err = e;
+        return used;
+    }
+    if (chain) {
+        QuantWeight w = weight_ref(d, mm->in[1], mm->plan.quant[1]).quant;
+        QgemvFused f{};
+        f.a = a.mirror;
+        f.w[0] = &w;
+        f.out[0] = fptr(d, mm->out);
+        f.nseg = 1;
+        f.m = B * S;
+        f.epilogue = kFusedPlain;
+        size_t extra = 1;
+        if (i + used + 1 < n) {
+            const Logged& ad = d->log[i + used + 1];
+            const int other = residual_port(ad, mm->out, B * S * w.n, nullptr, 0);
+            if (other >= 0) {
+                f.epilogue = kFusedResidual;
+                f.resid[0] = fptr(d, ad.in[other]);
+                f.out2[0] = fptr(d, ad.out);
+                extra = 2;
+            }
+        }
+        e = launch_qgemv_fused(f, d->stream);
+        if (e == hipErrorNotSupported) {
+            // run the projection on its own, from the mirror
+            e = launch_qmatmul(a.mirror, w, f.out[0], B * S, ws.after(mirror_at + B * S * H * D), d->stream);
+            extra = 1;
+        }
+        used += extra;
+    }
+    *err = e;
+    d->stats.fused_commands += used;
+    return used;
+}
+
 hipError_t run_log(Device* d) {
     for (size_t i = 0; i < d->log.size();) {
         size_t used = 0;
         hipError_t e = hipSuccess;
-        if (d->options & SL_HIP_OPT_FUSION) used = try_fuse(d, i, &e);
+        if (d->options & SL_HIP_OPT_FUSION) {
+            used = try_fuse_attention(d, i, &e);
+            if (used == 0 && e == hipSuccess) used = try_fuse(d, i, &e);
+        }
         if (e != hipSuccess) return e;
         if (used == 0) {
             const Logged& c = d->log[i];

@@ -23,6 +23,7 @@
 //    LDS, so each K/V row read from L2 serves 64 queries.
 #include "common.h"
 #include "kernels.h"
+#include "starlight_hip.h"
 
 namespace slhip {
 namespace {
@@ -40,6 +41,12 @@ struct Geo {
     uint64_t batch_stride, layer_offset, parity_stride;  // elements
     float scale;
     const uint32_t* dyn;  // when set, dyn[0] is past_len
+    // fused form: rope inputs and the extra outputs (see AttentionArgs)
+    const uint32_t* pos;
+    double theta;
+    uint32_t rope_variant;
+    float* merged;
+    float* mirror;
 };
 
 __device__ __forceinline__ uint32_t past_of(const Geo& g) { return g.dyn != nullptr ? g.dyn[0] : g.past_len; }
@@ -182,9 +189,31 @@ __device__ __forceinline__ void fold_state(float& m, float& l, float4 (&a)[DV], 
     m = mn;
 }
 
-template <int DV, int RT>
+// Rope rotation of one pair, as reference/rope.rs (and rope.hip) computes it.
+__device__ __forceinline__ void rotate(float& x, float& y, float sine, float cosine) {
+    const float a = x * cosine - y * sine;
+    const float b = x * sine + y * cosine;
+    x = a;
+    y = b;
+}
+
+// The pair angles' sine and cosine for token t: sc[t * D + pair] = sin,
+// sc[t * D + D/2 + pair] = cos, from f64 pow / sin / cos rounded once.
+__device__ __forceinline__ void rope_table(const Geo& g, uint64_t b, uint32_t S, uint32_t D, float* sc) {
+    const uint32_t half = D / 2;
+    for (uint32_t i = threadIdx.x; i < S * half; i += blockDim.x) {
+        const uint32_t t = i / half, pair = i % half;
+        const double position = static_cast<double>(g.pos[b * S + t]);
+        const double angle = position / pow(g.theta, 2.0 * static_cast<double>(pair) / static_cast<double>(D));
+        sc[t * D + pair] = static_cast<float>(sin(angle));
+        sc[t * D + half + pair] = static_cast<float>(cos(angle));
+    }
+}
+
+template <int DV, int RT, bool FUSED>
 __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     constexpr int D4 = 16 * DV;  // float4 per row
+    extern __shared__ float sc[];  // FUSED: rope table [S][D]
     __shared__ float4 qs[RT * D4];
     __shared__ float4 wacc[4][RT][D4];
     __shared__ float wml[4][RT][2];
@@ -212,7 +241,10 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
             const float* kr = kbase + static_cast<uint64_t>(j) * time_stride;
             const float* vr = vbase + static_cast<uint64_t>(j) * time_stride;
             if (j >= past) {
-                const uint64_t src = ((b * g.kv_heads + kvh) * S + (j - past)) * (4 * D4);
+                // [B, Hkv, S, D], or [B, S, Hkv * D] before SplitHeads (fused)
+                const uint64_t t = j - past;
+                const uint64_t src = (FUSED ? (b * S + t) * g.kv_heads + kvh : (b * g.kv_heads + kvh) * S + t) *
+                                     (4 * D4);
                 kr = g.k_new + src;
                 vr = g.v_new + src;
             }
@@ -233,7 +265,9 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     for (int u = 0; u < QPT; ++u) {
         const uint32_t i = min(static_cast<uint32_t>(tid + 256 * u), static_cast<uint32_t>(RT * D4 - 1));
         const uint32_t r = min(i / D4, R - 1), c = i % D4, gi = r / S, t = r % S;
-        qv[u] = reinterpret_cast<const float4*>(g.q + ((b * g.heads + kvh * G + gi) * S + t) * (4 * D4))[c];
+        const uint64_t h = kvh * G + gi;
+        const uint64_t row = FUSED ? (b * S + t) * g.heads + h : (b * g.heads + h) * S + t;
+        qv[u] = reinterpret_cast<const float4*>(g.q + row * (4 * D4))[c];
     }
     uint32_t tile = p + P * wave;
     float4 kv[kDecodeKeys][DV], vv[kDecodeKeys][DV];
@@ -242,6 +276,34 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     for (int u = 0; u < QPT; ++u) {
         const uint32_t i = tid + 256 * u;
         if (i < RT * D4) qs[i] = i / D4 < R ? qv[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if constexpr (FUSED) {
+        // Rope of the query rows, in LDS
+        constexpr uint32_t D = 4 * D4;
+        rope_table(g, b, S, D, sc);
+        __syncthreads();
+        if (g.rope_variant == SL_ROPE_NEOX) {
+            for (uint32_t i = tid; i < R * (D4 / 2); i += 256) {  // four pairs (d, d + D/2) per item
+                const uint32_t r = i / (D4 / 2), c = i % (D4 / 2);
+                const float* st = sc + (r % S) * D;
+                float4 x = qs[r * D4 + c], y = qs[r * D4 + c + D4 / 2];
+                rotate(x.x, y.x, st[4 * c], st[D / 2 + 4 * c]);
+                rotate(x.y, y.y, st[4 * c + 1], st[D / 2 + 4 * c + 1]);
+                rotate(x.z, y.z, st[4 * c + 2], st[D / 2 + 4 * c + 2]);
+                rotate(x.w, y.w, st[4 * c + 3], st[D / 2 + 4 * c + 3]);
+                qs[r * D4 + c] = x;
+                qs[r * D4 + c + D4 / 2] = y;
+            }
+        } else {
+            for (uint32_t i = tid; i < R * D4; i += 256) {  // pairs (2i, 2i + 1), two per float4
+                const uint32_t r = i / D4, c = i % D4;
+                const float* st = sc + (r % S) * D;
+                float4 x = qs[r * D4 + c];
+                rotate(x.x, x.y, st[2 * c], st[D / 2 + 2 * c]);
+                rotate(x.z, x.w, st[2 * c + 1], st[D / 2 + 2 * c + 1]);
+                qs[r * D4 + c] = x;
+            }
+        }
     }
     __syncthreads();
 
@@ -264,6 +326,31 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
         for (int kb = 0; kb < kDecodeKeys; ++kb) {
             const uint32_t j = j0 + kb;
             if (j >= past && j < keys) {
+                if constexpr (FUSED) {
+                    // Rope of a new key row before it is used and appended
+                    constexpr uint32_t D = 4 * D4;
+                    const float* st = sc + (j - past) * D;
+                    if (g.rope_variant == SL_ROPE_NEOX) {
+#pragma unroll
+                        for (int u = 0; u < DV / 2; ++u) {  // pairs (d, d + D/2) sit in one lane
+                            const uint32_t d = 4 * li + 64 * u;
+                            float4& x = kv[kb][u];
+                            float4& y = kv[kb][u + DV / 2];
+                            rotate(x.x, y.x, st[d], st[D / 2 + d]);
+                            rotate(x.y, y.y, st[d + 1], st[D / 2 + d + 1]);
+                            rotate(x.z, y.z, st[d + 2], st[D / 2 + d + 2]);
+                            rotate(x.w, y.w, st[d + 3], st[D / 2 + d + 3]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < DV; ++u) {
+                            const uint32_t pr = (4 * li + 64 * u) / 2;
+                            float4& x = kv[kb][u];
+                            rotate(x.x, x.y, st[pr], st[D / 2 + pr]);
+                            rotate(x.z, x.w, st[pr + 1], st[D / 2 + pr + 1]);
+                        }
+                    }
+                }
 #pragma unroll
                 for (int u = 0; u < DV; ++u) {
                     reinterpret_cast<float4*>(kbase + j * time_stride)[li + 16 * u] = kv[kb][u];
@@ -437,7 +524,12 @@ __global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
         }
         if (q == 0 || T == 1) {
             const uint32_t gi = r / S, t = r % S;
-            reinterpret_cast<float4*>(g.out + ((b * g.heads + kvh * G + gi) * S + t) * (4 * D4))[c] = a;
+            const uint64_t h = kvh * G + gi;
+            if (g.out != nullptr) reinterpret_cast<float4*>(g.out + ((b * g.heads + h) * S + t) * (4 * D4))[c] = a;
+            // MergeHeads layout [B, S, H * D] (reference/layout.rs merge_heads)
+            const uint64_t mrow = (b * S + t) * g.heads + h;
+            if (g.merged != nullptr) reinterpret_cast<float4*>(g.merged + mrow * (4 * D4))[c] = a;
+            if (g.mirror != nullptr) reinterpret_cast<float4*>(g.mirror + mrow * (4 * D4))[c] = a;
         }
     }
 }
@@ -540,10 +632,10 @@ __global__ __launch_bounds__(128) void attn_tiled(Geo g) {
 
 }  // namespace
 
-hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStream_t s) {
-    const uint64_t queries = a.batch * a.heads * a.seq;
-    if (queries == 0 || a.head_dim == 0) return hipSuccess;
-    Geo g;
+namespace {
+
+Geo make_geo(const AttentionArgs& a, const Workspace& ws) {
+    Geo g{};
     g.q = a.q;
     g.k_new = a.k_new;
     g.v_new = a.v_new;
@@ -562,40 +654,89 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
     g.batch_stride = a.layers * 2 * g.parity_stride;
     g.scale = a.scale;
     g.dyn = a.dyn;
+    g.pos = a.positions;
+    g.theta = static_cast<double>(a.theta);
+    g.rope_variant = a.rope_variant;
+    g.merged = a.merged;
+    g.mirror = a.mirror;
+    return g;
+}
 
-    // Decode path: kv_append fused into the tile kernel, then the merge.
+uint64_t decode_parts(const AttentionArgs& a) {
+    uint64_t parts = (a.max_seq + 127) / 128;
+    return parts > kMergeMaxParts ? kMergeMaxParts : parts;
+}
+
+// The decode kernels (tile + merge); hipErrorNotSupported for shapes they
+// do not take (nothing launched).
+hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hipStream_t s, bool fused) {
     const uint64_t rows = static_cast<uint64_t>(g.group) * a.seq;
     const uint64_t dv = a.head_dim / 64;
     const uint64_t rt = rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
-    uint64_t parts = (a.max_seq + 127) / 128;
-    if (parts > kMergeMaxParts) parts = kMergeMaxParts;
+    const uint64_t parts = decode_parts(a);
     const bool aligned = aligned16(a.q) && aligned16(a.k_new) && aligned16(a.v_new) && aligned16(a.cache) &&
-                         aligned16(a.out);
-    if (rows <= kDecodeMaxRows && a.head_dim % 64 == 0 && dv >= 1 && dv <= 4 && rt * dv <= 32 && aligned &&
-        a.batch * a.kv_heads * parts * rows * (kDecodePartStride + a.head_dim) <= ws.floats) {
-        g.chunks = static_cast<uint32_t>(parts);
-        g.chunk = kDecodeTile;
-        const dim3 grid(static_cast<unsigned>(parts), g.kv_heads, static_cast<unsigned>(a.batch));
-        switch (dv * 100 + rt) {
-            case 104: attn_decode<1, 4><<<grid, 256, 0, s>>>(g); break;
-            case 108: attn_decode<1, 8><<<grid, 256, 0, s>>>(g); break;
-            case 116: attn_decode<1, 16><<<grid, 256, 0, s>>>(g); break;
-            case 204: attn_decode<2, 4><<<grid, 256, 0, s>>>(g); break;
-            case 208: attn_decode<2, 8><<<grid, 256, 0, s>>>(g); break;
-            case 216: attn_decode<2, 16><<<grid, 256, 0, s>>>(g); break;
-            case 304: attn_decode<3, 4><<<grid, 256, 0, s>>>(g); break;
-            case 308: attn_decode<3, 8><<<grid, 256, 0, s>>>(g); break;
-            case 404: attn_decode<4, 4><<<grid, 256, 0, s>>>(g); break;
-            default: attn_decode<4, 8><<<grid, 256, 0, s>>>(g); break;
-        }
-        attn_decode_merge<<<dim3(g.kv_heads, static_cast<unsigned>(a.batch)), 256, 0, s>>>(
-            g, static_cast<uint32_t>(parts));
-        return hipGetLastError();
+                         (a.out == nullptr || aligned16(a.out)) && (a.merged == nullptr || aligned16(a.merged)) &&
+                         (a.mirror == nullptr || aligned16(a.mirror));
+    if (!(rows <= kDecodeMaxRows && a.head_dim % 64 == 0 && dv >= 1 && dv <= 4 && rt * dv <= 32 && aligned &&
+          a.batch * a.kv_heads * parts * rows * (kDecodePartStride + a.head_dim) <= ws.floats))
+        return hipErrorNotSupported;
+    if (fused && (a.positions == nullptr || (a.rope_variant == SL_ROPE_NEOX && dv % 2 != 0) ||
+                  a.rope_variant > SL_ROPE_GPTJ))
+        return hipErrorNotSupported;
+    g.chunks = static_cast<uint32_t>(parts);
+    g.chunk = kDecodeTile;
+    const dim3 grid(static_cast<unsigned>(parts), g.kv_heads, static_cast<unsigned>(a.batch));
+    const size_t lds = fused ? a.seq * a.head_dim * sizeof(float) : 0;
+#define SL_DECODE(DVv, RTv)                                                   \
+    (fused ? attn_decode<DVv, RTv, true><<<grid, 256, lds, s>>>(g)            \
+           : attn_decode<DVv, RTv, false><<<grid, 256, lds, s>>>(g))
+    switch (dv * 100 + rt) {
+        case 104: SL_DECODE(1, 4); break;
+        case 108: SL_DECODE(1, 8); break;
+        case 116: SL_DECODE(1, 16); break;
+        case 204: SL_DECODE(2, 4); break;
+        case 208: SL_DECODE(2, 8); break;
+        case 216: SL_DECODE(2, 16); break;
+        case 304: SL_DECODE(3, 4); break;
+        case 308: SL_DECODE(3, 8); break;
+        case 404: SL_DECODE(4, 4); break;
+        default: SL_DECODE(4, 8); break;
     }
+#undef SL_DECODE
+    attn_decode_merge<<<dim3(g.kv_heads, static_cast<unsigned>(a.batch)), 256, 0, s>>>(
+        g, static_cast<uint32_t>(parts));
+    return hipGetLastError();
+}
+
+}  // namespace
+
+uint64_t attention_workspace_floats(const AttentionArgs& a) {
+    const uint64_t rows = a.heads / (a.kv_heads ? a.kv_heads : 1) * a.seq;
+    return a.batch * a.kv_heads * decode_parts(a) * rows * (kDecodePartStride + a.head_dim);
+}
+
+hipError_t launch_attention_fused(const AttentionArgs& a, const Workspace& ws, hipStream_t s) {
+    if (a.batch * a.heads * a.seq == 0 || a.head_dim == 0 || a.kv_heads == 0) return hipErrorNotSupported;
+    return launch_decode(a, make_geo(a, ws), ws, s, true);
+}
+
+hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStream_t s) {
+    const uint64_t queries = a.batch * a.heads * a.seq;
+    if (queries == 0 || a.head_dim == 0) return hipSuccess;
+    AttentionArgs plain = a;  // the unfused op writes only `out`
+    plain.positions = nullptr;
+    plain.merged = nullptr;
+    plain.mirror = nullptr;
+    Geo g = make_geo(plain, ws);
+
+    // Decode path: kv_append fused into the tile kernel, then the merge.
+    const hipError_t d = launch_decode(a, g, ws, s, false);
+    if (d != hipErrorNotSupported) return d;
 
     hipError_t e = launch_kv_append(a.k_new, a.v_new, a.cache, a.batch, a.layers, a.layer, a.kv_heads, a.head_dim,
                                     a.max_seq, a.past_len, a.seq, a.dyn, s);
     if (e != hipSuccess) return e;
+    const bool aligned = aligned16(a.q) && aligned16(a.cache) && aligned16(a.out);
     if (a.seq >= 16 && aligned && (a.head_dim == 64 || a.head_dim == 128)) {
         dim3 grid(static_cast<unsigned>((a.seq + kTileQ - 1) / kTileQ), g.heads, static_cast<unsigned>(a.batch));
         if (a.head_dim == 64) attn_tiled<64><<<grid, 128, 0, s>>>(g);

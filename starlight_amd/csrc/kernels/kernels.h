@@ -76,9 +76,25 @@ struct AttentionArgs {
     uint64_t batch, layers, layer, heads, kv_heads, seq, past_len, head_dim, max_seq;
     float scale;
     const uint32_t* dyn;  // device copy of past_len read by the kernels, or null
+    // Fused form (launch_attention_fused): q / k_new / v_new are the
+    // projections before SplitHeads, [batch, seq, heads * head_dim], and are
+    // rotated by Rope at `positions` inside the kernel; `out` (the attention
+    // output, may be null), `merged` (MergeHeads of it, may be null) and
+    // `mirror` (a copy of merged in the workspace, may be null) are written.
+    const uint32_t* positions = nullptr;
+    float theta = 0.f;
+    uint32_t rope_variant = 0;
+    float* merged = nullptr;
+    float* mirror = nullptr;
 };
 // Appends k_new / v_new to the cache and computes the attention output.
 hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStream_t s);
+// SplitHeads x3 + Rope x2 + CausalAttention (+ MergeHeads) as the two decode
+// launches; hipErrorNotSupported (nothing launched) for shapes the decode
+// kernel does not take. `mirror` must lie in `ws` past the first
+// attention_workspace_floats(a) floats.
+hipError_t launch_attention_fused(const AttentionArgs& a, const Workspace& ws, hipStream_t s);
+uint64_t attention_workspace_floats(const AttentionArgs& a);
 
 // ---- dense f32 matmul (reference/matmul.rs) ----
 // out[b] = a[b or 0] x op(b[b or 0]); op = transpose when `nt`.

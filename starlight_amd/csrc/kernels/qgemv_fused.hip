@@ -66,8 +66,12 @@ struct Item {
     float s0, s1;
 };
 
-template <int BITS, int NT, int GPS>
+// SPG: 64-k steps per group (1: group 64, 2: group 128, 0: a multiple of 256,
+// counted at run time); MR: accumulator rows a lane finishes (1 when m == 1,
+// else 4). Both only trim bookkeeping from the stream loop.
+template <int BITS, int NT, int SPG, int MR>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(Args p) {
+    constexpr int GPS = SPG == 1 ? 2 : 1;
     constexpr int PF = BITS == 4 ? 6 : 4;  // superblocks in flight per wave
     constexpr int WPT = kWaves / NT;  // waves per tile
     constexpr uint32_t SB_BYTES = BITS == 4 ? 1024 : 2048;
@@ -271,7 +275,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // ---- main loop over the stream ----
     const uint32_t kb4 = lane / 16;
     const uint32_t am = min(static_cast<uint32_t>(lane % 16), M - 1);  // rows past M repeat row M - 1, unused
-    const uint32_t rm = M < 4 ? M : 4;                                 // accumulator rows worth finishing
     const uint32_t steps_per_group = p.group / 64;
     const uint32_t g_start = sbA * 128 / p.group;
     const v4i zero = {0, 0, 0, 0};
@@ -287,8 +290,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         for (int s = 0; s < PF; ++s) {
             const uint32_t i = base + s;
             if (i >= items) break;
-            const Item<BITS> cur = win[s];
-            fetch_next(win[s]);
+            // win[s] is used in place and refilled after the item's MFMAs, so
+            // the wait for it is for this item's loads only (a copy would
+            // make the compiler wait before the refill).
+            const Item<BITS>& cur = win[s];
             const uint32_t j = cj;
             if (q < nlive) {
                 const int8_t* ap = a_row + q * 128;
@@ -315,25 +320,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                     acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bv, acc0, 0, 0, 0);
                     acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bv, acc1, 0, 0, 0);
                     acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bv, acc2, 0, 0, 0);
-                    if (++gstep == steps_per_group) {
-                        gstep = 0;
+                    bool group_end;
+                    if constexpr (SPG == 1) group_end = true;
+                    else if constexpr (SPG == 2) group_end = st == 1;
+                    else group_end = ++gstep == steps_per_group;
+                    if (group_end) {
+                        if constexpr (SPG == 0) gstep = 0;
+                        if constexpr (SPG == 1) gi = 2 * (sbA + q) + st;
+                        if constexpr (SPG == 2) gi = sbA + q;
                         const float sc = st == 1 ? cur.s1 : cur.s0;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            if (static_cast<uint32_t>(r) >= rm) continue;
+                        for (int r = 0; r < MR; ++r) {
                             const uint32_t m = min(kb4 * 4 + r, M - 1);
                             float val = fmaf(static_cast<float>(acc2[r]), 65536.0f,
                                              fmaf(static_cast<float>(acc1[r]), 256.0f, static_cast<float>(acc0[r])));
                             if (BITS == 4) val -= 8.0f * static_cast<float>(xsum[m * p.groups_total + gi]);
                             total[r] = fmaf(val, sc, total[r]);
                         }
-                        ++gi;
+                        if constexpr (SPG == 0) ++gi;
                         acc0 = zero;
                         acc1 = zero;
                         acc2 = zero;
                     }
                 }
             }
+            fetch_next(win[s]);
             if (++q == len) {
                 q = 0;
                 ++cj;
@@ -441,15 +452,21 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const size_t lds = static_cast<size_t>(3) * p.m * p.k + sizeof(int) * p.m * p.groups_total +
                        sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m;
     if (lds + kStaticLds > max_lds_per_block()) return hipErrorNotSupported;
-    const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, g64 = p.group == 64;
-#define SL_QGEMV_FUSED(B, T, G) qgemv_fused<B, T, G><<<blocks, kThreads, lds, s>>>(p)
+    const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, m1 = p.m == 1;
+    const int spg = p.group == 64 ? 1 : p.group == 128 ? 2 : 0;
+#define SL_QGEMV_FUSED(B, T, G)                                                        \
+    (m1 ? qgemv_fused<B, T, G, 1><<<blocks, kThreads, lds, s>>>(p)                     \
+        : qgemv_fused<B, T, G, 4><<<blocks, kThreads, lds, s>>>(p))
+#define SL_QGEMV_FUSED_G(B, T) \
+    (spg == 1 ? SL_QGEMV_FUSED(B, T, 1) : spg == 2 ? SL_QGEMV_FUSED(B, T, 2) : SL_QGEMV_FUSED(B, T, 0))
     if (int4) {
-        if (pair) g64 ? SL_QGEMV_FUSED(4, 2, 2) : SL_QGEMV_FUSED(4, 2, 1);
-        else g64 ? SL_QGEMV_FUSED(4, 1, 2) : SL_QGEMV_FUSED(4, 1, 1);
+        if (pair) SL_QGEMV_FUSED_G(4, 2);
+        else SL_QGEMV_FUSED_G(4, 1);
     } else {
-        if (pair) g64 ? SL_QGEMV_FUSED(8, 2, 2) : SL_QGEMV_FUSED(8, 2, 1);
-        else g64 ? SL_QGEMV_FUSED(8, 1, 2) : SL_QGEMV_FUSED(8, 1, 1);
+        if (pair) SL_QGEMV_FUSED_G(8, 2);
+        else SL_QGEMV_FUSED_G(8, 1);
     }
+#undef SL_QGEMV_FUSED_G
 #undef SL_QGEMV_FUSED
     return hipGetLastError();
 }

@@ -1,0 +1,125 @@
+"""Fused submission units on the GPU, against the oracle run op by op.
+
+The device fuses SplitHeads x3 + Rope x2 + CausalAttention + MergeHeads into
+the decode attention kernels when the split and rotated heads are dead (every
+element overwritten by a later command of the same submission before any
+read). These tests lay the values out in one scratch buffer, make the
+intermediates dead with a later Scale over their region, and check the
+attention output, the merged heads and the KV cache; a variant where a later
+command reads an intermediate must run unfused and still match.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_normwise, rel_l2
+from starlight_amd.ir import BufferRef, Op, RopeVariant, Value, ValueRole
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # batch, heads, kv_heads, seq, past_len, head_dim, max_seq, variant
+    (1, 32, 8, 1, 1000, 128, 1100, RopeVariant.NEOX),   # 8B-shaped decode step
+    (1, 8, 2, 1, 77, 256, 128, RopeVariant.NEOX),
+    (2, 16, 4, 1, 300, 128, 512, RopeVariant.GPTJ),
+    (1, 8, 2, 2, 40, 64, 64, RopeVariant.GPTJ),         # two-token chunk, head_dim 64
+    (1, 4, 4, 1, 0, 128, 16, RopeVariant.NEOX),         # first token
+]
+
+
+def run_group(hip, case, consume_intermediate):
+    B, H, Hkv, S, past, D, max_seq, variant = case
+    r = np.random.default_rng(sum(case[:-1]))
+    nq, nk = B * S * H * D, B * S * Hkv * D
+    q = r.uniform(-1, 1, nq).astype(np.float32)
+    k = r.uniform(-1, 1, nk).astype(np.float32)
+    v = r.uniform(-1, 1, nk).astype(np.float32)
+    cache = r.uniform(-1, 1, B * 1 * 2 * max_seq * Hkv * D).astype(np.float32)
+    pos = (past + np.arange(S, dtype=np.uint32))[None, :].repeat(B, 0).ravel()
+    theta = 500000.0
+    scale = float(np.float32(1.0 / math.sqrt(D)))
+
+    # scratch layout: q k v | qh kh vh qr kr | att merged
+    offs = {}
+    cur = 0
+    for name, size in [("q", nq), ("k", nk), ("v", nk), ("qh", nq), ("kh", nk), ("vh", nk), ("qr", nq),
+                       ("kr", nk), ("att", nq), ("merged", nq)]:
+        offs[name] = (cur, size)
+        cur += (size + 63) // 64 * 64
+    scratch = hip.allocate_f32(cur, 256)
+    init = np.zeros(cur, np.float32)
+    for name, arr in (("q", q), ("k", k), ("v", v)):
+        o, n = offs[name]
+        init[o:o + n] = arr
+    hip.upload_f32(scratch, init)
+    ref = {name: BufferRef(scratch, o, n) for name, (o, n) in offs.items()}
+    cb = hip.upload_new_f32(cache)
+    pb = hip.upload_new_u32(pos)
+    posr = BufferRef(pb, 0, B * S)
+
+    inter_lo = offs["qh"][0]
+    inter_hi = offs["kr"][0] + offs["kr"][1]
+    # (uploads submit the log, so everything is uploaded before the group)
+    src = hip.upload_new_f32(np.ones(inter_hi - inter_lo, np.float32))
+    extra = hip.allocate_f32(nq, 256) if consume_intermediate else None
+
+    qf, kf = Value.f32([B, S, H * D]), Value.f32([B, S, Hkv * D])
+    q4, k4 = Value.f32([B, H, S, D]), Value.f32([B, Hkv, S, D])
+    pv = Value.u32([B, S])
+    before = hip.stats()
+    hip.dispatch(Op.split_heads(H, D), [ref["q"]], [qf], [ref["qh"]], [q4])
+    hip.dispatch(Op.split_heads(Hkv, D), [ref["k"]], [kf], [ref["kh"]], [k4])
+    hip.dispatch(Op.split_heads(Hkv, D), [ref["v"]], [kf], [ref["vh"]], [k4])
+    hip.dispatch(Op.rope(variant, theta), [ref["qh"], posr], [q4, pv], [ref["qr"]], [q4])
+    hip.dispatch(Op.rope(variant, theta), [ref["kh"], posr], [k4, pv], [ref["kr"]], [k4])
+    hip.dispatch(Op.causal_attention(0, H, Hkv, D, scale),
+                 [ref["qr"], ref["kr"], ref["vh"], BufferRef(cb, 0, cache.size)],
+                 [q4, k4, k4, Value.f32([B, 1, 2, max_seq, Hkv, D], ValueRole.STATE)],
+                 [ref["att"]], [q4], [past])
+    hip.dispatch(Op.merge_heads(H, D), [ref["att"]], [q4], [ref["merged"]], [qf])
+    span = BufferRef(scratch, inter_lo, inter_hi - inter_lo)
+    sv = Value.f32([inter_hi - inter_lo])
+    if consume_intermediate:
+        # a later read of qr keeps it alive: the group must run unfused
+        hip.dispatch(Op.scale_by(2.0), [ref["qr"]], [q4], [BufferRef(extra, 0, nq)], [q4])
+    # overwrite the split / rotated heads: they are dead after the group
+    hip.dispatch(Op.scale_by(3.0), [BufferRef(src, 0, inter_hi - inter_lo)], [sv], [span], [sv])
+    hip.synchronize()
+    after = hip.stats()
+
+    qh = oracle.split_heads(q, B, S, H, D)
+    kh = oracle.split_heads(k, B, S, Hkv, D)
+    vh = oracle.split_heads(v, B, S, Hkv, D)
+    vname = "neox" if variant == RopeVariant.NEOX else "gptj"
+    qr = oracle.rope(qh, pos, B, H, S, D, theta, vname)
+    kr = oracle.rope(kh, pos, B, Hkv, S, D, theta, vname)
+    want_att, want_cache = oracle.causal_attention(qr, kr, vh, cache, B, 1, 0, H, Hkv, S, past, D, max_seq, scale)
+    want_merged = oracle.merge_heads(want_att, B, S, H, D)
+    got = hip.read_f32(scratch, cur)
+    got_cache = hip.read_f32(cb, cache.size)
+    o, n = offs["att"]
+    assert_normwise(got[o:o + n], want_att)
+    o, n = offs["merged"]
+    assert_normwise(got[o:o + n], want_merged)
+    assert np.all(got[inter_lo:inter_hi] == 3.0)
+    assert rel_l2(got_cache, want_cache) <= 1e-6
+    if extra is not None:
+        np.testing.assert_array_equal(hip.read_f32(extra, nq), (qr * np.float32(2.0)).astype(np.float32))
+    return after["fused_commands"] - before["fused_commands"]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_attention_group_fuses_and_matches(hip, case):
+    fused = run_group(hip, case, consume_intermediate=False)
+    B, H, Hkv, S, past, D, max_seq, variant = case
+    if variant == RopeVariant.NEOX and (D // 64) % 2:
+        assert fused == 0  # NEOX pairs of head_dim 64 span lanes: not fused
+    else:
+        assert fused >= 7
+
+
+@pytest.mark.parametrize("case", CASES[:2])
+def test_attention_group_with_live_intermediate_runs_unfused(hip, case):
+    assert run_group(hip, case, consume_intermediate=True) == 0

@@ -11,12 +11,21 @@ embeddings and RMSNorm weights stay f32, lm_head is INT4.
 
 The JSON line also carries
   roofline     — the INT4 q-GEMV (the decode's dominant kernel) on the
-                 [14336 x 4096] gate/up shape, timed with HIP events on the
-                 device stream over rotating weight copies (no MALL reuse):
-                 algorithmic bytes per launch / average launch time vs 8 TB/s;
+                 [14336 x 4096] gate/up shape, M = 1: 200 dispatches over 16
+                 weight copies (500 MB, no MALL reuse), fusion off so each
+                 dispatch is one launch, replayed as a graph and timed with
+                 HIP events on the device stream: algorithmic bytes per
+                 launch / average launch time vs 8 TB/s. `traffic` is the
+                 HBM bytes per launch measured with rocprofv3 FETCH_SIZE and
+                 WRITE_SIZE (scaled by the same counters on a plain copy),
+                 read from the committed summary when present;
+  rmsnorm      — RMSNorm over [4096 x 4096] f32, the same way;
   cpu_baseline — the C oracle (scalar restatement of backend-cpu) on the
                  host: one 8B-shaped layer decoding at 1024 cached positions
                  plus a slice of lm_head, extrapolated to a full token.
+
+--mode roofline runs only the q-GEMV leg and --mode copy only a plain
+copy (Scale by 1 over 64 Mi floats), for the counter runs.
 """
 from __future__ import annotations
 
@@ -131,7 +140,22 @@ class HipTimer:
         return ms.value
 
 
-def qgemv_roofline(dev, n=14336, k=4096, copies=16, launches=200):
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "qgemv_int4_14336x4096_m1_pmc.txt")
+
+
+def measured_traffic():
+    """HBM bytes per q-GEMV launch from the committed counter summary."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return int(float(line.split("=")[1]))
+    except OSError:
+        pass
+    return None
+
+
+def qgemv_roofline(dev, n=14336, k=4096, copies=16, launches=200, graphs=True):
     """Times the INT4 g128 q-GEMV at [n x k], M = 1, over `copies` distinct
     weight copies (16 x 31 MB > the 256 MB MALL) with HIP events."""
     from starlight_amd import quant
@@ -155,8 +179,10 @@ def qgemv_roofline(dev, n=14336, k=4096, copies=16, launches=200):
         dev.dispatch(Op.matmul_nt(), [BufferRef(x, 0, k), BufferRef(weights[i % copies], 0, words.size)], [xv, wv],
                      [BufferRef(outs[i % copies], 0, n)], [ov])
 
-    # The same submission three times: run, captured as a graph, replayed;
-    # the timed one replays the graph, so the events see back-to-back kernels.
+    # One launch per dispatch (no fusion of same-input GEMVs). The same
+    # submission three times: run, captured as a graph, replayed; the timed
+    # one replays the graph, so the events see back-to-back kernels.
+    dev.set_options(fusion=False, graphs=graphs)
     for _ in range(3):
         for i in range(launches):
             run(i)
@@ -168,16 +194,76 @@ def qgemv_roofline(dev, n=14336, k=4096, copies=16, launches=200):
     timer.begin()
     dev.submit()
     ms = timer.end_ms()
+    dev.set_options()
     avg_us = ms * 1000.0 / launches
     algorithmic = n * k // 2 + n * (k // 128) * 4 + k * 4 + n * 4
     achieved = algorithmic / (avg_us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": f"q-GEMV INT4 g128 [{n}x{k}] M=1", "bytes_per_launch": algorithmic,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+            "kernel": f"qgemv_fused (q-GEMV INT4 g128 [{n}x{k}] M=1)", "bytes_per_launch": algorithmic,
             "avg_launch_us": round(avg_us, 3)}
 
 
+def rmsnorm_roofline(dev, rows=4096, hidden=4096, copies=4, launches=40):
+    """RMSNorm over [rows x hidden] f32 with weight ~N(1, 0.1), rotating
+    input/output copies, graph-replayed and timed with HIP events."""
+    from starlight_amd.ir import BufferRef, Op, Value, ValueRole
+
+    rng = np.random.default_rng(6)
+    xs = [dev.upload_new_f32(rng.standard_normal(rows * hidden, dtype=np.float32)) for _ in range(copies)]
+    ys = [dev.allocate_f32(rows * hidden, 256) for _ in range(copies)]
+    g = dev.upload_new_f32((1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float32))
+    v = Value.f32([rows, hidden])
+
+    def run(i):
+        dev.dispatch(Op.rms_norm(1e-5), [BufferRef(xs[i % copies], 0, rows * hidden), BufferRef(g, 0, hidden)],
+                     [v, Value.f32([hidden], ValueRole.PARAM)], [BufferRef(ys[i % copies], 0, rows * hidden)], [v])
+
+    for _ in range(3):
+        for i in range(launches):
+            run(i)
+        dev.submit()
+    dev.synchronize()
+    timer = HipTimer(dev.stream)
+    for i in range(launches):
+        run(i)
+    timer.begin()
+    dev.submit()
+    ms = timer.end_ms()
+    avg_us = ms * 1000.0 / launches
+    algorithmic = 2 * rows * hidden * 4 + hidden * 4
+    achieved = algorithmic / (avg_us * 1e-6) / 1e9
+    return {"kernel": f"rms_norm [{rows}x{hidden}] f32", "achieved": round(achieved, 1), "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_launch": algorithmic,
+            "avg_launch_us": round(avg_us, 3)}
+
+
+def copy_run(dev, n=64 << 20, launches=20):
+    """A plain copy (Scale by 1) of n floats, the counters' calibration."""
+    from starlight_amd.ir import BufferRef, Op, Value
+
+    x = dev.allocate_f32(n, 256)
+    y = dev.allocate_f32(n, 256)
+    v = Value.f32([n])
+    dev.set_options(fusion=False, graphs=False)
+    for _ in range(launches):
+        dev.dispatch(Op.scale_by(1.0), [BufferRef(x, 0, n)], [v], [BufferRef(y, 0, n)], [v])
+    dev.synchronize()
+    log(f"copy: {launches} launches of {n * 4} bytes read + {n * 4} bytes written")
+
+
 # ------------------------------------------------------------ cpu leg ------
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
 
 
 def cpu_baseline(cfg, budget_s=25.0):
@@ -223,7 +309,8 @@ def cpu_baseline(cfg, budget_s=25.0):
     return {"value": round(1.0 / per_token, 5), "unit": "tok/s", "cores": 1, "kind": "port",
             "sample": (f"oracle decode of one 8B-shaped layer (dequantized INT4 weights, 1024 cached positions) "
                        f"x {steps} steps = {per_layer:.3f} s/layer, x{cfg.layers} layers + lm_head "
-                       f"(1/16 slice timed, x16) = {per_token:.2f} s/token; extrapolated")}
+                       f"(1/16 slice timed, x16) = {per_token:.2f} s/token; extrapolated; single-threaded on "
+                       f"{cpu_model()} ({os.cpu_count()} logical CPUs visible)")}
 
 
 # ------------------------------------------------------------------ main ---
@@ -232,15 +319,27 @@ def cpu_baseline(cfg, budget_s=25.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--int8", action="store_true", help="INT8 g128 weights instead of INT4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--mode", choices=["full", "roofline", "copy"], default="full")
+    ap.add_argument("--no-graphs", action="store_true", help="roofline/copy modes: launch eagerly")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU runs are not part of "
                                    "this build (use --gpus 1)"}))
         sys.exit(2)
+    if args.mode != "full":
+        from starlight_amd.device import HipDevice
+
+        dev = HipDevice(0)
+        if args.mode == "roofline":
+            print(json.dumps(qgemv_roofline(dev, graphs=not args.no_graphs)), flush=True)
+        else:
+            copy_run(dev)
+        dev.close()
+        return
 
     import torch
 
@@ -297,6 +396,8 @@ def main():
 
     roof = qgemv_roofline(dev)
     log(f"q-GEMV roofline: {roof}")
+    norm = rmsnorm_roofline(dev)
+    log(f"RMSNorm: {norm}")
     cpu = None if args.no_cpu else cpu_baseline(cfg)
     if cpu:
         log(f"cpu baseline: {cpu}")
@@ -325,6 +426,7 @@ def main():
         "decode_hbm_frac": round(hbm_frac, 4),
         "prefill_tok_s": round(PROMPT_LEN / prefill_s, 1),
         "roofline": roof,
+        "rmsnorm": norm,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

@@ -88,8 +88,9 @@ sl_status sl_engine_step(sl_engine *engine, uint32_t mode, const uint32_t *token
 /* Greedy decode loop for benchmarks and tests (not part of sl-core, which
  * has no sampler, ARCH-0008 G-13): after a prefill of `prompt` (batch 1),
  * runs `steps` decode steps feeding back the first maximum logit, writes the
- * generated ids to `tokens_out` and, if `logits_out` is non-null, every
- * step's logits (steps + 1 rows of vocab floats, the prefill row first). */
+ * steps + 1 generated ids to `tokens_out` (the prefill's first, then one per
+ * decode step) and, if `logits_out` is non-null, every step's logits
+ * (steps + 1 rows of vocab floats, the prefill row first). */
 sl_status sl_engine_generate(sl_engine *engine, const uint32_t *prompt, size_t prompt_len, uint32_t steps,
                              uint32_t *tokens_out, float *logits_out, size_t vocab);
 

@@ -7,7 +7,7 @@
  * implementation of that trait is `CpuDevice`
  * (crates/backends/backend-cpu/src/device.rs:114-213); every entry point below
  * names the method it replaces. A Rust `backend-hip` crate binds these
- * symbols one-to-one (see INTEGRATION.md for the `extern "C"` block).
+ * symbols one-to-one through an `extern "C"` block.
  *
  * Conventions
  *  - All entry points return `sl_status`; SL_OK is 0. On failure the device
@@ -16,9 +16,13 @@
  *    `sl_device::BufferRef` (ARCH-0007 §3.1).
  *  - A device is single-owner and not thread-safe, like `&mut self` methods of
  *    `trait Device: Send`.
- *  - dispatch() enqueues work on the device's stream and returns; results are
- *    visible to download_*() (which orders after all enqueued work) and after
- *    synchronize(). dispatch() performs no device allocation.
+ *  - dispatch() validates (every error a reference dispatch reports is
+ *    reported by the same call) and logs the command; logged commands are
+ *    enqueued on the device's stream, in order, before anything can observe
+ *    them: synchronize(), upload_*(), download_*(), bind_quantized(),
+ *    sl_hip_submit(). Results are visible to download_*() and after
+ *    synchronize(); a kernel failure surfaces there as Execution. dispatch()
+ *    performs no device allocation.
  */
 #ifndef STARLIGHT_HIP_H
 #define STARLIGHT_HIP_H
@@ -185,8 +189,8 @@ sl_status sl_hip_dispatch(sl_hip_device *device, const sl_op *op, const sl_buffe
                           const sl_value *output_values, size_t n_outputs, const uint32_t *scalars,
                           size_t n_scalars);
 
-/* Device::synchronize (device.rs:210-212): blocks until all dispatched work
- * has finished and reports any deferred execution failure. */
+/* Device::synchronize (device.rs:210-212): submits the logged commands,
+ * blocks until all of them have finished and reports any execution failure. */
 sl_status sl_hip_synchronize(sl_hip_device *device);
 
 /* The DeviceError of the most recent failing call on `device`. */

@@ -3,8 +3,8 @@
  *
  * Scalar CPU restatement of StarLight's reference kernels
  * (the files under crates/backends/backend-cpu/src/reference/). Only tests/, the smoke
- * check and the CPU-baseline leg of bench.py load this library, and only as
- * the checker; the product (starlight_amd/) never links or calls it.
+ * check and the CPU-baseline leg of bench.py load this library, and only to
+ * check or time against it; the product (starlight_amd/) never links or calls it.
  *
  * Contract kept from the reference (backend-cpu/README.md:55-67):
  *   - f32 data, row-major, no strides;

@@ -14,8 +14,9 @@
 //    resident over several tiles (at most two per CU), so the prologue is
 //    paid once per block, and the per-tile LDS sums are double-buffered;
 //  * the activations are converted once per block from registers: every
-//    thread holds its share of the m x k input as float4, the per-row
-//    reductions (sum of squares, max |x|) go wave -> LDS -> one wave per row;
+//    thread holds its share of the m x k input as float4; the exponent of
+//    each 256-element chunk comes from one wave's DPP max (no block-wide
+//    pass), and only the RMSNorm sum of squares goes wave -> LDS -> row;
 //  * up to three weights that read the same input run as one launch (q/k/v);
 //  * prologue RMSNorm: x = (a * inv) * gamma with inv = 1/sqrt(ss/k + eps)
 //    (reference/norm.rs:27-60), block 0 also writes x as the norm's output;
@@ -34,8 +35,8 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxF4 = 8;  // float4 of activations per thread
 constexpr uint32_t kMaxElems = kThreads * 4 * kMaxF4;
-// static LDS of the kernel: red, row_val, exps, wres
-constexpr size_t kStaticLds = sizeof(float) * (kMaxF4 * kWaves + 16 + 16 + 2 * kWaves * 16 * 16);
+// static LDS of the kernel: red, row_val, cfac, wres
+constexpr size_t kStaticLds = sizeof(float) * (kMaxF4 * kWaves + 16 + kMaxElems / 256 + 2 * kWaves * 16 * 16);
 
 struct Seg {
     const uint8_t* tiles;
@@ -53,7 +54,7 @@ struct Args {
     float eps;
     Seg seg[kFusedMaxSegs];
     uint32_t nseg;
-    uint32_t m, k, group, sb_total, groups_total, sb_per_wave;
+    uint32_t m, k, group, unit, sb_total, groups_total, sb_per_wave;
     uint32_t tiles_total;  // block tiles (pair mode: gate tiles)
     uint32_t epilogue;
 };
@@ -78,14 +79,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     extern __shared__ __align__(16) int8_t limbs[];  // [3][m][k], xsum [m][groups], tres [tiles][16][m]
     __shared__ float red[kMaxF4][kWaves];
     __shared__ float row_val[16];
-    __shared__ int exps[16];
+    __shared__ float cfac[kMaxElems / 256];  // per 256-element chunk: 2^(E-22)
     __shared__ float wres[2][kWaves][16][16];
 
     const int tid = threadIdx.x, lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, kept in scalar registers
     const uint32_t M = p.m, K = p.k, K4 = K / 4;
     int* xsum = reinterpret_cast<int*>(limbs + 3 * M * K);
-    float* tres = reinterpret_cast<float*>(xsum + M * p.groups_total);
+    float* tres = reinterpret_cast<float*>(xsum + M * (K / p.unit));
 
     // ---- this wave's stream: for each block tile j (global tile
     // blockIdx.x + j * gridDim.x) the superblocks [sbA, sbA + len); every
@@ -164,6 +165,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     float4 v[kMaxF4], gv[kMaxF4];
 #pragma unroll
     for (int u = 0; u < kMaxF4; ++u) {
+        v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (kThreads * u >= total4) continue;  // block-uniform: runs past the input load nothing
         const uint32_t f = min(tid + kThreads * u, total4 - 1);
         v[u] = reinterpret_cast<const float4*>(p.a)[f];
         if (p.gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(p.gamma)[f % K4];
@@ -174,7 +177,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
     for (int u = 0; u < kMaxF4; ++u)
         if (tid + kThreads * u >= total4) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (uint32_t i = tid; i < M * p.groups_total; i += kThreads) xsum[i] = 0;
 
     // Row of the wave-uniform run (u, wave): k % 256 == 0 keeps a wave's 64
     // float4 inside one row. Each wave reduces the rows w, w + 8 over the
@@ -219,55 +221,56 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             }
         }
     }
-#pragma unroll
-    for (int u = 0; u < kMaxF4; ++u) {
-        float mx = fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w)));
-        mx = wave_max(mx);
-        if (lane == 0) red[u][wave] = mx;
-    }
-    row_reduce(true);
-    if (tid < 16) {
-        int e = 0;
-        if (tid < static_cast<int>(M) && row_val[tid] != 0.f) frexpf(row_val[tid], &e);
-        exps[tid] = e;  // max|x| < 2^e
-    }
-    __syncthreads();
-
-    // exact integers X = rint(x * 2^(22-E)) as three signed int8 limbs
-    const int seg_lanes = p.group / 4 < kWave ? static_cast<int>(p.group / 4) : kWave;
+    // Exact integers X = rint(x * 2^(22-E)) as three signed int8 limbs, with
+    // E the exponent of the largest |x| of each 256-element chunk (one wave's
+    // run): the wave that converts a chunk finds its maximum with a DPP
+    // reduction, so no block-wide pass is needed. The integer sums are
+    // combined per unit of min(group, 256) elements, which never spans two
+    // chunks, each with its chunk's factor 2^(E-22).
+    const uint32_t U = p.unit, seg_lanes = U / 4;  // 16, 32 or 64 lanes per unit
+    const uint32_t chunks = K / 256, units = K / U;
 #pragma unroll
     for (int u = 0; u < kMaxF4; ++u) {
         const uint32_t fb = static_cast<uint32_t>(wave) * kWave + kThreads * u;
         if (fb >= total4) continue;  // whole wave past the end
         const uint32_t f = tid + kThreads * u;
         const uint32_t r = f / K4, c4 = f % K4;
-        const int shift = 22 - exps[r];
+        const float mx = wave_max(fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+        int ex = 0;
+        if (mx != 0.f) frexpf(mx, &ex);  // max|x| < 2^ex
+        const int shift = 22 - ex;
+        if (lane == 0) cfac[r * chunks + c4 / 64] = ldexpf(1.0f, ex - 22);
+        // |X| <= 2^22, so X + 0x808080 lies in [0, 2^24) and its bytes b_i
+        // satisfy X = sum (b_i - 128) 256^i: the bytes of
+        // (X + 0x808080) ^ 0x808080 are the three signed limbs; v_perm
+        // gathers byte i of the four elements into limb word i.
         const float xe[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-        uint32_t packed[3] = {0u, 0u, 0u};
+        uint32_t y[4];
         int sx = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int X = static_cast<int>(rintf(ldexpf(xe[e], shift)));
-            const int l0 = ((X + 128) & 255) - 128;
-            const int x1 = (X - l0) >> 8;
-            const int l1 = ((x1 + 128) & 255) - 128;
-            const int l2 = (x1 - l1) >> 8;
-            packed[0] |= (static_cast<uint32_t>(l0) & 0xFFu) << (8 * e);
-            packed[1] |= (static_cast<uint32_t>(l1) & 0xFFu) << (8 * e);
-            packed[2] |= (static_cast<uint32_t>(l2) & 0xFFu) << (8 * e);
+            y[e] = static_cast<uint32_t>(X + 0x808080) ^ 0x808080u;
             sx += X;
         }
+        const uint32_t lo01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);  // y0.b0 y1.b0 y0.b1 y1.b1
+        const uint32_t lo23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
+        const uint32_t hi01 = __builtin_amdgcn_perm(y[1], y[0], 0x07030602u);  // y0.b2 y1.b2 ..
+        const uint32_t hi23 = __builtin_amdgcn_perm(y[3], y[2], 0x07030602u);
+        const uint32_t packed[3] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u),
+                                    __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                                    __builtin_amdgcn_perm(hi23, hi01, 0x05040100u)};
 #pragma unroll
         for (int limb = 0; limb < 3; ++limb)
             *reinterpret_cast<uint32_t*>(limbs + (limb * M + r) * K + 4 * c4) = packed[limb];
         if (BITS == 4) {
-            // group sums of X: a group covers 16, 32 or 64 lanes (one, two
-            // or four DPP rows)
+            // unit sums of X (for the offset-binary correction): a unit covers
+            // 16, 32 or 64 lanes (one, two or four DPP rows) of this run
             const int rs = row_sum(sx);
             const int r0 = __builtin_amdgcn_readlane(rs, 0), r1 = __builtin_amdgcn_readlane(rs, 16);
             const int r2 = __builtin_amdgcn_readlane(rs, 32), r3 = __builtin_amdgcn_readlane(rs, 48);
-            const int gsum = seg_lanes == 16 ? rs : seg_lanes == 32 ? (lane < 32 ? r0 + r1 : r2 + r3) : r0 + r1 + r2 + r3;
-            if (lane % seg_lanes == 0) atomicAdd(&xsum[r * p.groups_total + (4 * c4) / p.group], gsum);
+            const int usum = seg_lanes == 16 ? rs : seg_lanes == 32 ? (lane < 32 ? r0 + r1 : r2 + r3) : r0 + r1 + r2 + r3;
+            if (lane % seg_lanes == 0) xsum[r * units + (4 * c4) / U] = usum;
         }
     }
     __syncthreads();
@@ -275,15 +278,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // ---- main loop over the stream ----
     const uint32_t kb4 = lane / 16;
     const uint32_t am = min(static_cast<uint32_t>(lane % 16), M - 1);  // rows past M repeat row M - 1, unused
-    const uint32_t steps_per_group = p.group / 64;
-    const uint32_t g_start = sbA * 128 / p.group;
+    const uint32_t steps_per_unit = p.unit / 64;
+    const uint32_t g_start = sbA * 128 / p.unit;
     const v4i zero = {0, 0, 0, 0};
     float total[4] = {0.f, 0.f, 0.f, 0.f};
     // integer sums of the current group (a group may span superblocks; the
     // wave runs are group-aligned, so a group never spans two runs)
     v4i acc0 = zero, acc1 = zero, acc2 = zero;
     uint32_t cj = 0, q = 0;               // block tile and position of the item being consumed
-    uint32_t gstep = 0, gi = g_start;     // 64-k steps into the current group, its index
+    uint32_t gstep = 0, gi = g_start;     // 64-k steps into the current unit, its index
     const int8_t* a_row = limbs + am * K + sbA * 128 + kb4 * 16;
     for (uint32_t base = 0; base < items; base += PF) {
 #pragma unroll
@@ -323,19 +326,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                     bool group_end;
                     if constexpr (SPG == 1) group_end = true;
                     else if constexpr (SPG == 2) group_end = st == 1;
-                    else group_end = ++gstep == steps_per_group;
+                    else group_end = ++gstep == steps_per_unit;
                     if (group_end) {
                         if constexpr (SPG == 0) gstep = 0;
                         if constexpr (SPG == 1) gi = 2 * (sbA + q) + st;
                         if constexpr (SPG == 2) gi = sbA + q;
                         const float sc = st == 1 ? cur.s1 : cur.s0;
+                        const uint32_t chunk = ((sbA + q) * 128 + st * 64) / 256;
 #pragma unroll
                         for (int r = 0; r < MR; ++r) {
                             const uint32_t m = min(kb4 * 4 + r, M - 1);
                             float val = fmaf(static_cast<float>(acc2[r]), 65536.0f,
                                              fmaf(static_cast<float>(acc1[r]), 256.0f, static_cast<float>(acc0[r])));
-                            if (BITS == 4) val -= 8.0f * static_cast<float>(xsum[m * p.groups_total + gi]);
-                            total[r] = fmaf(val, sc, total[r]);
+                            if (BITS == 4) val -= 8.0f * static_cast<float>(xsum[m * units + gi]);
+                            total[r] = fmaf(val * cfac[m * chunks + chunk], sc, total[r]);
                         }
                         if constexpr (SPG == 0) ++gi;
                         acc0 = zero;
@@ -366,7 +370,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                         float acc = 0.f;
 #pragma unroll
                         for (int w = 0; w < kWaves; ++w) acc += wres[buf][w][m][col];
-                        val = ldexpf(acc, exps[m] - 22);
+                        val = acc;
                     } else {
                         float g = 0.f, up = 0.f;
 #pragma unroll
@@ -374,8 +378,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                             g += wres[buf][w][m][col];
                             up += wres[buf][WPT + w][m][col];
                         }
-                        g = ldexpf(g, exps[m] - 22);
-                        up = ldexpf(up, exps[m] - 22);
                         val = (g * (1.0f / (1.0f + expf(-g)))) * up;
                     }
                     tres[(j * 16 + col) * M + m] = val;
@@ -423,6 +425,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     p.group = w0.group;
     p.sb_total = p.k / 128;
     p.groups_total = p.k / p.group;
+    p.unit = p.group < 256 ? p.group : 256;
     p.epilogue = f.epilogue;
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < f.nseg; ++i) {
@@ -449,7 +452,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const uint32_t per_cap = 4096 / (16 * p.m);
     if (per_block > per_cap) per_block = per_cap;
     const uint32_t blocks = (tiles + per_block - 1) / per_block;
-    const size_t lds = static_cast<size_t>(3) * p.m * p.k + sizeof(int) * p.m * p.groups_total +
+    const size_t lds = static_cast<size_t>(3) * p.m * p.k + sizeof(int) * p.m * (p.k / p.unit) +
                        sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m;
     if (lds + kStaticLds > max_lds_per_block()) return hipErrorNotSupported;
     const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, m1 = p.m == 1;

@@ -26,10 +26,25 @@
 #include "kernels.h"
 #include "starlight_hip.h"
 
+#include <type_traits>
+
 namespace slhip {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Calls f(std::integral_constant<int, I>) for I = 0 .. N-1, unrolled.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for_from(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for_from<I + 1, N>(f);
+    }
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_from<0, N>(f);
+}
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
@@ -64,13 +79,14 @@ struct Args {
 template <int BITS>
 struct Item {
     uint4 c0, c1;
-    float s0, s1;
+    float s0, s1;  // s1: the second group's scale (group 64 only)
 };
 
 // SPG: 64-k steps per group (1: group 64, 2: group 128, 0: a multiple of 256,
-// counted at run time); MR: accumulator rows a lane finishes (1 when m == 1,
-// else 4). Both only trim bookkeeping from the stream loop.
-template <int BITS, int NT, int SPG, int MR>
+// counted at run time). LR (m <= 4): the three limbs of every activation row
+// share one MFMA as its A rows 4 * m + limb, so a 64-k step is one LDS read
+// and one MFMA; otherwise (m <= 16) each limb matrix is an MFMA of its own.
+template <int BITS, int NT, int SPG, bool LR>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(Args p) {
     constexpr int GPS = SPG == 1 ? 2 : 1;
     constexpr int PF = BITS == 4 ? 6 : 4;  // superblocks in flight per wave
@@ -144,7 +160,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             it.s1 = s2.y;
         } else {
             it.s0 = sp[0];
-            it.s1 = it.s0;
         }
         // The window fetches PF items past the stream's end; those re-read
         // the last item, so the cursor never leaves this wave's last tile.
@@ -277,113 +292,152 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 
     // ---- main loop over the stream ----
     const uint32_t kb4 = lane / 16;
-    const uint32_t am = min(static_cast<uint32_t>(lane % 16), M - 1);  // rows past M repeat row M - 1, unused
+    // A-operand row of this lane: with LR row 4 * m + limb (limb 3 repeats
+    // limb 2), else row m of each limb matrix; rows past M repeat row M - 1.
+    // Their products are never read.
+    uint32_t a_off;
+    if constexpr (LR) {
+        const uint32_t row = static_cast<uint32_t>(lane % 16);
+        a_off = (min(row % 4, 2u) * M + min(row / 4, M - 1)) * K;
+    } else {
+        a_off = min(static_cast<uint32_t>(lane % 16), M - 1) * K;
+    }
+    constexpr int NR = LR ? 1 : 4;  // output rows a lane finishes (LR: m = kb4)
     const uint32_t steps_per_unit = p.unit / 64;
     const uint32_t g_start = sbA * 128 / p.unit;
     const v4i zero = {0, 0, 0, 0};
-    float total[4] = {0.f, 0.f, 0.f, 0.f};
+    float total[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) total[r] = 0.f;
     // integer sums of the current group (a group may span superblocks; the
     // wave runs are group-aligned, so a group never spans two runs)
     v4i acc0 = zero, acc1 = zero, acc2 = zero;
     uint32_t cj = 0, q = 0;               // block tile and position of the item being consumed
     uint32_t gstep = 0, gi = g_start;     // 64-k steps into the current unit, its index
-    const int8_t* a_row = limbs + am * K + sbA * 128 + kb4 * 16;
-    for (uint32_t base = 0; base < items; base += PF) {
+    const int8_t* a_col = limbs + a_off + kb4 * 16;
+    // One item of the stream: win[S] is used in place (a copy would make the
+    // compiler wait before its refill) and refilled afterwards. A dead item
+    // (a trailing wave's padding past k) computes on clamped addresses and
+    // its sums are dropped by a select rather than a branch.
+    auto consume = [&](auto s_c, bool use) {
+        constexpr int S = decltype(s_c)::value;
+        const Item<BITS>& cur = win[S];
+        const uint32_t sbi = use ? sbA + q : 0u;  // superblock along k (dead: 0)
+        const int8_t* ap = a_col + sbi * 128;
 #pragma unroll
-        for (int s = 0; s < PF; ++s) {
-            const uint32_t i = base + s;
-            if (i >= items) break;
-            // win[s] is used in place and refilled after the item's MFMAs, so
-            // the wait for it is for this item's loads only (a copy would
-            // make the compiler wait before the refill).
-            const Item<BITS>& cur = win[s];
-            const uint32_t j = cj;
-            if (q < nlive) {
-                const int8_t* ap = a_row + q * 128;
-#pragma unroll
-                for (int st = 0; st < 2; ++st) {
-                    v4i bv;
-                    if (BITS == 4) {
-                        const uint32_t wa = st == 0 ? cur.c0.x : cur.c0.z;
-                        const uint32_t wb = st == 0 ? cur.c0.y : cur.c0.w;
-                        bv[0] = static_cast<int>(wa & 0x0F0F0F0Fu);
-                        bv[1] = static_cast<int>((wa >> 4) & 0x0F0F0F0Fu);
-                        bv[2] = static_cast<int>(wb & 0x0F0F0F0Fu);
-                        bv[3] = static_cast<int>((wb >> 4) & 0x0F0F0F0Fu);
-                    } else {
-                        const uint4 cw = st == 0 ? cur.c0 : cur.c1;
-                        bv[0] = static_cast<int>(cw.x);
-                        bv[1] = static_cast<int>(cw.y);
-                        bv[2] = static_cast<int>(cw.z);
-                        bv[3] = static_cast<int>(cw.w);
-                    }
-                    const v4i a0 = *reinterpret_cast<const v4i*>(ap + st * 64);
-                    const v4i a1 = *reinterpret_cast<const v4i*>(ap + M * K + st * 64);
-                    const v4i a2 = *reinterpret_cast<const v4i*>(ap + 2 * M * K + st * 64);
-                    acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bv, acc0, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bv, acc1, 0, 0, 0);
-                    acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bv, acc2, 0, 0, 0);
-                    bool group_end;
-                    if constexpr (SPG == 1) group_end = true;
-                    else if constexpr (SPG == 2) group_end = st == 1;
-                    else group_end = ++gstep == steps_per_unit;
-                    if (group_end) {
-                        if constexpr (SPG == 0) gstep = 0;
-                        if constexpr (SPG == 1) gi = 2 * (sbA + q) + st;
-                        if constexpr (SPG == 2) gi = sbA + q;
-                        const float sc = st == 1 ? cur.s1 : cur.s0;
-                        const uint32_t chunk = ((sbA + q) * 128 + st * 64) / 256;
-#pragma unroll
-                        for (int r = 0; r < MR; ++r) {
-                            const uint32_t m = min(kb4 * 4 + r, M - 1);
-                            float val = fmaf(static_cast<float>(acc2[r]), 65536.0f,
-                                             fmaf(static_cast<float>(acc1[r]), 256.0f, static_cast<float>(acc0[r])));
-                            if (BITS == 4) val -= 8.0f * static_cast<float>(xsum[m * units + gi]);
-                            total[r] = fmaf(val * cfac[m * chunks + chunk], sc, total[r]);
-                        }
-                        if constexpr (SPG == 0) ++gi;
-                        acc0 = zero;
-                        acc1 = zero;
-                        acc2 = zero;
-                    }
-                }
+        for (int st = 0; st < 2; ++st) {
+            v4i bv;
+            if (BITS == 4) {
+                const uint32_t wa = st == 0 ? cur.c0.x : cur.c0.z;
+                const uint32_t wb = st == 0 ? cur.c0.y : cur.c0.w;
+                bv[0] = static_cast<int>(wa & 0x0F0F0F0Fu);
+                bv[1] = static_cast<int>((wa >> 4) & 0x0F0F0F0Fu);
+                bv[2] = static_cast<int>(wb & 0x0F0F0F0Fu);
+                bv[3] = static_cast<int>((wb >> 4) & 0x0F0F0F0Fu);
+            } else {
+                const uint4 cw = st == 0 ? cur.c0 : cur.c1;
+                bv[0] = static_cast<int>(cw.x);
+                bv[1] = static_cast<int>(cw.y);
+                bv[2] = static_cast<int>(cw.z);
+                bv[3] = static_cast<int>(cw.w);
             }
-            fetch_next(win[s]);
-            if (++q == len) {
-                q = 0;
-                ++cj;
-                gi = g_start;
-                // tile j done: wave partials -> LDS, summed in wave order
-                // into the block's result area (global writes wait until the
-                // stream is done, so the loop issues only the window's loads)
-                const uint32_t buf = j & 1;
+            if constexpr (LR) {
+                // a group's first step starts from zero (no reset moves)
+                const bool fresh = SPG == 1 || (SPG == 2 && st == 0);
+                const v4i a0 = *reinterpret_cast<const v4i*>(ap + st * 64);
+                acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bv, fresh ? zero : acc0, 0, 0, 0);
+            } else {
+                const v4i a0 = *reinterpret_cast<const v4i*>(ap + st * 64);
+                const v4i a1 = *reinterpret_cast<const v4i*>(ap + M * K + st * 64);
+                const v4i a2 = *reinterpret_cast<const v4i*>(ap + 2 * M * K + st * 64);
+                acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bv, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bv, acc1, 0, 0, 0);
+                acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bv, acc2, 0, 0, 0);
+            }
+            bool group_end;
+            if constexpr (SPG == 1) group_end = true;
+            else if constexpr (SPG == 2) group_end = st == 1;
+            else group_end = ++gstep == steps_per_unit;
+            if (group_end) {
+                if constexpr (SPG == 0) gstep = 0;
+                if constexpr (SPG == 1) gi = 2 * sbi + st;
+                if constexpr (SPG == 2) gi = sbi;
+                const uint32_t gix = min(gi, units - 1);
+                const float sc = GPS == 2 && st == 1 ? cur.s1 : cur.s0;
+                const uint32_t chunk = (sbi * 128 + st * 64) / 256;
+                if constexpr (LR) {
+                    // rows 4 * kb4 + limb: this lane holds all three limbs of m = kb4
+                    const uint32_t m = min(kb4, M - 1);
+                    float val = fmaf(static_cast<float>(acc0[2]), 65536.0f,
+                                     fmaf(static_cast<float>(acc0[1]), 256.0f, static_cast<float>(acc0[0])));
+                    if (BITS == 4) val -= 8.0f * static_cast<float>(xsum[m * units + gix]);
+                    const float t = fmaf(val * cfac[m * chunks + chunk], sc, total[0]);
+                    total[0] = use ? t : total[0];
+                } else {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    wres[buf][wave][kb4 * 4 + r][lane % 16] = total[r];
-                    total[r] = 0.f;
-                }
-                __syncthreads();
-                if (static_cast<uint32_t>(tid) < 16 * M) {
-                    const uint32_t m = tid / 16, col = tid % 16;
-                    float val;
-                    if (NT == 1) {
-                        float acc = 0.f;
-#pragma unroll
-                        for (int w = 0; w < kWaves; ++w) acc += wres[buf][w][m][col];
-                        val = acc;
-                    } else {
-                        float g = 0.f, up = 0.f;
-#pragma unroll
-                        for (int w = 0; w < WPT; ++w) {
-                            g += wres[buf][w][m][col];
-                            up += wres[buf][WPT + w][m][col];
-                        }
-                        val = (g * (1.0f / (1.0f + expf(-g)))) * up;
+                    for (int r = 0; r < NR; ++r) {
+                        const uint32_t m = min(kb4 * 4 + r, M - 1);
+                        float val = fmaf(static_cast<float>(acc2[r]), 65536.0f,
+                                         fmaf(static_cast<float>(acc1[r]), 256.0f, static_cast<float>(acc0[r])));
+                        if (BITS == 4) val -= 8.0f * static_cast<float>(xsum[m * units + gix]);
+                        const float t = fmaf(val * cfac[m * chunks + chunk], sc, total[r]);
+                        total[r] = use ? t : total[r];
                     }
-                    tres[(j * 16 + col) * M + m] = val;
                 }
+                if constexpr (SPG == 0) ++gi;
+                acc0 = zero;
+                acc1 = zero;
+                acc2 = zero;
             }
         }
+    };
+    // tile j done: wave partials -> LDS, summed in wave order into the
+    // block's result area (global writes wait until the stream is done, so
+    // the loop issues only the window's loads)
+    auto tile_end = [&]() {
+        const uint32_t j = cj;
+        q = 0;
+        ++cj;
+        gi = g_start;
+        const uint32_t buf = j & 1;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            wres[buf][wave][LR ? kb4 : kb4 * 4 + r][lane % 16] = total[r];
+            total[r] = 0.f;
+        }
+        __syncthreads();
+        if (static_cast<uint32_t>(tid) < 16 * M) {
+            const uint32_t m = tid / 16, col = tid % 16;
+            float val;
+            if (NT == 1) {
+                float acc = 0.f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) acc += wres[buf][w][m][col];
+                val = acc;
+            } else {
+                float g = 0.f, up = 0.f;
+#pragma unroll
+                for (int w = 0; w < WPT; ++w) {
+                    g += wres[buf][w][m][col];
+                    up += wres[buf][WPT + w][m][col];
+                }
+                val = (g * (1.0f / (1.0f + expf(-g)))) * up;
+            }
+            tres[(j * 16 + col) * M + m] = val;
+        }
+    };
+    // Rounds of PF items; in the last one the items past the stream do no
+    // work and no tile bookkeeping but still refill their slot (with the
+    // last item again). There is no exit inside a round, so every wait stays
+    // one item deep: an early exit, or a second copy of the round for the
+    // tail, makes the compiler wait for the whole window.
+    for (uint32_t base = 0; base < items; base += PF) {
+        static_for<PF>([&](auto s_c) {
+            const bool live = base + decltype(s_c)::value < items;
+            if (live) consume(s_c, q < nlive);
+            fetch_next(win[decltype(s_c)::value]);
+            if (live && ++q == len) tile_end();
+        });
     }
 
     // ---- results of all the block's tiles ----
@@ -455,11 +509,11 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const size_t lds = static_cast<size_t>(3) * p.m * p.k + sizeof(int) * p.m * (p.k / p.unit) +
                        sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m;
     if (lds + kStaticLds > max_lds_per_block()) return hipErrorNotSupported;
-    const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, m1 = p.m == 1;
+    const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, lr = p.m <= 4;
     const int spg = p.group == 64 ? 1 : p.group == 128 ? 2 : 0;
 #define SL_QGEMV_FUSED(B, T, G)                                                        \
-    (m1 ? qgemv_fused<B, T, G, 1><<<blocks, kThreads, lds, s>>>(p)                     \
-        : qgemv_fused<B, T, G, 4><<<blocks, kThreads, lds, s>>>(p))
+    (lr ? qgemv_fused<B, T, G, true><<<blocks, kThreads, lds, s>>>(p)                  \
+        : qgemv_fused<B, T, G, false><<<blocks, kThreads, lds, s>>>(p))
 #define SL_QGEMV_FUSED_G(B, T) \
     (spg == 1 ? SL_QGEMV_FUSED(B, T, 1) : spg == 2 ? SL_QGEMV_FUSED(B, T, 2) : SL_QGEMV_FUSED(B, T, 0))
     if (int4) {

@@ -271,7 +271,9 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     }
     uint32_t tile = p + P * wave;
     float4 kv[kDecodeKeys][DV], vv[kDecodeKeys][DV];
-    load_tile(min(tile, ntiles - 1), kv, vv);  // unconditional: a wave with no tile loads and ignores one
+    // a wave with no tile loads nothing: loads in flight into registers the
+    // combine reuses would hold the whole block at its barrier
+    if (tile < ntiles) load_tile(tile, kv, vv);
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
         const uint32_t i = tid + 256 * u;
@@ -320,8 +322,11 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     for (; tile < ntiles; tile += 4 * P) {
         const uint32_t j0 = tile * kDecodeTile + grp * kDecodeKeys;
         float4 kn[kDecodeKeys][DV], vn[kDecodeKeys][DV];
+        // the next tile's loads only when there is one: loads still in flight
+        // at the loop's end would hold the combine below (their registers are
+        // reused), and most decode waves have a single tile
         const bool more = tile + 4 * P < ntiles;
-        load_tile(min(tile + 4 * P, ntiles - 1), kn, vn);
+        if (more) load_tile(tile + 4 * P, kn, vn);
 #pragma unroll
         for (int kb = 0; kb < kDecodeKeys; ++kb) {
             const uint32_t j = j0 + kb;

@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void ew_vec4(const float4* __restrict__ a, con
         r.y = apply<OP>(x.y, y.y, factor);
         r.z = apply<OP>(x.z, y.z, factor);
         r.w = apply<OP>(x.w, y.w, factor);
-        out[i] = r;
+        stream_store(out + i, r);
     }
 }
 

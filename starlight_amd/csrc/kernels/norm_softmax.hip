@@ -21,12 +21,21 @@ __global__ __launch_bounds__(256) void rms_norm_vec(const float4* __restrict__ x
     __shared__ float scratch[4];
     const uint64_t row = blockIdx.x;
     const float4* xr = x + row * hidden4;
-    float4 v[VPT];
+    float4 v[VPT], g[VPT];
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t c = threadIdx.x + i * 256u;
         v[i] = c < hidden4 ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // the weight row goes out with the input, not after the reduction
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const uint32_t c = threadIdx.x + i * 256u;
+        g[i] = c < hidden4 ? w[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
         ss = fmaf(v[i].x, v[i].x, ss);
         ss = fmaf(v[i].y, v[i].y, ss);
         ss = fmaf(v[i].z, v[i].z, ss);
@@ -39,13 +48,12 @@ __global__ __launch_bounds__(256) void rms_norm_vec(const float4* __restrict__ x
     for (int i = 0; i < VPT; ++i) {
         const uint32_t c = threadIdx.x + i * 256u;
         if (c < hidden4) {
-            const float4 g = w[c];
             float4 r;
-            r.x = (v[i].x * inv) * g.x;
-            r.y = (v[i].y * inv) * g.y;
-            r.z = (v[i].z * inv) * g.z;
-            r.w = (v[i].w * inv) * g.w;
-            orow[c] = r;
+            r.x = (v[i].x * inv) * g[i].x;
+            r.y = (v[i].y * inv) * g[i].y;
+            r.z = (v[i].z * inv) * g[i].z;
+            r.w = (v[i].w * inv) * g[i].w;
+            stream_store(orow + c, r);
         }
     }
 }
@@ -95,7 +103,7 @@ __global__ __launch_bounds__(256) void softmax_regs(const float* __restrict__ x,
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t c = threadIdx.x + i * 256u;
-        if (c < cols) orow[c] = v[i] * inv;  // masked columns: exactly 0
+        if (c < cols) stream_store(orow + c, v[i] * inv);  // masked columns: exactly 0
     }
 }
 

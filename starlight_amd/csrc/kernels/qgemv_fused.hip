@@ -49,6 +49,10 @@ __device__ __forceinline__ void static_for(F&& f) {
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxF4 = 8;  // float4 of activations per thread
+// Bytes between consecutive rows of the limb matrices beyond k: the A
+// operand of a 64-k step reads the same 16-byte columns of several rows,
+// and rows a multiple of the bank width apart would all hit the same banks.
+constexpr uint32_t kLimbPad = 64;
 constexpr uint32_t kMaxElems = kThreads * 4 * kMaxF4;
 // static LDS of the kernel: red, row_val, cfac, wres
 constexpr size_t kStaticLds = sizeof(float) * (kMaxF4 * kWaves + 16 + kMaxElems / 256 + 2 * kWaves * 16 * 16);
@@ -92,7 +96,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     constexpr int PF = BITS == 4 ? 6 : 4;  // superblocks in flight per wave
     constexpr int WPT = kWaves / NT;  // waves per tile
     constexpr uint32_t SB_BYTES = BITS == 4 ? 1024 : 2048;
-    extern __shared__ __align__(16) int8_t limbs[];  // [3][m][k], xsum [m][groups], tres [tiles][16][m]
+    extern __shared__ __align__(16) int8_t limbs[];  // [3][m][k + kLimbPad], xsum [m][units], tres [tiles][16][m]
     __shared__ float red[kMaxF4][kWaves];
     __shared__ float row_val[16];
     __shared__ float cfac[kMaxElems / 256];  // per 256-element chunk: 2^(E-22)
@@ -101,7 +105,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int tid = threadIdx.x, lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, kept in scalar registers
     const uint32_t M = p.m, K = p.k, K4 = K / 4;
-    int* xsum = reinterpret_cast<int*>(limbs + 3 * M * K);
+    const uint32_t RS = K + kLimbPad;  // limb row stride
+    int* xsum = reinterpret_cast<int*>(limbs + 3 * M * RS);
     float* tres = reinterpret_cast<float*>(xsum + M * (K / p.unit));
 
     // ---- this wave's stream: for each block tile j (global tile
@@ -182,7 +187,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     for (int u = 0; u < kMaxF4; ++u) {
         v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (kThreads * u >= total4) continue;  // block-uniform: runs past the input load nothing
-        const uint32_t f = min(tid + kThreads * u, total4 - 1);
+        const uint32_t f = min(static_cast<uint32_t>(tid + kThreads * u), total4 - 1);
         v[u] = reinterpret_cast<const float4*>(p.a)[f];
         if (p.gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(p.gamma)[f % K4];
     }
@@ -277,7 +282,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                                     __builtin_amdgcn_perm(hi23, hi01, 0x05040100u)};
 #pragma unroll
         for (int limb = 0; limb < 3; ++limb)
-            *reinterpret_cast<uint32_t*>(limbs + (limb * M + r) * K + 4 * c4) = packed[limb];
+            *reinterpret_cast<uint32_t*>(limbs + (limb * M + r) * RS + 4 * c4) = packed[limb];
         if (BITS == 4) {
             // unit sums of X (for the offset-binary correction): a unit covers
             // 16, 32 or 64 lanes (one, two or four DPP rows) of this run
@@ -298,9 +303,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     uint32_t a_off;
     if constexpr (LR) {
         const uint32_t row = static_cast<uint32_t>(lane % 16);
-        a_off = (min(row % 4, 2u) * M + min(row / 4, M - 1)) * K;
+        a_off = (min(row % 4, 2u) * M + min(row / 4, M - 1)) * RS;
     } else {
-        a_off = min(static_cast<uint32_t>(lane % 16), M - 1) * K;
+        a_off = min(static_cast<uint32_t>(lane % 16), M - 1) * RS;
     }
     constexpr int NR = LR ? 1 : 4;  // output rows a lane finishes (LR: m = kb4)
     const uint32_t steps_per_unit = p.unit / 64;
@@ -348,8 +353,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bv, fresh ? zero : acc0, 0, 0, 0);
             } else {
                 const v4i a0 = *reinterpret_cast<const v4i*>(ap + st * 64);
-                const v4i a1 = *reinterpret_cast<const v4i*>(ap + M * K + st * 64);
-                const v4i a2 = *reinterpret_cast<const v4i*>(ap + 2 * M * K + st * 64);
+                const v4i a1 = *reinterpret_cast<const v4i*>(ap + M * RS + st * 64);
+                const v4i a2 = *reinterpret_cast<const v4i*>(ap + 2 * M * RS + st * 64);
                 acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bv, acc0, 0, 0, 0);
                 acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bv, acc1, 0, 0, 0);
                 acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bv, acc2, 0, 0, 0);
@@ -506,7 +511,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const uint32_t per_cap = 4096 / (16 * p.m);
     if (per_block > per_cap) per_block = per_cap;
     const uint32_t blocks = (tiles + per_block - 1) / per_block;
-    const size_t lds = static_cast<size_t>(3) * p.m * p.k + sizeof(int) * p.m * (p.k / p.unit) +
+    const size_t lds = static_cast<size_t>(3) * p.m * (p.k + kLimbPad) + sizeof(int) * p.m * (p.k / p.unit) +
                        sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m;
     if (lds + kStaticLds > max_lds_per_block()) return hipErrorNotSupported;
     const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, lr = p.m <= 4;

@@ -58,8 +58,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const float* __restrict__ x, 
             const uint32_t i = i0 + u * blockDim.x;
             if (i >= total) continue;
             const float sine = sc[pr[u]], cosine = sc[half + pr[u]];
-            out[idx0[u]] = first[u] * cosine - second[u] * sine;
-            out[idx1[u]] = first[u] * sine + second[u] * cosine;
+            stream_store(out + idx0[u], first[u] * cosine - second[u] * sine);
+            stream_store(out + idx1[u], first[u] * sine + second[u] * cosine);
         }
     }
 }

@@ -96,7 +96,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     constexpr int PF = BITS == 4 ? 6 : 4;  // superblocks in flight per wave
     constexpr int WPT = kWaves / NT;  // waves per tile
     constexpr uint32_t SB_BYTES = BITS == 4 ? 1024 : 2048;
-    extern __shared__ __align__(16) int8_t limbs[];  // [3][m][k + kLimbPad], xsum [m][units], tres [tiles][16][m]
+    extern __shared__ __align__(16) int8_t limbs[];  // [3][m][k + kLimbPad], tres [tiles][16][m]
     __shared__ float red[kMaxF4][kWaves];
     __shared__ float row_val[16];
     __shared__ float cfac[kMaxElems / 256];  // per 256-element chunk: 2^(E-22)
@@ -106,8 +106,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, kept in scalar registers
     const uint32_t M = p.m, K = p.k, K4 = K / 4;
     const uint32_t RS = K + kLimbPad;  // limb row stride
-    int* xsum = reinterpret_cast<int*>(limbs + 3 * M * RS);
-    float* tres = reinterpret_cast<float*>(xsum + M * (K / p.unit));
+    float* tres = reinterpret_cast<float*>(limbs + 3 * M * RS);
 
     // ---- this wave's stream: for each block tile j (global tile
     // blockIdx.x + j * gridDim.x) the superblocks [sbA, sbA + len); every
@@ -246,9 +245,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // run): the wave that converts a chunk finds its maximum with a DPP
     // reduction, so no block-wide pass is needed. The integer sums are
     // combined per unit of min(group, 256) elements, which never spans two
-    // chunks, each with its chunk's factor 2^(E-22).
-    const uint32_t U = p.unit, seg_lanes = U / 4;  // 16, 32 or 64 lanes per unit
-    const uint32_t chunks = K / 256, units = K / U;
+    // chunks, each with its chunk's factor 2^(E-22) (2^(E-26) for INT4,
+    // whose operands are the signed bytes 16 q).
+    const uint32_t chunks = K / 256;
 #pragma unroll
     for (int u = 0; u < kMaxF4; ++u) {
         const uint32_t fb = static_cast<uint32_t>(wave) * kWave + kThreads * u;
@@ -259,19 +258,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         int ex = 0;
         if (mx != 0.f) frexpf(mx, &ex);  // max|x| < 2^ex
         const int shift = 22 - ex;
-        if (lane == 0) cfac[r * chunks + c4 / 64] = ldexpf(1.0f, ex - 22);
-        // |X| <= 2^22, so X + 0x808080 lies in [0, 2^24) and its bytes b_i
-        // satisfy X = sum (b_i - 128) 256^i: the bytes of
+        if (lane == 0) cfac[r * chunks + c4 / 64] = ldexpf(1.0f, ex - 22 - (BITS == 4 ? 4 : 0));
+        // X from one fma: with |x * 2^shift| <= 2^22, y = x * 2^shift +
+        // 1.5 * 2^23 rounds to an integer (ties to even, as rintf) and
+        // bits(y) = 0x4B400000 + X. X + 0x808080 lies in [0, 2^24) and its
+        // bytes b_i satisfy X = sum (b_i - 128) 256^i, so the bytes of
         // (X + 0x808080) ^ 0x808080 are the three signed limbs; v_perm
-        // gathers byte i of the four elements into limb word i.
+        // gathers byte i of the four elements into limb word i. A chunk
+        // whose 2^shift is not a normal float (max|x| < 2^-105) scales in
+        // two exact steps.
         const float xe[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
         uint32_t y[4];
-        int sx = 0;
+        if (shift <= 127) {  // wave-uniform
+            const float s2 = __uint_as_float(static_cast<uint32_t>(shift + 127) << 23);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int X = static_cast<int>(rintf(ldexpf(xe[e], shift)));
-            y[e] = static_cast<uint32_t>(X + 0x808080) ^ 0x808080u;
-            sx += X;
+            for (int e = 0; e < 4; ++e)
+                y[e] = (__float_as_uint(fmaf(xe[e], s2, 12582912.0f)) - 0x4ABF7F80u) ^ 0x808080u;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float xs = xe[e] * 0x1p127f;  // exact: |x| < 2^-105
+                y[e] = (__float_as_uint(fmaf(xs, ldexpf(1.0f, shift - 127), 12582912.0f)) - 0x4ABF7F80u) ^ 0x808080u;
+            }
         }
         const uint32_t lo01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);  // y0.b0 y1.b0 y0.b1 y1.b1
         const uint32_t lo23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
@@ -283,15 +291,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
         for (int limb = 0; limb < 3; ++limb)
             *reinterpret_cast<uint32_t*>(limbs + (limb * M + r) * RS + 4 * c4) = packed[limb];
-        if (BITS == 4) {
-            // unit sums of X (for the offset-binary correction): a unit covers
-            // 16, 32 or 64 lanes (one, two or four DPP rows) of this run
-            const int rs = row_sum(sx);
-            const int r0 = __builtin_amdgcn_readlane(rs, 0), r1 = __builtin_amdgcn_readlane(rs, 16);
-            const int r2 = __builtin_amdgcn_readlane(rs, 32), r3 = __builtin_amdgcn_readlane(rs, 48);
-            const int usum = seg_lanes == 16 ? rs : seg_lanes == 32 ? (lane < 32 ? r0 + r1 : r2 + r3) : r0 + r1 + r2 + r3;
-            if (lane % seg_lanes == 0) xsum[r * units + (4 * c4) / U] = usum;
-        }
     }
     __syncthreads();
 
@@ -335,10 +334,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             if (BITS == 4) {
                 const uint32_t wa = st == 0 ? cur.c0.x : cur.c0.z;
                 const uint32_t wb = st == 0 ? cur.c0.y : cur.c0.w;
-                bv[0] = static_cast<int>(wa & 0x0F0F0F0Fu);
-                bv[1] = static_cast<int>((wa >> 4) & 0x0F0F0F0Fu);
-                bv[2] = static_cast<int>(wb & 0x0F0F0F0Fu);
-                bv[3] = static_cast<int>((wb >> 4) & 0x0F0F0F0Fu);
+                // two's complement nibbles -> the signed bytes 16 q
+                bv[0] = static_cast<int>((wa << 4) & 0xF0F0F0F0u);
+                bv[1] = static_cast<int>(wa & 0xF0F0F0F0u);
+                bv[2] = static_cast<int>((wb << 4) & 0xF0F0F0F0u);
+                bv[3] = static_cast<int>(wb & 0xF0F0F0F0u);
             } else {
                 const uint4 cw = st == 0 ? cur.c0 : cur.c1;
                 bv[0] = static_cast<int>(cw.x);
@@ -367,7 +367,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 if constexpr (SPG == 0) gstep = 0;
                 if constexpr (SPG == 1) gi = 2 * sbi + st;
                 if constexpr (SPG == 2) gi = sbi;
-                const uint32_t gix = min(gi, units - 1);
                 const float sc = GPS == 2 && st == 1 ? cur.s1 : cur.s0;
                 const uint32_t chunk = (sbi * 128 + st * 64) / 256;
                 if constexpr (LR) {
@@ -375,7 +374,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                     const uint32_t m = min(kb4, M - 1);
                     float val = fmaf(static_cast<float>(acc0[2]), 65536.0f,
                                      fmaf(static_cast<float>(acc0[1]), 256.0f, static_cast<float>(acc0[0])));
-                    if (BITS == 4) val -= 8.0f * static_cast<float>(xsum[m * units + gix]);
                     const float t = fmaf(val * cfac[m * chunks + chunk], sc, total[0]);
                     total[0] = use ? t : total[0];
                 } else {
@@ -384,7 +382,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                         const uint32_t m = min(kb4 * 4 + r, M - 1);
                         float val = fmaf(static_cast<float>(acc2[r]), 65536.0f,
                                          fmaf(static_cast<float>(acc1[r]), 256.0f, static_cast<float>(acc0[r])));
-                        if (BITS == 4) val -= 8.0f * static_cast<float>(xsum[m * units + gix]);
                         const float t = fmaf(val * cfac[m * chunks + chunk], sc, total[r]);
                         total[r] = use ? t : total[r];
                     }
@@ -511,7 +508,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const uint32_t per_cap = 4096 / (16 * p.m);
     if (per_block > per_cap) per_block = per_cap;
     const uint32_t blocks = (tiles + per_block - 1) / per_block;
-    const size_t lds = static_cast<size_t>(3) * p.m * (p.k + kLimbPad) + sizeof(int) * p.m * (p.k / p.unit) +
+    const size_t lds = static_cast<size_t>(3) * p.m * (p.k + kLimbPad) +
                        sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m;
     if (lds + kStaticLds > max_lds_per_block()) return hipErrorNotSupported;
     const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, lr = p.m <= 4;

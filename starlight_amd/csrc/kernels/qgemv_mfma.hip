@@ -17,10 +17,10 @@
 // 16-row tile nt and 128-k superblock sb, one contiguous block in which lane l
 // of a wave finds exactly its MFMA B operand for both 64-k steps:
 //   INT4: 1024 bytes, lane l owns bytes [16l, 16l + 16): 8 bytes per step;
-//         codes stored offset-binary (u = q + 8) and arranged so that
-//         w & 0x0F0F0F0F and (w >> 4) & 0x0F0F0F0F give the operand bytes in
-//         k order; the +8 offset is removed exactly with a per-group
-//         integer correction 8 * sum_k X.
+//         codes stored as 4-bit two's complement and arranged so that
+//         (w << 4) & 0xF0F0F0F0 and w & 0xF0F0F0F0 give the operand bytes
+//         in k order, each the signed byte 16 q; the factor 16 is exact and
+//         folded into the final 2^(E-22) scaling.
 //   INT8: 2048 bytes, step s at 1024 s, lane l owns bytes [16l, 16l + 16).
 // Operand k order within a step: lane l holds k = 16 (l / 16) + j, j < 16,
 // for row l % 16 — identical for A and B, which is all the product needs.
@@ -65,7 +65,6 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
     extern __shared__ __align__(16) int8_t limbs[];  // [3][m][kslice]
     __shared__ uint32_t max_bits[16];
     __shared__ int exps[16];
-    __shared__ int xsum[16 * 64];    // [m][group in split]: sum of X, for the INT4 offset correction
 
     const int tid = threadIdx.x;
     const int lane = tid % kWave, wave = tid / kWave;
@@ -74,7 +73,7 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
     const uint32_t sb1 = min(sb0 + p.sb_per_split, p.sb_total);
     const uint32_t kslice = p.sb_per_split * 128;
     const uint32_t k0 = sb0 * 128, klen = (sb1 - sb0) * 128;
-    const uint32_t g0 = k0 / p.group, gcount = klen / p.group;
+    const uint32_t g0 = k0 / p.group;
     const uint32_t M = p.m;
 
     // ---- the wave's weight stream: a rolling window of kPrefetch
@@ -100,7 +99,6 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
     // ---- prologue: the activation slice as exact int8 limbs in LDS ----
     // (float4 loads, four in flight per thread per pass)
     if (tid < 16) max_bits[tid] = 0u;
-    for (uint32_t i = tid; i < M * gcount; i += 256) xsum[i] = 0;
     __syncthreads();
     const uint32_t q4 = klen / 4;  // float4 per row slice
     for (uint32_t m = 0; m < M; ++m) {
@@ -124,8 +122,6 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
         exps[tid] = e;  // max|x| < 2^e
     }
     __syncthreads();
-    // lanes whose 4-element runs share a group (group is a multiple of 64)
-    const int seg = p.group / 4 < kWave ? static_cast<int>(p.group / 4) : kWave;
     for (uint32_t m = 0; m < M; ++m) {
         const float4* xr = reinterpret_cast<const float4*>(p.a + static_cast<uint64_t>(m) * p.k + k0);
         const int shift = 22 - exps[m];
@@ -141,7 +137,6 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
                 const uint32_t f = f0 + tid + 256 * u;
                 if (f0 + (tid & ~(kWave - 1)) + 256 * u >= q4) continue;  // whole wave out of range
                 const float xe[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-                int sx = 0;
                 uint32_t packed[3] = {0u, 0u, 0u};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -153,16 +148,11 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
                     packed[0] |= (static_cast<uint32_t>(l0) & 0xFFu) << (8 * e);
                     packed[1] |= (static_cast<uint32_t>(l1) & 0xFFu) << (8 * e);
                     packed[2] |= (static_cast<uint32_t>(l2) & 0xFFu) << (8 * e);
-                    sx += X;
                 }
                 if (f < q4) {
 #pragma unroll
                     for (int limb = 0; limb < 3; ++limb)
                         *reinterpret_cast<uint32_t*>(limbs + (limb * M + m) * kslice + 4 * f) = packed[limb];
-                }
-                if (BITS == 4) {
-                    for (int off = seg / 2; off > 0; off >>= 1) sx += __shfl_xor(sx, off, kWave);
-                    if (f < q4 && lane % seg == 0) atomicAdd(&xsum[m * gcount + (4 * f) / p.group], sx);
                 }
             }
         }
@@ -204,10 +194,10 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
                     if (BITS == 4) {
                         const uint32_t wa = s == 0 ? c0.x : c0.z;
                         const uint32_t wb = s == 0 ? c0.y : c0.w;
-                        bv[0] = static_cast<int>(wa & 0x0F0F0F0Fu);
-                        bv[1] = static_cast<int>((wa >> 4) & 0x0F0F0F0Fu);
-                        bv[2] = static_cast<int>(wb & 0x0F0F0F0Fu);
-                        bv[3] = static_cast<int>((wb >> 4) & 0x0F0F0F0Fu);
+                        bv[0] = static_cast<int>((wa << 4) & 0xF0F0F0F0u);
+                        bv[1] = static_cast<int>(wa & 0xF0F0F0F0u);
+                        bv[2] = static_cast<int>((wb << 4) & 0xF0F0F0F0u);
+                        bv[3] = static_cast<int>(wb & 0xF0F0F0F0u);
                     } else {
                         const uint4 cw = s == 0 ? c0 : c1;
                         bv[0] = static_cast<int>(cw.x);
@@ -235,7 +225,6 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
                             const uint32_t m = kb4 * 4 + r;
                             float v = fmaf(static_cast<float>(acc2[r]), 65536.0f,
                                            fmaf(static_cast<float>(acc1[r]), 256.0f, static_cast<float>(acc0[r])));
-                            if (BITS == 4 && m < M) v -= 8.0f * static_cast<float>(xsum[m * gcount + gl]);
                             total[r] = fmaf(v, sc, total[r]);
                         }
                         acc0 = zero;
@@ -252,7 +241,7 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
     for (int r = 0; r < 4; ++r) {
         const uint32_t m = kb4 * 4 + r;
         if (!tile_live || m >= M || row >= p.n) continue;
-        const float v = ldexpf(total[r], exps[m] - 22);
+        const float v = ldexpf(total[r], exps[m] - 22 - (BITS == 4 ? 4 : 0));  // INT4 operands are 16 q
         if (p.splits == 1) p.out[static_cast<uint64_t>(m) * p.n + row] = v;
         else p.partial[(static_cast<uint64_t>(split) * M + m) * p.n + row] = v;
     }

@@ -129,8 +129,8 @@ __device__ __forceinline__ float decode(const uint8_t* tiles, uint32_t bits, uin
         const uint32_t j = c % 16;
         if (bits == 4) {
             const uint8_t byte = tiles[(nt * sb_total + sb) * 1024 + lane * 16 + s * 8 + (j < 8 ? 0 : 4) + (j & 3)];
-            const int u = (j & 4) ? byte >> 4 : byte & 0x0F;
-            return static_cast<float>(u - 8);
+            const int u = (j & 4) ? byte >> 4 : byte & 0x0F;  // two's complement nibble
+            return static_cast<float>(u >= 8 ? u - 16 : u);
         }
         return static_cast<float>(
             static_cast<int8_t>(tiles[(nt * sb_total + sb) * 2048 + s * 1024 + lane * 16 + j]));
@@ -170,7 +170,8 @@ __global__ void repack_mfma(const uint8_t* __restrict__ payload, uint32_t* __res
             for (uint32_t jj = 0; jj < 8; ++jj) {
                 const uint32_t j = half * 8 + jj;
                 const uint64_t c = sb * 128 + s * 64 + (lane / 16) * 16 + j;
-                const uint32_t u = r < n ? static_cast<uint32_t>(payload_code(payload, 4, k, r, c) + 8) : 8u;
+                // two's complement nibble; rows past n are zero
+                const uint32_t u = r < n ? static_cast<uint32_t>(payload_code(payload, 4, k, r, c)) & 0xFu : 0u;
                 const uint32_t nib = jj < 4 ? 2 * jj : 2 * (jj - 4) + 1;
                 out |= (u & 0xF) << (4 * nib);
             }

@@ -578,14 +578,26 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
         mh = &c[6];
         used = 7;
     }
-    // The split and rotated heads must be dead: each is scanned from the
-    // command after its last reader inside the unit, so the unit's own later
-    // writes (the attention output, MergeHeads) count as overwrites.
-    const sl_buffer_ref skipped[5] = {sq.out, sk.out, sv.out, rq.out, rk.out};
-    const size_t after_reader[5] = {i + 4, i + 5, i + 6, i + 6, i + 6};
-    for (int x = 0; x < 5; ++x)
-        if (!dead_after(d, after_reader[x], skipped[x])) return 0;
+    // The split and rotated heads are written only when a later command reads
+    // them: each is scanned from the command after its last reader inside the
+    // unit, so the unit's own later writes (the attention output, MergeHeads)
+    // count as overwrites. The decode kernel writes a live one, so it must
+    // not overlap anything that kernel reads or another live one; the
+    // attention output and MergeHeads come from the merge kernel after it,
+    // which keeps the op order where they overlap.
     const sl_buffer_ref& cache = at.in[ap.state_index];
+    const sl_buffer_ref inter[5] = {sq.out, sk.out, sv.out, rq.out, rk.out};
+    const size_t after_reader[5] = {i + 4, i + 5, i + 6, i + 6, i + 6};
+    bool live[5];
+    for (int x = 0; x < 5; ++x) {
+        live[x] = !dead_after(d, after_reader[x], inter[x]);
+        if (!live[x]) continue;
+        const sl_buffer_ref read[5] = {sq.in[0], sk.in[0], sv.in[0], cache, rq.in[1]};
+        for (const sl_buffer_ref& t : read)
+            if (overlaps(inter[x], t)) return 0;
+        for (int y = 0; y < x; ++y)
+            if (live[y] && overlaps(inter[x], inter[y])) return 0;
+    }
     const sl_buffer_ref att = at.out;
     const bool att_dead = mh != nullptr && dead_after(d, i + used, att);
     // the projection chained below reads the mirror, not MergeHeads' output
@@ -606,6 +618,9 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
     a.theta = rq.plan.theta;
     a.rope_variant = rq.plan.rope_variant;
     a.merged = merged_needed ? fptr(d, mh->out) : nullptr;
+    float** const inter_ptr[5] = {&a.q_split, &a.k_split, &a.v_split, &a.q_rot, &a.k_rot};
+    for (int x = 0; x < 5; ++x)
+        if (live[x]) *inter_ptr[x] = fptr(d, inter[x]);
 
     // the output projection (and its residual Add) reading the mirror
     const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};

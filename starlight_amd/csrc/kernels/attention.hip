@@ -47,6 +47,11 @@ struct Geo {
     uint32_t rope_variant;
     float* merged;
     float* mirror;
+    float* q_split;  // fused form: intermediates a later command reads, or null
+    float* k_split;
+    float* v_split;
+    float* q_rot;
+    float* k_rot;
 };
 
 __device__ __forceinline__ uint32_t past_of(const Geo& g) { return g.dyn != nullptr ? g.dyn[0] : g.past_len; }
@@ -175,6 +180,13 @@ __device__ __forceinline__ float4 f4_fma(float a, float4 x, float4 y) {
 
 __device__ __forceinline__ float4 f4_scale(float4 x, float a) { return make_float4(x.x * a, x.y * a, x.z * a, x.w * a); }
 
+__device__ __forceinline__ void put4(float* p, float4 v) {
+    p[0] = v.x;
+    p[1] = v.y;
+    p[2] = v.z;
+    p[3] = v.w;
+}
+
 // Folds state (mo, lo, ao) into (m, l, a); an empty state has m == -inf.
 template <int DV>
 __device__ __forceinline__ void fold_state(float& m, float& l, float4 (&a)[DV], float mo, float lo,
@@ -279,11 +291,21 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
         const uint32_t i = tid + 256 * u;
         if (i < RT * D4) qs[i] = i / D4 < R ? qv[u] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    // the query rows of this KV head in SplitHeads layout [B, H, S, D]
+    // (element stores: the buffers may sit at any offset)
+    auto put_q_rows = [&](float* dst) {
+        for (uint32_t i = tid; i < R * D4; i += 256) {
+            const uint32_t r = i / D4, c = i % D4, t = r % S;
+            const uint64_t h = kvh * G + r / S;
+            put4(dst + ((b * g.heads + h) * S + t) * (4 * D4) + 4 * c, qs[i]);
+        }
+    };
     if constexpr (FUSED) {
         // Rope of the query rows, in LDS
         constexpr uint32_t D = 4 * D4;
         rope_table(g, b, S, D, sc);
         __syncthreads();
+        if (p == 0 && g.q_split != nullptr) put_q_rows(g.q_split);
         if (g.rope_variant == SL_ROPE_NEOX) {
             for (uint32_t i = tid; i < R * (D4 / 2); i += 256) {  // four pairs (d, d + D/2) per item
                 const uint32_t r = i / (D4 / 2), c = i % (D4 / 2);
@@ -306,6 +328,8 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
                 qs[r * D4 + c] = x;
             }
         }
+        __syncthreads();
+        if (p == 0 && g.q_rot != nullptr) put_q_rows(g.q_rot);
     }
     __syncthreads();
 
@@ -331,6 +355,16 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
         for (int kb = 0; kb < kDecodeKeys; ++kb) {
             const uint32_t j = j0 + kb;
             if (j >= past && j < keys) {
+                // the new row in SplitHeads / Rope layout [B, Hkv, S, D]
+                const uint64_t split_row = ((b * g.kv_heads + kvh) * S + (j - past)) * (4 * D4);
+                if (FUSED && g.k_split != nullptr) {
+#pragma unroll
+                    for (int u = 0; u < DV; ++u) put4(g.k_split + split_row + 4 * (li + 16 * u), kv[kb][u]);
+                }
+                if (FUSED && g.v_split != nullptr) {
+#pragma unroll
+                    for (int u = 0; u < DV; ++u) put4(g.v_split + split_row + 4 * (li + 16 * u), vv[kb][u]);
+                }
                 if constexpr (FUSED) {
                     // Rope of a new key row before it is used and appended
                     constexpr uint32_t D = 4 * D4;
@@ -355,6 +389,10 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
                             rotate(x.z, x.w, st[pr + 1], st[D / 2 + pr + 1]);
                         }
                     }
+                }
+                if (FUSED && g.k_rot != nullptr) {
+#pragma unroll
+                    for (int u = 0; u < DV; ++u) put4(g.k_rot + split_row + 4 * (li + 16 * u), kv[kb][u]);
                 }
 #pragma unroll
                 for (int u = 0; u < DV; ++u) {
@@ -664,6 +702,11 @@ Geo make_geo(const AttentionArgs& a, const Workspace& ws) {
     g.rope_variant = a.rope_variant;
     g.merged = a.merged;
     g.mirror = a.mirror;
+    g.q_split = a.q_split;
+    g.k_split = a.k_split;
+    g.v_split = a.v_split;
+    g.q_rot = a.q_rot;
+    g.k_rot = a.k_rot;
     return g;
 }
 

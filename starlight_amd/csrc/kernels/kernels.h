@@ -86,6 +86,14 @@ struct AttentionArgs {
     uint32_t rope_variant = 0;
     float* merged = nullptr;
     float* mirror = nullptr;
+    // Fused form, when a later command reads them: the SplitHeads outputs
+    // [batch, heads, seq, head_dim] of q / k / v and the Rope outputs of q / k
+    // (same layout), each written when non-null.
+    float* q_split = nullptr;
+    float* k_split = nullptr;
+    float* v_split = nullptr;
+    float* q_rot = nullptr;
+    float* k_rot = nullptr;
 };
 // Appends k_new / v_new to the cache and computes the attention output.
 hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStream_t s);

@@ -1,12 +1,14 @@
 """Fused submission units on the GPU, against the oracle run op by op.
 
 The device fuses SplitHeads x3 + Rope x2 + CausalAttention + MergeHeads into
-the decode attention kernels when the split and rotated heads are dead (every
-element overwritten by a later command of the same submission before any
-read). These tests lay the values out in one scratch buffer, make the
-intermediates dead with a later Scale over their region, and check the
-attention output, the merged heads and the KV cache; a variant where a later
-command reads an intermediate must run unfused and still match.
+the decode attention kernels. The split and rotated heads are written only
+when a later command of the same submission reads them (dead ones, every
+element overwritten before any read, are skipped). These tests lay the values
+out in one scratch buffer, make the intermediates dead with a later Scale over
+their region, and check the attention output, the merged heads and the KV
+cache; variants where a later command reads an intermediate, or where nothing
+overwrites them, must fuse as well and leave every intermediate as the op
+sequence would.
 """
 import math
 
@@ -29,7 +31,7 @@ CASES = [
 ]
 
 
-def run_group(hip, case, consume_intermediate):
+def run_group(hip, case, consume_intermediate, keep_all=False):
     B, H, Hkv, S, past, D, max_seq, variant = case
     r = np.random.default_rng(sum(case[:-1]))
     nq, nk = B * S * H * D, B * S * Hkv * D
@@ -84,8 +86,9 @@ def run_group(hip, case, consume_intermediate):
     if consume_intermediate:
         # a later read of qr keeps it alive: the group must run unfused
         hip.dispatch(Op.scale_by(2.0), [ref["qr"]], [q4], [BufferRef(extra, 0, nq)], [q4])
-    # overwrite the split / rotated heads: they are dead after the group
-    hip.dispatch(Op.scale_by(3.0), [BufferRef(src, 0, inter_hi - inter_lo)], [sv], [span], [sv])
+    if not keep_all:
+        # overwrite the split / rotated heads: they are dead after the group
+        hip.dispatch(Op.scale_by(3.0), [BufferRef(src, 0, inter_hi - inter_lo)], [sv], [span], [sv])
     hip.synchronize()
     after = hip.stats()
 
@@ -103,7 +106,16 @@ def run_group(hip, case, consume_intermediate):
     assert_normwise(got[o:o + n], want_att)
     o, n = offs["merged"]
     assert_normwise(got[o:o + n], want_merged)
-    assert np.all(got[inter_lo:inter_hi] == 3.0)
+    if keep_all:
+        # nothing overwrites them: every intermediate holds the op's result
+        for name, want in (("qh", qh), ("kh", kh), ("vh", vh)):
+            o, n = offs[name]
+            np.testing.assert_array_equal(got[o:o + n], want)
+        for name, want in (("qr", qr), ("kr", kr)):
+            o, n = offs[name]
+            assert rel_l2(got[o:o + n], want) <= 1e-6, name
+    else:
+        assert np.all(got[inter_lo:inter_hi] == 3.0)
     assert rel_l2(got_cache, want_cache) <= 1e-6
     if extra is not None:
         np.testing.assert_array_equal(hip.read_f32(extra, nq), (qr * np.float32(2.0)).astype(np.float32))
@@ -120,6 +132,18 @@ def test_attention_group_fuses_and_matches(hip, case):
         assert fused >= 7
 
 
+def fusable(case):
+    B, H, Hkv, S, past, D, max_seq, variant = case
+    return not (variant == RopeVariant.NEOX and (D // 64) % 2)
+
+
 @pytest.mark.parametrize("case", CASES[:2])
-def test_attention_group_with_live_intermediate_runs_unfused(hip, case):
-    assert run_group(hip, case, consume_intermediate=True) == 0
+def test_attention_group_with_live_intermediate_fuses_and_writes_it(hip, case):
+    fused = run_group(hip, case, consume_intermediate=True)
+    assert fused >= 7 if fusable(case) else fused == 0
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_attention_group_keeps_every_live_intermediate(hip, case):
+    fused = run_group(hip, case, consume_intermediate=False, keep_all=True)
+    assert fused >= 7 if fusable(case) else fused == 0

@@ -46,6 +46,7 @@ namespace {
 
 constexpr uint64_t kMirrorMaxElements = 1ull << 22;        // host copy of u32 buffers up to 16 MiB
 constexpr uint64_t kWorkspaceBytes = 512ull << 20;          // split-K partials, SwiGlu intermediates
+constexpr uint64_t kRopeTableFloats = 16 * 512;  // tokens x head_dim of one decode submission
 constexpr uint64_t kCounterWords = 1ull << 16;              // cross-block completion counters (kept at zero)
 constexpr uint64_t kIdScratchElements = 1ull << 20;         // host scratch for unmirrored id checks
 
@@ -103,6 +104,16 @@ struct Device : BufferView {
     std::vector<GraphEntry> graphs;
     uint64_t use_clock = 0;
     sl_hip_stats stats{};
+    // Rope sine / cosine table shared by the fused attention units of a
+    // submission (one per step: every layer rotates at the same positions)
+    float* rope_tab = nullptr;
+    struct {
+        bool valid = false;
+        sl_buffer_ref pos{};
+        float theta = 0.f;
+        uint64_t head_dim = 0, tokens = 0;
+        size_t at = 0;  // log index where it was computed
+    } rope;
 
     size_t count() const override { return buffers.size(); }
     const sl_buffer_desc* get(uint32_t id) const override {
@@ -618,6 +629,30 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
     a.theta = rq.plan.theta;
     a.rope_variant = rq.plan.rope_variant;
     a.merged = merged_needed ? fptr(d, mh->out) : nullptr;
+    // the Rope table: computed once per submission for these positions,
+    // again only if a command since has written the positions buffer
+    const uint64_t tokens = B * S;
+    if (tokens * D <= kRopeTableFloats) {
+        auto& rt = d->rope;
+        bool fresh = rt.valid && same_ref(rt.pos, rq.in[1]) && rt.theta == rq.plan.theta && rt.head_dim == D &&
+                     rt.tokens == tokens;
+        for (size_t x = rt.at; fresh && x < i; ++x)
+            if (overlaps(d->log[x].out, rt.pos)) fresh = false;
+        if (!fresh) {
+            const hipError_t te = launch_rope_sincos(a.positions, tokens, D, rq.plan.theta, d->rope_tab, d->stream);
+            if (te != hipSuccess) {
+                *err = te;
+                return 1;
+            }
+            rt.valid = true;
+            rt.pos = rq.in[1];
+            rt.theta = rq.plan.theta;
+            rt.head_dim = D;
+            rt.tokens = tokens;
+            rt.at = i;
+        }
+        a.rope_table = d->rope_tab;
+    }
     float** const inter_ptr[5] = {&a.q_split, &a.k_split, &a.v_split, &a.q_rot, &a.k_rot};
     for (int x = 0; x < 5; ++x)
         if (live[x]) *inter_ptr[x] = fptr(d, inter[x]);
@@ -667,6 +702,7 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
 }
 
 hipError_t run_log(Device* d) {
+    d->rope.valid = false;
     for (size_t i = 0; i < d->log.size();) {
         size_t used = 0;
         hipError_t e = hipSuccess;
@@ -855,6 +891,13 @@ sl_status sl_hip_device_create(int ordinal, sl_hip_device** out) {
         delete d;
         return SL_ERR_OUT_OF_MEMORY;
     }
+    if (hipMalloc(reinterpret_cast<void**>(&d->rope_tab), slhip::kRopeTableFloats * 4) != hipSuccess) {
+        (void)hipFree(d->counters);
+        (void)hipFree(d->workspace);
+        (void)hipStreamDestroy(d->stream);
+        delete d;
+        return SL_ERR_OUT_OF_MEMORY;
+    }
     d->id_scratch.resize(slhip::kIdScratchElements);
     *out = d;
     return SL_OK;
@@ -873,6 +916,7 @@ void sl_hip_device_destroy(sl_hip_device* d) {
     }
     if (d->workspace) (void)hipFree(d->workspace);
     if (d->counters) (void)hipFree(d->counters);
+    if (d->rope_tab) (void)hipFree(d->rope_tab);
     (void)hipStreamDestroy(d->stream);
     delete d;
 }

@@ -52,6 +52,7 @@ struct Geo {
     float* v_split;
     float* q_rot;
     float* k_rot;
+    const float* rope_tab;  // fused form: the sine / cosine table, or null
 };
 
 __device__ __forceinline__ uint32_t past_of(const Geo& g) { return g.dyn != nullptr ? g.dyn[0] : g.past_len; }
@@ -222,6 +223,18 @@ __device__ __forceinline__ void rope_table(const Geo& g, uint64_t b, uint32_t S,
     }
 }
 
+__global__ __launch_bounds__(256) void rope_sincos(const uint32_t* __restrict__ pos, uint32_t tokens, uint32_t D,
+                                                   double theta, float* __restrict__ table) {
+    const uint32_t half = D / 2;
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= tokens * half) return;
+    const uint32_t t = i / half, pair = i % half;
+    const double position = static_cast<double>(pos[t]);
+    const double angle = position / pow(theta, 2.0 * static_cast<double>(pair) / static_cast<double>(D));
+    table[t * D + pair] = static_cast<float>(sin(angle));
+    table[t * D + half + pair] = static_cast<float>(cos(angle));
+}
+
 template <int DV, int RT, bool FUSED>
 __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     constexpr int D4 = 16 * DV;  // float4 per row
@@ -303,7 +316,11 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     if constexpr (FUSED) {
         // Rope of the query rows, in LDS
         constexpr uint32_t D = 4 * D4;
-        rope_table(g, b, S, D, sc);
+        if (g.rope_tab != nullptr) {
+            for (uint32_t i = tid; i < S * D; i += 256) sc[i] = g.rope_tab[b * S * D + i];
+        } else {
+            rope_table(g, b, S, D, sc);
+        }
         __syncthreads();
         if (p == 0 && g.q_split != nullptr) put_q_rows(g.q_split);
         if (g.rope_variant == SL_ROPE_NEOX) {
@@ -505,23 +522,36 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     }
 }
 
-// Merges the P partials of one (KV head, batch): grid (kv_heads, batch).
-// Each wave turns the (m, l) of a query row over all partials into weights
-// exp(m_p - max) / sum; then threads own float4 output slots, several threads
-// per slot when there are few, and sum their share of the partials with all
-// loads of a batch of eight in flight.
+// Merges the P partials of one query row of a KV head: grid (kv_heads * R,
+// batch), R = group * seq rows per KV head. Threads own float4 output slots,
+// T = 256 / (head_dim / 4) threads per slot, each over every T-th partial;
+// all of a thread's partial rows are loaded before the weights exp(m_p -
+// max) / sum are worked out (one wave, from the (m, l) of every partial), so
+// both wait on one memory round trip. The T sums of a slot are added in LDS
+// in thread order.
 constexpr int kMergeMaxParts = 64;
 
 __global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
-    __shared__ float coef[kMergeMaxParts][kDecodeMaxRows];
+    __shared__ float coef[kMergeMaxParts];
     __shared__ float4 red[256];
     const uint32_t D4 = g.head_dim / 4, S = g.seq, G = g.group, R = G * S;
-    const uint32_t kvh = blockIdx.x;
+    const uint32_t kvh = blockIdx.x / R, r = blockIdx.x % R;
     const uint64_t b = blockIdx.y;
-    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int tid = threadIdx.x, lane = tid % kWave;
     const uint64_t row_stride = kDecodePartStride + 4 * D4;
     const float* base = g.ws + (b * g.kv_heads + kvh) * P * R * row_stride;
-    for (uint32_t r = wave; r < R; r += 4) {
+    const uint32_t T = 256 / D4;  // threads per slot: 4 .. 16
+    const uint32_t c = tid % D4, q = tid / D4;  // q >= T (head_dim 192): idle
+    const bool mine = q < T;
+    constexpr int kPer = kMergeMaxParts / 4;  // partials per thread at most
+    float4 v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const uint32_t pp = q + u * T;
+        v[u] = mine && pp < P ? reinterpret_cast<const float4*>(base + (pp * R + r) * row_stride + kDecodePartStride)[c]
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (tid < kWave) {
         const bool on = static_cast<uint32_t>(lane) < P;
         const float* pr = base + (static_cast<uint64_t>(on ? lane : 0) * R + r) * row_stride;
         const float mp = on ? pr[0] : -INFINITY;
@@ -529,52 +559,32 @@ __global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
         const float mx = wave_max(mp);
         const float e = mp == -INFINITY ? 0.f : expf(mp - mx);
         const float total = wave_sum(lp * e);
-        if (on) coef[lane][r] = e / total;
+        if (on) coef[lane] = e / total;
     }
     __syncthreads();
-    const uint32_t slots = R * D4;
-    const uint32_t T = slots >= 256 ? 1 : 256 / slots;  // threads per slot
-    const uint32_t q = tid / slots;
-    for (uint32_t slot = tid % slots; slot < slots; slot += 256) {
-        const uint32_t r = slot / D4, c = slot % D4;
-        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (q < T) {
-            for (uint32_t p0 = q; p0 < P; p0 += 8 * T) {
-                float4 v[8];
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const uint32_t pp = p0 + u * T;
-                    v[u] = pp < P ? reinterpret_cast<const float4*>(base + (pp * R + r) * row_stride +
-                                                                    kDecodePartStride)[c]
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const uint32_t pp = p0 + u * T;
-                    if (pp < P) a = f4_fma(coef[pp][r], v[u], a);
-                }
-            }
-        }
-        if (T > 1) {
-            red[tid] = a;
-            __syncthreads();
-            if (q == 0) {
-                for (uint32_t o = 1; o < T; ++o) {
-                    const float4 x = red[tid + o * slots];
-                    a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
-                }
-            }
-        }
-        if (q == 0 || T == 1) {
-            const uint32_t gi = r / S, t = r % S;
-            const uint64_t h = kvh * G + gi;
-            if (g.out != nullptr) reinterpret_cast<float4*>(g.out + ((b * g.heads + h) * S + t) * (4 * D4))[c] = a;
-            // MergeHeads layout [B, S, H * D] (reference/layout.rs merge_heads)
-            const uint64_t mrow = (b * S + t) * g.heads + h;
-            if (g.merged != nullptr) reinterpret_cast<float4*>(g.merged + mrow * (4 * D4))[c] = a;
-            if (g.mirror != nullptr) reinterpret_cast<float4*>(g.mirror + mrow * (4 * D4))[c] = a;
-        }
+    for (int u = 0; u < kPer; ++u) {
+        const uint32_t pp = q + u * T;
+        if (mine && pp < P) a = f4_fma(coef[pp], v[u], a);
     }
+    red[tid] = a;
+    __syncthreads();
+    if (q != 0) return;
+    for (uint32_t o = 1; o < T; ++o) {
+        const float4 x = red[tid + o * D4];
+        a.x += x.x;
+        a.y += x.y;
+        a.z += x.z;
+        a.w += x.w;
+    }
+    const uint32_t gi = r / S, t = r % S;
+    const uint64_t h = kvh * G + gi;
+    if (g.out != nullptr) reinterpret_cast<float4*>(g.out + ((b * g.heads + h) * S + t) * (4 * D4))[c] = a;
+    // MergeHeads layout [B, S, H * D] (reference/layout.rs merge_heads)
+    const uint64_t mrow = (b * S + t) * g.heads + h;
+    if (g.merged != nullptr) reinterpret_cast<float4*>(g.merged + mrow * (4 * D4))[c] = a;
+    if (g.mirror != nullptr) reinterpret_cast<float4*>(g.mirror + mrow * (4 * D4))[c] = a;
 }
 
 constexpr int kTileQ = 64;  // queries per block
@@ -707,6 +717,7 @@ Geo make_geo(const AttentionArgs& a, const Workspace& ws) {
     g.v_split = a.v_split;
     g.q_rot = a.q_rot;
     g.k_rot = a.k_rot;
+    g.rope_tab = a.rope_table;
     return g;
 }
 
@@ -751,12 +762,22 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
         default: SL_DECODE(4, 8); break;
     }
 #undef SL_DECODE
-    attn_decode_merge<<<dim3(g.kv_heads, static_cast<unsigned>(a.batch)), 256, 0, s>>>(
+    attn_decode_merge<<<dim3(g.kv_heads * static_cast<unsigned>(rows), static_cast<unsigned>(a.batch)), 256, 0, s>>>(
         g, static_cast<uint32_t>(parts));
     return hipGetLastError();
 }
 
 }  // namespace
+
+hipError_t launch_rope_sincos(const uint32_t* positions, uint64_t tokens, uint64_t head_dim, float theta,
+                              float* table, hipStream_t s) {
+    if (tokens == 0) return hipSuccess;
+    if (head_dim % 2 != 0 || tokens * head_dim > 0xffffffffull) return hipErrorInvalidValue;
+    const uint64_t n = tokens * (head_dim / 2);
+    rope_sincos<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(
+        positions, static_cast<uint32_t>(tokens), static_cast<uint32_t>(head_dim), static_cast<double>(theta), table);
+    return hipGetLastError();
+}
 
 uint64_t attention_workspace_floats(const AttentionArgs& a) {
     const uint64_t rows = a.heads / (a.kv_heads ? a.kv_heads : 1) * a.seq;

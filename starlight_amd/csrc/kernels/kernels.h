@@ -94,7 +94,15 @@ struct AttentionArgs {
     float* v_split = nullptr;
     float* q_rot = nullptr;
     float* k_rot = nullptr;
+    // Fused form: the Rope sine / cosine table of these positions
+    // (launch_rope_sincos), or null to compute it in every block.
+    const float* rope_table = nullptr;
 };
+// Rope angles' sine and cosine for `tokens` positions: table[t * head_dim +
+// pair] = sin, table[t * head_dim + head_dim / 2 + pair] = cos, from f64
+// pow / sin / cos rounded once (reference/rope.rs:32-35).
+hipError_t launch_rope_sincos(const uint32_t* positions, uint64_t tokens, uint64_t head_dim, float theta,
+                              float* table, hipStream_t s);
 // Appends k_new / v_new to the cache and computes the attention output.
 hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStream_t s);
 // SplitHeads x3 + Rope x2 + CausalAttention (+ MergeHeads) as the two decode

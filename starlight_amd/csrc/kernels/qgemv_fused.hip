@@ -308,7 +308,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     }
     constexpr int NR = LR ? 1 : 4;  // output rows a lane finishes (LR: m = kb4)
     const uint32_t steps_per_unit = p.unit / 64;
-    const uint32_t g_start = sbA * 128 / p.unit;
     const v4i zero = {0, 0, 0, 0};
     float total[NR];
 #pragma unroll
@@ -317,7 +316,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // wave runs are group-aligned, so a group never spans two runs)
     v4i acc0 = zero, acc1 = zero, acc2 = zero;
     uint32_t cj = 0, q = 0;               // block tile and position of the item being consumed
-    uint32_t gstep = 0, gi = g_start;     // 64-k steps into the current unit, its index
+    uint32_t gstep = 0;                   // 64-k steps into the current unit
     const int8_t* a_col = limbs + a_off + kb4 * 16;
     // One item of the stream: win[S] is used in place (a copy would make the
     // compiler wait before its refill) and refilled afterwards. A dead item
@@ -365,8 +364,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             else group_end = ++gstep == steps_per_unit;
             if (group_end) {
                 if constexpr (SPG == 0) gstep = 0;
-                if constexpr (SPG == 1) gi = 2 * sbi + st;
-                if constexpr (SPG == 2) gi = sbi;
                 const float sc = GPS == 2 && st == 1 ? cur.s1 : cur.s0;
                 const uint32_t chunk = (sbi * 128 + st * 64) / 256;
                 if constexpr (LR) {
@@ -386,7 +383,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                         total[r] = use ? t : total[r];
                     }
                 }
-                if constexpr (SPG == 0) ++gi;
                 acc0 = zero;
                 acc1 = zero;
                 acc2 = zero;
@@ -400,7 +396,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         const uint32_t j = cj;
         q = 0;
         ++cj;
-        gi = g_start;
         const uint32_t buf = j & 1;
 #pragma unroll
         for (int r = 0; r < NR; ++r) {

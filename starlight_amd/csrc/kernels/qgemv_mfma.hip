@@ -222,8 +222,7 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
                             row < p.n ? p.scales[static_cast<uint64_t>(row) * groups_total + g0 + gl] : 0.f;
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const uint32_t m = kb4 * 4 + r;
-                            float v = fmaf(static_cast<float>(acc2[r]), 65536.0f,
+                            const float v = fmaf(static_cast<float>(acc2[r]), 65536.0f,
                                            fmaf(static_cast<float>(acc1[r]), 256.0f, static_cast<float>(acc0[r])));
                             total[r] = fmaf(v, sc, total[r]);
                         }

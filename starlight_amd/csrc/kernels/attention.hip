@@ -59,6 +59,7 @@ __device__ __forceinline__ uint32_t past_of(const Geo& g) { return g.dyn != null
 
 template <int DPL>  // head_dim <= 64 * DPL
 __global__ __launch_bounds__(256) void attn_split(Geo g, uint64_t items) {
+    prefetch_kernarg<arg_bytes<Geo, uint64_t>()>();
     const uint64_t item = static_cast<uint64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
     if (item >= items) return;
     const int lane = threadIdx.x % kWave;
@@ -131,6 +132,7 @@ __global__ __launch_bounds__(256) void attn_split(Geo g, uint64_t items) {
 
 // Combines the chunk partials of one (b, h, t) per block.
 __global__ __launch_bounds__(256) void attn_merge(Geo g) {
+    prefetch_kernarg<arg_bytes<Geo>()>();
     const uint64_t bht = blockIdx.x;  // (b*heads + h)*seq + t
     const float* base = g.ws + bht * g.chunks * (g.head_dim + 2);
     float mx = -INFINITY;
@@ -225,6 +227,7 @@ __device__ __forceinline__ void rope_table(const Geo& g, uint64_t b, uint32_t S,
 
 __global__ __launch_bounds__(256) void rope_sincos(const uint32_t* __restrict__ pos, uint32_t tokens, uint32_t D,
                                                    double theta, float* __restrict__ table) {
+    prefetch_kernarg<arg_bytes<const uint32_t*, uint32_t, uint32_t, double, float*>()>();
     const uint32_t half = D / 2;
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= tokens * half) return;
@@ -237,6 +240,7 @@ __global__ __launch_bounds__(256) void rope_sincos(const uint32_t* __restrict__ 
 
 template <int DV, int RT, bool FUSED>
 __global__ __launch_bounds__(256) void attn_decode(Geo g) {
+    prefetch_kernarg<arg_bytes<Geo>()>();
     constexpr int D4 = 16 * DV;  // float4 per row
     extern __shared__ float sc[];  // FUSED: rope table [S][D]
     __shared__ float4 qs[RT * D4];
@@ -532,6 +536,7 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
 constexpr int kMergeMaxParts = 64;
 
 __global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
+    prefetch_kernarg<arg_bytes<Geo, uint32_t>()>();
     __shared__ float coef[kMergeMaxParts];
     __shared__ float4 red[256];
     const uint32_t D4 = g.head_dim / 4, S = g.seq, G = g.group, R = G * S;
@@ -592,6 +597,7 @@ constexpr int kTileK = 32;  // keys per LDS tile
 
 template <int D>
 __global__ __launch_bounds__(128) void attn_tiled(Geo g) {
+    prefetch_kernarg<arg_bytes<Geo>()>();
     constexpr int H = D / 2;  // dims per thread
     __shared__ float4 ks[kTileK * D / 4];
     __shared__ float4 vs[kTileK * D / 4];

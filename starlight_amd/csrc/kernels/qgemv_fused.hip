@@ -8,7 +8,7 @@
 //  * a block of 8 waves owns one 16-row tile (or, for a gate/up pair, one
 //    tile of each with 4 waves apiece) and the whole K range; its waves take
 //    contiguous, group-aligned runs of superblocks and start their weight
-//    and scale loads (6 INT4 / 4 INT8 superblocks, rolling) before the
+//    and scale loads (4 superblocks, rolling) before the
 //    activation prologue, then add their partial sums in LDS in wave order.
 //    No split partials in HBM, no second launch, deterministic. Blocks stay
 //    resident over several tiles (at most two per CU), so the prologue is
@@ -46,9 +46,28 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_from<0, N>(f);
 }
 
+// p, read into scalar registers: the value is wave-uniform by construction,
+// and the compiler can no longer turn a per-lane choice among such values
+// into a load from a per-lane address.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// p as a global-memory pointer: accesses through a pointer rebuilt from
+// integers are otherwise flat, and a flat load makes the compiler wait for
+// every outstanding load wherever it waits for this one.
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* global_ptr(T* p) {
+    return (__attribute__((address_space(1))) T*)p;
+}
+
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kMaxF4 = 8;  // float4 of activations per thread
+constexpr int kMaxF4 = 8;  // float4 of activations per thread, at most (F4: this launch's)
 // Bytes between consecutive rows of the limb matrices beyond k: the A
 // operand of a 64-k step reads the same 16-byte columns of several rows,
 // and rows a multiple of the bank width apart would all hit the same banks.
@@ -90,10 +109,10 @@ struct Item {
 // counted at run time). LR (m <= 4): the three limbs of every activation row
 // share one MFMA as its A rows 4 * m + limb, so a 64-k step is one LDS read
 // and one MFMA; otherwise (m <= 16) each limb matrix is an MFMA of its own.
-template <int BITS, int NT, int SPG, bool LR>
+template <int BITS, int NT, int SPG, bool LR, int F4>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(Args p) {
     constexpr int GPS = SPG == 1 ? 2 : 1;
-    constexpr int PF = BITS == 4 ? 6 : 4;  // superblocks in flight per wave
+    constexpr int PF = 4;  // superblocks in flight per wave
     constexpr int WPT = kWaves / NT;  // waves per tile
     constexpr uint32_t SB_BYTES = BITS == 4 ? 1024 : 2048;
     extern __shared__ __align__(16) int8_t limbs[];  // [3][m][k + kLimbPad], tres [tiles][16][m]
@@ -102,6 +121,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     __shared__ float cfac[kMaxElems / 256];  // per 256-element chunk: 2^(E-22)
     __shared__ float wres[2][kWaves][16][16];
 
+    prefetch_kernarg<arg_bytes<Args>()>();
     const int tid = threadIdx.x, lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, kept in scalar registers
     const uint32_t M = p.m, K = p.k, K4 = K / 4;
@@ -134,6 +154,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         return si;
     };
 #define SEG_FIELD(si, f) ((si) == 0 ? p.seg[0].f : (si) == 1 ? p.seg[1].f : p.seg[2].f)
+    // The output-side fields are chosen per thread in the epilogue (and for
+    // the residual prefetch); inside that divergent code a choice among
+    // argument fields compiles to vector loads of the argument block, one
+    // more memory round trip, so they are held in scalar registers here.
+    float* s_out[kFusedMaxSegs];
+    float* s_out2[kFusedMaxSegs];
+    const float* s_res[kFusedMaxSegs];
+    uint32_t s_n[kFusedMaxSegs];
+#pragma unroll
+    for (uint32_t i = 0; i < kFusedMaxSegs; ++i) {
+        s_out[i] = uniform_ptr(p.seg[i].out);
+        s_out2[i] = uniform_ptr(p.seg[i].out2);
+        s_res[i] = uniform_ptr(p.seg[i].resid);
+        s_n[i] = __builtin_amdgcn_readfirstlane(p.seg[i].n);
+    }
+#define SEG_PICK(a, si) ((si) == 0 ? a[0] : (si) == 1 ? a[1] : a[2])
     // The stream is walked with cursors: the segment, tile and base address
     // are resolved once per tile and the addresses advance by a constant per
     // superblock, keeping the shared scalar unit's work per item small.
@@ -181,20 +217,47 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // ---- activations first (the prologue waits for them only), then the
     // weight window: element float4 f = tid + kThreads * u of [m][k/4] ----
     const uint32_t total4 = M * K4;
-    float4 v[kMaxF4], gv[kMaxF4];
+    float4 v[F4], gv[F4];
 #pragma unroll
-    for (int u = 0; u < kMaxF4; ++u) {
+    for (int u = 0; u < F4; ++u) {
         v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (kThreads * u >= total4) continue;  // block-uniform: runs past the input load nothing
         const uint32_t f = min(static_cast<uint32_t>(tid + kThreads * u), total4 - 1);
         v[u] = reinterpret_cast<const float4*>(p.a)[f];
         if (p.gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(p.gamma)[f % K4];
     }
+    // Output element e of the block's [tiles][16][m] results: its segment
+    // and offset, false past the segment's rows.
+    auto out_at = [&](uint32_t e, uint32_t& si, uint64_t& o) -> bool {
+        const uint32_t j = e / (16 * M), col = (e / M) % 16, m = e % M;
+        uint32_t tile = blockIdx.x + j * gridDim.x;
+        si = 0;
+        if (NT == 1) si = seg_of(tile, tile);
+        const uint32_t sn = SEG_PICK(s_n, si);
+        const uint32_t orow = tile * 16 + col;
+        o = static_cast<uint64_t>(m) * sn + orow;
+        return orow < sn;
+    };
+    // The residual input of this thread's first output is loaded right
+    // after the weight window, so the epilogue does not wait a memory round
+    // trip for it. Every thread loads (threads without one re-read an
+    // activation), which keeps the compiler's wait counts exact.
+    const float* res_src = p.a;
+    if (p.epilogue == kFusedResidual && static_cast<uint32_t>(tid) < my_tiles * 16 * M) {
+        uint32_t si;
+        uint64_t o;
+        if (out_at(tid, si, o)) res_src = SEG_PICK(s_res, si) + o;
+    }
+#ifndef SL_PF0
+#define SL_PF0 PF
+#endif
+    constexpr int PF0 = SL_PF0 < PF ? SL_PF0 : PF;
     Item<BITS> win[PF];
 #pragma unroll
-    for (int i = 0; i < PF; ++i) fetch_next(win[i]);
+    for (int i = 0; i < PF0; ++i) fetch_next(win[i]);
+    const float res0 = *global_ptr(res_src);
 #pragma unroll
-    for (int u = 0; u < kMaxF4; ++u)
+    for (int u = 0; u < F4; ++u)
         if (tid + kThreads * u >= total4) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
 
     // Row of the wave-uniform run (u, wave): k % 256 == 0 keeps a wave's 64
@@ -215,7 +278,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 
     if (p.gamma != nullptr) {
 #pragma unroll
-        for (int u = 0; u < kMaxF4; ++u) {
+        for (int u = 0; u < F4; ++u) {
             float ss = 0.f;
             ss = fmaf(v[u].x, v[u].x, ss);
             ss = fmaf(v[u].y, v[u].y, ss);
@@ -227,7 +290,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         row_reduce(false);
         const float kf = static_cast<float>(K);
 #pragma unroll
-        for (int u = 0; u < kMaxF4; ++u) {
+        for (int u = 0; u < F4; ++u) {
             const uint32_t f = tid + kThreads * u;
             if (f < total4) {
                 const float inv = 1.0f / sqrtf(row_val[f / K4] / kf + p.eps);
@@ -249,7 +312,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // whose operands are the signed bytes 16 q).
     const uint32_t chunks = K / 256;
 #pragma unroll
-    for (int u = 0; u < kMaxF4; ++u) {
+    for (int u = 0; u < F4; ++u) {
         const uint32_t fb = static_cast<uint32_t>(wave) * kWave + kThreads * u;
         if (fb >= total4) continue;  // whole wave past the end
         const uint32_t f = tid + kThreads * u;
@@ -294,6 +357,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     }
     __syncthreads();
 
+#pragma unroll
+    for (int i = PF0; i < PF; ++i) fetch_next(win[i]);
     // ---- main loop over the stream ----
     const uint32_t kb4 = lane / 16;
     // A-operand row of this lane: with LR row 4 * m + limb (limb 3 repeats
@@ -440,19 +505,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // ---- results of all the block's tiles ----
     __syncthreads();
     for (uint32_t e = tid; e < my_tiles * 16 * M; e += kThreads) {
-        const uint32_t j = e / (16 * M), col = (e / M) % 16, m = e % M;
-        uint32_t tile = blockIdx.x + j * gridDim.x, si = 0;
-        if (NT == 1) si = seg_of(tile, tile);
-        const uint32_t sn = SEG_FIELD(si, n);
-        const uint32_t orow = tile * 16 + col;
-        if (orow >= sn) continue;
+        uint32_t si;
+        uint64_t o;
+        if (!out_at(e, si, o)) continue;
         const float val = tres[e];
-        const uint64_t o = static_cast<uint64_t>(m) * sn + orow;
-        SEG_FIELD(si, out)[o] = val;
-        if (p.epilogue == kFusedResidual) SEG_FIELD(si, out2)[o] = SEG_FIELD(si, resid)[o] + val;
+        global_ptr(SEG_PICK(s_out, si))[o] = val;
+        if (p.epilogue == kFusedResidual)
+            global_ptr(SEG_PICK(s_out2, si))[o] = (e == tid ? res0 : global_ptr(SEG_PICK(s_res, si))[o]) + val;
     }
 }
 #undef SEG_FIELD
+#undef SEG_PICK
 
 }  // namespace
 
@@ -508,9 +571,16 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     if (lds + kStaticLds > max_lds_per_block()) return hipErrorNotSupported;
     const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, lr = p.m <= 4;
     const int spg = p.group == 64 ? 1 : p.group == 128 ? 2 : 0;
-#define SL_QGEMV_FUSED(B, T, G)                                                        \
-    (lr ? qgemv_fused<B, T, G, true><<<blocks, kThreads, lds, s>>>(p)                  \
-        : qgemv_fused<B, T, G, false><<<blocks, kThreads, lds, s>>>(p))
+    // Float4 of activations per thread, a compile-time count: the prologue
+    // is straight-line code run once per wave, fetched cold by every CU at
+    // each launch, so its length shows in the launch time (about 1 us for
+    // the RMSNorm prologue at 8 float4 per thread against 2).
+    const uint32_t f4 = (p.m * p.k / 4 + kThreads - 1) / kThreads;
+#define SL_QGEMV_FUSED_F(B, T, G, L)                                                   \
+    (f4 <= 2   ? qgemv_fused<B, T, G, L, 2><<<blocks, kThreads, lds, s>>>(p)            \
+     : f4 <= 4 ? qgemv_fused<B, T, G, L, 4><<<blocks, kThreads, lds, s>>>(p)            \
+               : qgemv_fused<B, T, G, L, 8><<<blocks, kThreads, lds, s>>>(p))
+#define SL_QGEMV_FUSED(B, T, G) (lr ? SL_QGEMV_FUSED_F(B, T, G, true) : SL_QGEMV_FUSED_F(B, T, G, false))
 #define SL_QGEMV_FUSED_G(B, T) \
     (spg == 1 ? SL_QGEMV_FUSED(B, T, 1) : spg == 2 ? SL_QGEMV_FUSED(B, T, 2) : SL_QGEMV_FUSED(B, T, 0))
     if (int4) {
@@ -522,6 +592,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     }
 #undef SL_QGEMV_FUSED_G
 #undef SL_QGEMV_FUSED
+#undef SL_QGEMV_FUSED_F
     return hipGetLastError();
 }
 

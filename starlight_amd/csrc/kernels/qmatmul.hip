@@ -79,6 +79,7 @@ template <int BITS>
 __global__ __launch_bounds__(256) void qgemv_valu(const float* __restrict__ a, const uint8_t* __restrict__ tiles,
                                                   const float* __restrict__ scales, float* __restrict__ out,
                                                   uint32_t n, uint32_t k, uint32_t group) {
+    prefetch_kernarg<arg_bytes<const float*, const uint8_t*, const float*, float*, uint32_t, uint32_t, uint32_t>()>();
     constexpr int CK = BITS == 4 ? 32 : 16;        // codes per 16-byte chunk
     constexpr float OFF = BITS == 4 ? 8.f : 128.f;  // offset-binary bias
     const uint32_t lane = threadIdx.x % kWave;

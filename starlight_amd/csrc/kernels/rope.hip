@@ -23,6 +23,7 @@ template <bool INTERLEAVED>
 __global__ __launch_bounds__(256) void rope_kernel(const float* __restrict__ x, const uint32_t* __restrict__ pos,
                                                    float* __restrict__ out, uint32_t heads, uint32_t seq,
                                                    uint32_t head_dim, double theta) {
+    prefetch_kernarg<arg_bytes<const float*, const uint32_t*, float*, uint32_t, uint32_t, uint32_t, double>()>();
     extern __shared__ float sc[];  // [half] sine, [half] cosine
     const uint32_t half = head_dim / 2;
     const uint64_t bt = blockIdx.x;  // b * seq + t

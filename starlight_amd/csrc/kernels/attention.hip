@@ -298,11 +298,24 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
         const uint64_t row = FUSED ? (b * S + t) * g.heads + h : (b * g.heads + h) * S + t;
         qv[u] = reinterpret_cast<const float4*>(g.q + row * (4 * D4))[c];
     }
+    // FUSED: the first entries of the Rope table, loaded with the query rows
+    // and ahead of the K/V tile, whose bytes they would otherwise wait behind
+    // (every thread loads: without a table, from the query rows)
+    constexpr int kTabRegs = 2;
+    float tabv[kTabRegs];
+    if constexpr (FUSED) {
+        const uint32_t SD = S * 4 * D4;
+        const float* tab = g.rope_tab != nullptr ? g.rope_tab + b * SD : g.q;
+#pragma unroll
+        for (int u = 0; u < kTabRegs; ++u) tabv[u] = tab[min(static_cast<uint32_t>(tid + 256 * u), SD - 1)];
+    }
     uint32_t tile = p + P * wave;
     float4 kv[kDecodeKeys][DV], vv[kDecodeKeys][DV];
-    // a wave with no tile loads nothing: loads in flight into registers the
-    // combine reuses would hold the whole block at its barrier
-    if (tile < ntiles) load_tile(tile, kv, vv);
+    // Every wave loads a first tile, unconditionally (a wave without one
+    // re-reads the last key row, which its neighbours load too): loads
+    // under a branch leave register copies at the join that wait for the
+    // data right away, ahead of the query staging and Rope below.
+    load_tile(tile, kv, vv);
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
         const uint32_t i = tid + 256 * u;
@@ -321,12 +334,18 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
         // Rope of the query rows, in LDS
         constexpr uint32_t D = 4 * D4;
         if (g.rope_tab != nullptr) {
-            for (uint32_t i = tid; i < S * D; i += 256) sc[i] = g.rope_tab[b * S * D + i];
+#pragma unroll
+            for (int u = 0; u < kTabRegs; ++u)
+                if (tid + 256 * u < S * D) sc[tid + 256 * u] = tabv[u];
+            for (uint32_t i = tid + 256 * kTabRegs; i < S * D; i += 256) sc[i] = g.rope_tab[b * S * D + i];
         } else {
             rope_table(g, b, S, D, sc);
         }
         __syncthreads();
-        if (p == 0 && g.q_split != nullptr) put_q_rows(g.q_split);
+        if (p == 0 && g.q_split != nullptr) {  // block-uniform
+            put_q_rows(g.q_split);
+            __syncthreads();  // the rotation below rewrites rows other threads store here
+        }
         if (g.rope_variant == SL_ROPE_NEOX) {
             for (uint32_t i = tid; i < R * (D4 / 2); i += 256) {  // four pairs (d, d + D/2) per item
                 const uint32_t r = i / (D4 / 2), c = i % (D4 / 2);
@@ -477,16 +496,18 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         if (r >= static_cast<int>(R)) continue;
+        static_assert(kDecodeLanes == 16, "lane groups are 16-lane rows");
 #pragma unroll
-        for (int off = kDecodeLanes; off < kWave; off <<= 1) {
-            const float mo = __shfl_xor(m[r], off, kWave), lo = __shfl_xor(l[r], off, kWave);
+        for (int step = 0; step < 2; ++step) {  // partner group: lane ^ 16, then lane ^ 32
+            auto other = [&](float x) { return step == 0 ? lane_xor16(x) : lane_xor32(x); };
+            const float mo = other(m[r]), lo = other(l[r]);
             float4 ao[DV];
 #pragma unroll
             for (int u = 0; u < DV; ++u) {
-                ao[u].x = __shfl_xor(acc[r][u].x, off, kWave);
-                ao[u].y = __shfl_xor(acc[r][u].y, off, kWave);
-                ao[u].z = __shfl_xor(acc[r][u].z, off, kWave);
-                ao[u].w = __shfl_xor(acc[r][u].w, off, kWave);
+                ao[u].x = other(acc[r][u].x);
+                ao[u].y = other(acc[r][u].y);
+                ao[u].z = other(acc[r][u].z);
+                ao[u].w = other(acc[r][u].w);
             }
             fold_state<DV>(m[r], l[r], acc[r], mo, lo, ao);
         }

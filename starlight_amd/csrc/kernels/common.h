@@ -100,6 +100,21 @@ __device__ __forceinline__ void stream_store(float4* p, float4 v) {
 }
 __device__ __forceinline__ void stream_store(float* p, float v) { __builtin_nontemporal_store(v, p); }
 
+// v from lane i ^ 16 and i ^ 32 of the wave, with the gfx950 lane swaps:
+// VALU operations, where a ds_bpermute shuffle is an LDS round trip. With
+// both operands v, v_permlane16_swap leaves the even 16-lane rows of its
+// first result and the odd rows of its second unchanged, the other rows
+// taking their neighbour's values; v_permlane32_swap does the same for the
+// two 32-lane halves.
+__device__ __forceinline__ float lane_xor16(float v) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? s[0] : s[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? s[0] : s[1]);
+}
+
 // Pulls the first BYTES of the kernel's argument segment into the scalar
 // cache with one batch of independent loads (one word per 64-byte line) and
 // waits for them once. Left to itself the compiler fetches arguments as

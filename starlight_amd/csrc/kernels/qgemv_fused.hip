@@ -553,23 +553,36 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     }
     if (f.epilogue == kFusedPair) tiles = static_cast<uint32_t>((w0.n + 15) / 16);
     p.tiles_total = tiles;
+    const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, lr = p.m <= 4;
     const uint32_t wpt = f.epilogue == kFusedPair ? kWaves / 2 : kWaves;
     const uint32_t sb_per_group = p.group >= 128 ? p.group / 128 : 1;
     uint32_t per = (p.sb_total + wpt - 1) / wpt;
     per = (per + sb_per_group - 1) / sb_per_group * sb_per_group;
     p.sb_per_wave = per;
-    // Resident blocks: the tiles are dealt evenly over at most two blocks
-    // per CU, so every block converts the activations once for all its
-    // tiles; the results of a block's tiles wait in LDS (at most 16 KB).
-    const uint32_t max_blocks = 2 * compute_units();
-    uint32_t per_block = (tiles + max_blocks - 1) / max_blocks;
+    // Resident blocks: every block converts the activations once for all
+    // its tiles; the results of a block's tiles wait in LDS (at most 16 KB).
+    // Weights of up to 24 MB take one block per CU, the tiles dealt round
+    // robin (some blocks one more): the prologue, repeated by every block,
+    // is then paid once per CU. Larger ones take up to two per CU, with
+    // even shares, for more loads in flight. (Measured on MI355X, M = 1:
+    // the q/k/v launch [6144 x 4096] gains 1 us from one block per CU, the
+    // gate/up pair [2 x 14336 x 4096] loses 0.5 us.)
+    const uint64_t weight_bytes = static_cast<uint64_t>(tiles) * p.sb_total * (int4 ? 1024 : 2048) * (pair ? 2 : 1);
+    uint32_t blocks, per_block;
     const uint32_t per_cap = 4096 / (16 * p.m);
+    if (weight_bytes <= (24ull << 20)) {
+        blocks = tiles < compute_units() ? tiles : compute_units();
+        per_block = (tiles + blocks - 1) / blocks;
+    } else {
+        const uint32_t max_blocks = 2 * compute_units();
+        per_block = (tiles + max_blocks - 1) / max_blocks;
+        blocks = 0;
+    }
     if (per_block > per_cap) per_block = per_cap;
-    const uint32_t blocks = (tiles + per_block - 1) / per_block;
+    if (blocks == 0 || per_block == per_cap) blocks = (tiles + per_block - 1) / per_block;
     const size_t lds = static_cast<size_t>(3) * p.m * (p.k + kLimbPad) +
                        sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m;
     if (lds + kStaticLds > max_lds_per_block()) return hipErrorNotSupported;
-    const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, lr = p.m <= 4;
     const int spg = p.group == 64 ? 1 : p.group == 128 ? 2 : 0;
     // Float4 of activations per thread, a compile-time count: the prologue
     // is straight-line code run once per wave, fetched cold by every CU at

@@ -244,8 +244,12 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     constexpr int D4 = 16 * DV;  // float4 per row
     extern __shared__ float sc[];  // FUSED: rope table [S][D]
     __shared__ float4 qs[RT * D4];
-    __shared__ float4 wacc[4][RT][D4];
-    __shared__ float wml[4][RT][2];
+    // Softmax states combined through LDS at the end: with small per-lane
+    // state (RT * DV <= 8) every lane group's own (16 per block: 32 KB for
+    // head_dim 128, four rows), else one per wave after lane swaps.
+    constexpr int NS = RT * DV <= 8 ? 16 : 4;
+    __shared__ float4 wacc[NS][RT][D4];
+    __shared__ float wml[NS][RT][2];
     const uint32_t S = g.seq, G = g.group, R = G * S;
     const uint32_t P = gridDim.x, p = blockIdx.x, kvh = blockIdx.y;
     const uint64_t b = blockIdx.z;
@@ -492,11 +496,21 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
         }
     }
 
-    // combine the four lane groups of the wave, then the four waves
+    // combine the lane groups and waves
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         if (r >= static_cast<int>(R)) continue;
         static_assert(kDecodeLanes == 16, "lane groups are 16-lane rows");
+        if constexpr (NS == 16) {
+            const int st = wave * 4 + grp;
+#pragma unroll
+            for (int u = 0; u < DV; ++u) wacc[st][r][li + 16 * u] = acc[r][u];
+            if (li == 0) {
+                wml[st][r][0] = m[r];
+                wml[st][r][1] = l[r];
+            }
+            continue;
+        }
 #pragma unroll
         for (int step = 0; step < 2; ++step) {  // partner group: lane ^ 16, then lane ^ 32
             auto other = [&](float x) { return step == 0 ? lane_xor16(x) : lane_xor32(x); };
@@ -527,12 +541,12 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
         const uint32_t r = i / D4, c = i % D4;
         float mm = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) mm = fmaxf(mm, wml[w][r][0]);
+        for (int w = 0; w < NS; ++w) mm = fmaxf(mm, wml[w][r][0]);
         float ll = 0.f;
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
         if (mm != -INFINITY) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
+            for (int w = 0; w < NS; ++w) {
                 const float mw = wml[w][r][0];
                 const float cw = mw == -INFINITY ? 0.f : expf(mw - mm);
                 ll = fmaf(wml[w][r][1], cw, ll);

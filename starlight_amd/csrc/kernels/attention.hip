@@ -537,6 +537,39 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     __syncthreads();
     const uint64_t row_stride = kDecodePartStride + 4 * D4;
     float* part = g.ws + ((b * g.kv_heads + kvh) * P + p) * R * row_stride;
+    if constexpr (NS == 16) {
+        // the 16 states' weights exp(m_s - max) of each row, once: row r's
+        // states sit in the 16-lane row r of waves 0 .. R / 4 (DPP rows)
+        __shared__ float coef[RT][16];
+        __shared__ float rml[RT][2];
+        if (static_cast<uint32_t>(wave) * kWave < R * 16) {  // wave-uniform
+            const uint32_t r = tid / 16, st = tid % 16;
+            const float ms = r < R ? wml[st][r][0] : -INFINITY;
+            const float mm = row_max(ms);
+            const float cw = ms == -INFINITY ? 0.f : expf(ms - mm);
+            const float ll = row_sum((r < R ? wml[st][r][1] : 0.f) * cw);
+            if (r < R) {
+                coef[r][st] = cw;
+                if (st == 0) {
+                    rml[r][0] = mm;
+                    rml[r][1] = ll;
+                }
+            }
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < R * D4; i += 256) {
+            const uint32_t r = i / D4, c = i % D4;
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int w = 0; w < NS; ++w) a = f4_fma(coef[r][w], wacc[w][r][c], a);
+            reinterpret_cast<float4*>(part + r * row_stride + kDecodePartStride)[c] = a;
+            if (c == 0) {
+                part[r * row_stride] = rml[r][0];
+                part[r * row_stride + 1] = rml[r][1];
+            }
+        }
+        return;
+    }
     for (uint32_t i = tid; i < R * D4; i += 256) {
         const uint32_t r = i / D4, c = i % D4;
         float mm = -INFINITY;

@@ -32,6 +32,8 @@ namespace slhip {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 
 // Calls f(std::integral_constant<int, I>) for I = 0 .. N-1, unrolled.
 template <int I, int N, typename F>
@@ -153,7 +155,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         }
         return si;
     };
-#define SEG_FIELD(si, f) ((si) == 0 ? p.seg[0].f : (si) == 1 ? p.seg[1].f : p.seg[2].f)
     // The output-side fields are chosen per thread in the epilogue (and for
     // the residual prefetch); inside that divergent code a choice among
     // argument fields compiles to vector loads of the argument block, one
@@ -170,47 +171,59 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         s_n[i] = __builtin_amdgcn_readfirstlane(p.seg[i].n);
     }
 #define SEG_PICK(a, si) ((si) == 0 ? a[0] : (si) == 1 ? a[1] : a[2])
-    // The stream is walked with cursors: the segment, tile and base address
-    // are resolved once per tile and the addresses advance by a constant per
-    // superblock, keeping the shared scalar unit's work per item small.
-    // Every item issues the same loads (the dead superblocks of a trailing
-    // wave re-read its last live one), so each wait is for one item only.
+    // The stream as a table: lane l of the wave holds item l's weight and
+    // scale addresses and its meta word (superblock along k, live flag,
+    // last-of-tile flag), worked out once here in parallel; the loop then
+    // reads item k's entries with v_readlane, keeping the shared scalar
+    // unit's work per item small. A wave has at most 64 items (the launch
+    // caps tiles per block to fit). Every item issues the same loads (the
+    // dead superblocks of a trailing wave, and the window's fetches past the
+    // stream's end, re-read a live one), so each wait is for one item only.
     const uint32_t nlive = sbA < p.sb_total ? min(len, p.sb_total - sbA) : 0;
     const uint32_t sb0 = min(sbA, p.sb_total - 1);
-    auto tile_base = [&](uint32_t j, const uint8_t*& wp, const float*& sp) {
+    constexpr uint32_t kMetaLive = 1u << 16, kMetaTileEnd = 1u << 17;
+    uint32_t tw_lo, tw_hi, ts_lo, ts_hi, tmeta;
+    {
+        const uint8_t* s_tiles[kFusedMaxSegs];
+        const float* s_tsc[kFusedMaxSegs];
+#pragma unroll
+        for (uint32_t x = 0; x < kFusedMaxSegs; ++x) {
+            s_tiles[x] = uniform_ptr(p.seg[x].tiles);
+            s_tsc[x] = uniform_ptr(p.seg[x].tscales);
+        }
+        const uint32_t i = min(static_cast<uint32_t>(lane), items - 1);
+        const uint32_t j = i / len, q = i % len;
         uint32_t tile;
         const uint32_t si = seg_of(blockIdx.x + j * gridDim.x, tile);
-        const uint64_t ts = static_cast<uint64_t>(tile) * p.sb_total + sb0;
-        wp = SEG_FIELD(si, tiles) + ts * SB_BYTES;
-        sp = SEG_FIELD(si, tscales) + ts * 16 * gps;
+        const uint64_t ts = static_cast<uint64_t>(tile) * p.sb_total + sb0 + (q < nlive ? q : (nlive ? nlive - 1 : 0));
+        const uint64_t w = reinterpret_cast<uint64_t>(SEG_PICK(s_tiles, si) + ts * SB_BYTES);
+        const uint64_t sc = reinterpret_cast<uint64_t>(SEG_PICK(s_tsc, si) + ts * 16 * gps);
+        tw_lo = static_cast<uint32_t>(w);
+        tw_hi = static_cast<uint32_t>(w >> 32);
+        ts_lo = static_cast<uint32_t>(sc);
+        ts_hi = static_cast<uint32_t>(sc >> 32);
+        tmeta = (q < nlive ? (sbA + q) | kMetaLive : 0u) | (q == len - 1 ? kMetaTileEnd : 0u);
+    }
+    auto lane_u64 = [&](uint32_t lo, uint32_t hi, uint32_t k) {
+        return static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(hi), k))) << 32 |
+               static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), k));
     };
-    uint32_t pj = 0, pq = 0;  // block tile and position of the next item to fetch
-    bool pdone = false;       // the stream's last item has been fetched: stay on it
-    const uint8_t* pw;
-    const float* ps;
-    tile_base(0, pw, ps);
-    auto fetch_next = [&](Item<BITS>& it) {
-        const uint8_t* wp = pw + lane * 16;
-        it.c0 = *reinterpret_cast<const uint4*>(wp);
-        if constexpr (BITS == 8) it.c1 = *reinterpret_cast<const uint4*>(wp + 1024);
-        const float* sp = ps + (lane % 16) * gps;
+    auto fetch = [&](Item<BITS>& it, uint32_t k) {  // k wave-uniform
+        k = min(k, items - 1);
+        const auto wp = global_ptr(reinterpret_cast<const v4u*>(lane_u64(tw_lo, tw_hi, k))) + lane;
+        const v4u w0 = wp[0];
+        it.c0 = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+        if constexpr (BITS == 8) {
+            const v4u w1 = wp[64];
+            it.c1 = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+        }
+        const auto sp = global_ptr(reinterpret_cast<const float*>(lane_u64(ts_lo, ts_hi, k))) + (lane % 16) * gps;
         if constexpr (GPS == 2) {
-            const float2 s2 = *reinterpret_cast<const float2*>(sp);
-            it.s0 = s2.x;
-            it.s1 = s2.y;
+            const v2f s2 = *reinterpret_cast<const __attribute__((address_space(1))) v2f*>(sp);
+            it.s0 = s2[0];
+            it.s1 = s2[1];
         } else {
             it.s0 = sp[0];
-        }
-        // The window fetches PF items past the stream's end; those re-read
-        // the last item, so the cursor never leaves this wave's last tile.
-        if (pdone) return;
-        if (++pq == len) {
-            pq = 0;
-            if (pj + 1 < my_tiles) tile_base(++pj, pw, ps);
-            else pdone = true;
-        } else if (pq < nlive) {
-            pw += SB_BYTES;
-            ps += 16 * gps;
         }
     };
 
@@ -254,7 +267,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     constexpr int PF0 = SL_PF0 < PF ? SL_PF0 : PF;
     Item<BITS> win[PF];
 #pragma unroll
-    for (int i = 0; i < PF0; ++i) fetch_next(win[i]);
+    for (int i = 0; i < PF0; ++i) fetch(win[i], i);
     const float res0 = *global_ptr(res_src);
 #pragma unroll
     for (int u = 0; u < F4; ++u)
@@ -358,7 +371,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     __syncthreads();
 
 #pragma unroll
-    for (int i = PF0; i < PF; ++i) fetch_next(win[i]);
+    for (int i = PF0; i < PF; ++i) fetch(win[i], i);
     // ---- main loop over the stream ----
     const uint32_t kb4 = lane / 16;
     // A-operand row of this lane: with LR row 4 * m + limb (limb 3 repeats
@@ -380,17 +393,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // integer sums of the current group (a group may span superblocks; the
     // wave runs are group-aligned, so a group never spans two runs)
     v4i acc0 = zero, acc1 = zero, acc2 = zero;
-    uint32_t cj = 0, q = 0;               // block tile and position of the item being consumed
+    uint32_t cj = 0;                      // block tile of the item being consumed
     uint32_t gstep = 0;                   // 64-k steps into the current unit
     const int8_t* a_col = limbs + a_off + kb4 * 16;
     // One item of the stream: win[S] is used in place (a copy would make the
     // compiler wait before its refill) and refilled afterwards. A dead item
     // (a trailing wave's padding past k) computes on clamped addresses and
     // its sums are dropped by a select rather than a branch.
-    auto consume = [&](auto s_c, bool use) {
+    auto consume = [&](auto s_c, uint32_t meta) {
         constexpr int S = decltype(s_c)::value;
         const Item<BITS>& cur = win[S];
-        const uint32_t sbi = use ? sbA + q : 0u;  // superblock along k (dead: 0)
+        const bool use = (meta & kMetaLive) != 0;
+        const uint32_t sbi = meta & 0xffffu;  // superblock along k (dead: 0)
         const int8_t* ap = a_col + sbi * 128;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
@@ -459,7 +473,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // the loop issues only the window's loads)
     auto tile_end = [&]() {
         const uint32_t j = cj;
-        q = 0;
         ++cj;
         const uint32_t buf = j & 1;
 #pragma unroll
@@ -495,10 +508,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // tail, makes the compiler wait for the whole window.
     for (uint32_t base = 0; base < items; base += PF) {
         static_for<PF>([&](auto s_c) {
-            const bool live = base + decltype(s_c)::value < items;
-            if (live) consume(s_c, q < nlive);
-            fetch_next(win[decltype(s_c)::value]);
-            if (live && ++q == len) tile_end();
+            const uint32_t k = base + decltype(s_c)::value;
+            const bool live = k < items;
+            const uint32_t meta = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(tmeta), min(k, items - 1)));
+            if (live) consume(s_c, meta);
+            fetch(win[decltype(s_c)::value], k + PF);
+            if (live && (meta & kMetaTileEnd)) tile_end();
         });
     }
 
@@ -514,7 +529,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             global_ptr(SEG_PICK(s_out2, si))[o] = (e == tid ? res0 : global_ptr(SEG_PICK(s_res, si))[o]) + val;
     }
 }
-#undef SEG_FIELD
 #undef SEG_PICK
 
 }  // namespace
@@ -578,8 +592,11 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
         per_block = (tiles + max_blocks - 1) / max_blocks;
         blocks = 0;
     }
-    if (per_block > per_cap) per_block = per_cap;
-    if (blocks == 0 || per_block == per_cap) blocks = (tiles + per_block - 1) / per_block;
+    // the per-lane item table holds at most 64 items per wave
+    const uint32_t item_cap = 64 / per, cap = per_cap < item_cap ? per_cap : item_cap;
+    if (cap == 0) return hipErrorNotSupported;
+    if (per_block > cap) per_block = cap;
+    if (blocks == 0 || per_block == cap) blocks = (tiles + per_block - 1) / per_block;
     const size_t lds = static_cast<size_t>(3) * p.m * (p.k + kLimbPad) +
                        sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m;
     if (lds + kStaticLds > max_lds_per_block()) return hipErrorNotSupported;

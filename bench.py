@@ -42,6 +42,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense FP32 (vector or MFMA)
 PROMPT_LEN = 1024
 MAX_SEQ = 4096
 
@@ -155,29 +156,31 @@ def measured_traffic():
     return None
 
 
-def qgemv_roofline(dev, n=14336, k=4096, copies=16, launches=200, graphs=True):
-    """Times the INT4 g128 q-GEMV at [n x k], M = 1, over `copies` distinct
-    weight copies (16 x 31 MB > the 256 MB MALL) with HIP events."""
+def qgemv_roofline(dev, n=14336, k=4096, copies=16, launches=200, graphs=True, m=1, int8=False):
+    """Times the g128 q-GEMV (INT4, or INT8) at [n x k] with m activation
+    rows over `copies` distinct weight copies (16 x 31 MB > the 256 MB MALL)
+    with HIP events."""
     from starlight_amd import quant
     from starlight_amd.ir import BufferRef, Op, QuantFormat, Value
 
+    fmt = QuantFormat.INT8 if int8 else QuantFormat.INT4
     rng = np.random.default_rng(5)
     w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
-    words, scales = quant.quantize(w, 128, QuantFormat.INT4)
+    words, scales = quant.quantize(w, 128, fmt)
     weights = []
     for _ in range(copies):
         pb = dev.upload_new_u32(words)
         sb = dev.upload_new_f32(scales)
-        dev.bind_quantized(pb, sb, QuantFormat.INT4, 128, n, k)
+        dev.bind_quantized(pb, sb, fmt, 128, n, k)
         weights.append(pb)
-    x = dev.upload_new_f32(rng.standard_normal(k).astype(np.float32))
-    outs = [dev.allocate_f32(n, 256) for _ in range(copies)]
-    wv = Value.quantized([n, k], QuantFormat.INT4, 128)
-    xv, ov = Value.f32([1, k]), Value.f32([1, n])
+    x = dev.upload_new_f32(rng.standard_normal(m * k).astype(np.float32))
+    outs = [dev.allocate_f32(m * n, 256) for _ in range(copies)]
+    wv = Value.quantized([n, k], fmt, 128)
+    xv, ov = Value.f32([m, k]), Value.f32([m, n])
 
     def run(i):
-        dev.dispatch(Op.matmul_nt(), [BufferRef(x, 0, k), BufferRef(weights[i % copies], 0, words.size)], [xv, wv],
-                     [BufferRef(outs[i % copies], 0, n)], [ov])
+        dev.dispatch(Op.matmul_nt(), [BufferRef(x, 0, m * k), BufferRef(weights[i % copies], 0, words.size)],
+                     [xv, wv], [BufferRef(outs[i % copies], 0, m * n)], [ov])
 
     # One launch per dispatch (no fusion of same-input GEMVs). The same
     # submission three times: run, captured as a graph, replayed; the timed
@@ -196,12 +199,14 @@ def qgemv_roofline(dev, n=14336, k=4096, copies=16, launches=200, graphs=True):
     ms = timer.end_ms()
     dev.set_options()
     avg_us = ms * 1000.0 / launches
-    algorithmic = n * k // 2 + n * (k // 128) * 4 + k * 4 + n * 4
+    algorithmic = n * k // (1 if int8 else 2) + n * (k // 128) * 4 + m * k * 4 + m * n * 4
     achieved = algorithmic / (avg_us * 1e-6) / 1e9
+    name = "INT8" if int8 else "INT4"
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-            "kernel": f"qgemv_fused (q-GEMV INT4 g128 [{n}x{k}] M=1)", "bytes_per_launch": algorithmic,
-            "avg_launch_us": round(avg_us, 3)}
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic() if (n, k, m, int8) == (14336, 4096, 1, False) else None,
+            "kernel": f"{'qgemv_fused' if m * k <= 16384 else 'qgemv_mfma'} (q-GEMV {name} g128 [{n}x{k}] M={m})",
+            "bytes_per_launch": algorithmic, "avg_launch_us": round(avg_us, 3)}
 
 
 def rmsnorm_roofline(dev, rows=4096, hidden=4096, copies=4, launches=40):
@@ -236,6 +241,113 @@ def rmsnorm_roofline(dev, rows=4096, hidden=4096, copies=4, launches=40):
     return {"kernel": f"rms_norm [{rows}x{hidden}] f32", "achieved": round(achieved, 1), "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_launch": algorithmic,
             "avg_launch_us": round(avg_us, 3)}
+
+
+def submission_us(dev, dispatch_all):
+    """HIP-event time of one graph-replayed submission of dispatch_all()'s
+    commands (the first submissions run and capture it)."""
+    for _ in range(3):
+        dispatch_all()
+        dev.submit()
+    dev.synchronize()
+    timer = HipTimer(dev.stream)
+    dispatch_all()
+    timer.begin()
+    dev.submit()
+    return timer.end_ms() * 1000.0
+
+
+def hbm_line(kernel, bytes_per_launch, us):
+    achieved = bytes_per_launch / (us * 1e-6) / 1e9
+    return {"kernel": kernel, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_launch": bytes_per_launch,
+            "avg_launch_us": round(us, 3)}
+
+
+def micro_lines(dev):
+    """The microbenchmark configs: each op at its stated shape, graph-replayed
+    and timed with HIP events, working sets beyond the 256 MB MALL."""
+    from starlight_amd.ir import BufferRef, Op, RopeVariant, Value
+
+    rng = np.random.default_rng(7)
+    lines = []
+
+    def normal(n):
+        return rng.standard_normal(n, dtype=np.float32)
+
+    # Softmax [32 x 2048 x 2048]: rows 65,536 x cols 2,048, plain (unscaled) scores
+    rows, cols = 32 * 2048, 2048
+    x = dev.upload_new_f32(normal(rows * cols))
+    y = dev.allocate_f32(rows * cols, 256)
+    v = Value.f32([32, 2048, 2048])
+    us = submission_us(dev, lambda: [dev.dispatch(Op.softmax(), [BufferRef(x, 0, rows * cols)], [v],
+                                                  [BufferRef(y, 0, rows * cols)], [v]) for _ in range(10)]) / 10
+    lines.append(hbm_line("softmax_regs (Softmax [32x2048x2048] f32)", 2 * rows * cols * 4, us))
+    dev.synchronize()
+
+    # Add and fused SiLU(gate) * up, [4096 x 14336]
+    n = 4096 * 14336
+    a, b, out, t = (dev.upload_new_f32(normal(n)) for _ in range(4))
+    v = Value.f32([4096, 14336])
+    A, B, O, T = (BufferRef(z, 0, n) for z in (a, b, out, t))
+    us = submission_us(dev, lambda: [dev.dispatch(Op.add(), [A, B], [v, v], [O], [v]) for _ in range(10)]) / 10
+    lines.append(hbm_line("ew_vec4<Add> (Add [4096x14336] f32)", 3 * n * 4, us))
+
+    def pairs(count):
+        # Silu(gate) -> t, Mul(t, up) -> out; the next Silu overwrites t, so
+        # each pair runs fused; the trailing Silu keeps the last t dead
+        def go():
+            for _ in range(count):
+                dev.dispatch(Op.silu(), [A], [v], [T], [v])
+                dev.dispatch(Op.mul(), [T, B], [v, v], [O], [v])
+            dev.dispatch(Op.silu(), [A], [v], [T], [v])
+        return go
+
+    us = (submission_us(dev, pairs(30)) - submission_us(dev, pairs(10))) / 20
+    lines.append(hbm_line("ew_vec4<SiluMul> (SiLU(gate)*up fused [4096x14336] f32)", 3 * n * 4, us))
+    dev.synchronize()
+
+    # RoPE X[1, 32, 4096, 128], positions 0..4095, theta 500000, NeoX; 4 copies
+    heads, seq, hd = 32, 4096, 128
+    nx = heads * seq * hd
+    xs = [dev.upload_new_f32(normal(nx)) for _ in range(4)]
+    ys = [dev.allocate_f32(nx, 256) for _ in range(4)]
+    pos = dev.upload_new_u32(np.arange(seq, dtype=np.uint32))
+    xv, pv = Value.f32([1, heads, seq, hd]), Value.u32([1, seq])
+    us = submission_us(dev, lambda: [dev.dispatch(Op.rope(RopeVariant.NEOX, 500000.0),
+                                                  [BufferRef(xs[i % 4], 0, nx), BufferRef(pos, 0, seq)], [xv, pv],
+                                                  [BufferRef(ys[i % 4], 0, nx)], [xv]) for i in range(20)]) / 20
+    lines.append(hbm_line("rope_kernel (RoPE [1,32,4096,128] NeoX)", 2 * nx * 4 + seq * 4, us))
+    dev.synchronize()
+
+    lines.append(rmsnorm_roofline(dev))
+    lines.append(qgemv_roofline(dev, launches=100))
+    lines.append(qgemv_roofline(dev, n=4096, k=14336, launches=100))
+    lines.append(qgemv_roofline(dev, m=8, launches=100))
+    lines.append(qgemv_roofline(dev, copies=9, launches=90, int8=True))
+    dev.synchronize()
+
+    # q-GEMM INT4 g128 [14336 x 4096], M = 512 (prefill-shaped)
+    from starlight_amd import quant
+    from starlight_amd.ir import QuantFormat
+    nn, kk, mm = 14336, 4096, 512
+    words, scales = quant.quantize(normal(nn * kk).reshape(nn, kk) * np.float32(0.02), 128, QuantFormat.INT4)
+    pb, sb = dev.upload_new_u32(words), dev.upload_new_f32(scales)
+    dev.bind_quantized(pb, sb, QuantFormat.INT4, 128, nn, kk)
+    xa = dev.upload_new_f32(normal(mm * kk))
+    yo = dev.allocate_f32(mm * nn, 256)
+    wv = Value.quantized([nn, kk], QuantFormat.INT4, 128)
+    us = submission_us(dev, lambda: [dev.dispatch(Op.matmul_nt(), [BufferRef(xa, 0, mm * kk),
+                                                                   BufferRef(pb, 0, words.size)],
+                                                  [Value.f32([mm, kk]), wv], [BufferRef(yo, 0, mm * nn)],
+                                                  [Value.f32([mm, nn])]) for _ in range(3)]) / 3
+    flop = 2 * mm * nn * kk
+    tf = flop / (us * 1e-6) / 1e12
+    lines.append({"kernel": f"qgemm_tiled (q-GEMM INT4 g128 [{nn}x{kk}] M={mm})", "bound": "mfma",
+                  "achieved": round(tf, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                  "frac": round(tf / FP32_PEAK_TFLOPS, 4), "flop_per_launch": flop, "avg_launch_us": round(us, 1)})
+    dev.synchronize()
+    return lines
 
 
 def copy_run(dev, n=64 << 20, launches=20):
@@ -323,7 +435,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--int8", action="store_true", help="INT8 g128 weights instead of INT4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--mode", choices=["full", "roofline", "copy"], default="full")
+    ap.add_argument("--mode", choices=["full", "roofline", "copy", "micro"], default="full")
     ap.add_argument("--no-graphs", action="store_true", help="roofline/copy modes: launch eagerly")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -336,6 +448,10 @@ def main():
         dev = HipDevice(0)
         if args.mode == "roofline":
             print(json.dumps(qgemv_roofline(dev, graphs=not args.no_graphs)), flush=True)
+        elif args.mode == "micro":
+            for line in micro_lines(dev):
+                log(f"micro: {line}")
+                print(json.dumps(line), flush=True)
         else:
             copy_run(dev)
         dev.close()

@@ -45,6 +45,7 @@ namespace slhip {
 namespace {
 
 constexpr uint64_t kMirrorMaxElements = 1ull << 22;        // host copy of u32 buffers up to 16 MiB
+constexpr uint64_t kSmallUploadWords = 64;                  // uploads carried in kernel arguments, at most
 constexpr uint64_t kWorkspaceBytes = 512ull << 20;          // split-K partials, SwiGlu intermediates
 constexpr uint64_t kRopeTableFloats = 16 * 512;  // tokens x head_dim of one decode submission
 constexpr uint64_t kCounterWords = 1ull << 16;              // cross-block completion counters (kept at zero)
@@ -102,6 +103,7 @@ struct Device : BufferView {
     std::vector<uint32_t> dyn_values;
     std::vector<uint64_t> key, prev_key;
     std::vector<GraphEntry> graphs;
+    size_t last_graph = SIZE_MAX;  // entry of graphs the previous replay or capture used
     uint64_t use_clock = 0;
     sl_hip_stats stats{};
     // Rope sine / cosine table shared by the fused attention units of a
@@ -181,8 +183,19 @@ sl_status copy_in(Device* d, uint32_t id, const void* data, size_t len, uint32_t
     Buffer& b = d->buffers[id];
     if (b.desc.elements != len) return d->fail(Error::invalid_range(id, 0, len));
     if (len == 0) return SL_OK;
-    hipError_t e = hipMemcpyAsync(b.ptr, data, len * 4, hipMemcpyHostToDevice, d->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+    bool feeds_copies = b.tiles != nullptr;
+    if (kind == SL_BUFFER_F32)
+        for (const Buffer& p : d->buffers) feeds_copies |= p.tile_scales != nullptr && p.scales == id;
+    hipError_t e = hipSuccess;
+    if (len <= kSmallUploadWords && !feeds_copies) {
+        // A few words (token ids, positions of a decode step): written by a
+        // kernel that carries them in its arguments, in stream order, so the
+        // host neither stages a copy nor waits for it.
+        e = launch_set_words(static_cast<uint32_t*>(b.ptr), static_cast<const uint32_t*>(data), len, d->stream);
+    } else {
+        e = hipMemcpyAsync(b.ptr, data, len * 4, hipMemcpyHostToDevice, d->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+    }
     if (e != hipSuccess) return d->hip_fail(e);
     if (b.mirrored) std::memcpy(b.mirror.data(), data, len * 4);
     if (b.tiles) {
@@ -596,18 +609,24 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
     // not overlap anything that kernel reads or another live one; the
     // attention output and MergeHeads come from the merge kernel after it,
     // which keeps the op order where they overlap.
+    // A live one that overlaps what the decode kernel reads, or another one
+    // it writes, is staged instead: the kernel writes it to the workspace,
+    // and once the unit's kernels are done its ranges that no later command
+    // of the unit writes are copied to their place (the rotated q of a last
+    // layer, whose tail nothing overwrites before the submission ends).
     const sl_buffer_ref& cache = at.in[ap.state_index];
     const sl_buffer_ref inter[5] = {sq.out, sk.out, sv.out, rq.out, rk.out};
     const size_t after_reader[5] = {i + 4, i + 5, i + 6, i + 6, i + 6};
-    bool live[5];
+    bool live[5], staged[5] = {false, false, false, false, false};
     for (int x = 0; x < 5; ++x) {
         live[x] = !dead_after(d, after_reader[x], inter[x]);
         if (!live[x]) continue;
-        const sl_buffer_ref read[5] = {sq.in[0], sk.in[0], sv.in[0], cache, rq.in[1]};
+        if (overlaps(inter[x], cache)) return 0;
+        const sl_buffer_ref read[4] = {sq.in[0], sk.in[0], sv.in[0], rq.in[1]};
         for (const sl_buffer_ref& t : read)
-            if (overlaps(inter[x], t)) return 0;
+            if (overlaps(inter[x], t)) staged[x] = true;
         for (int y = 0; y < x; ++y)
-            if (live[y] && overlaps(inter[x], inter[y])) return 0;
+            if (live[y] && !staged[y] && overlaps(inter[x], inter[y])) staged[x] = true;
     }
     const sl_buffer_ref att = at.out;
     const bool att_dead = mh != nullptr && dead_after(d, i + used, att);
@@ -653,17 +672,62 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
         }
         a.rope_table = d->rope_tab;
     }
-    float** const inter_ptr[5] = {&a.q_split, &a.k_split, &a.v_split, &a.q_rot, &a.k_rot};
-    for (int x = 0; x < 5; ++x)
-        if (live[x]) *inter_ptr[x] = fptr(d, inter[x]);
-
-    // the output projection (and its residual Add) reading the mirror
+    // Workspace: the decode partials, the mirror of the merged heads, then
+    // the staged intermediates.
     const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
     const uint64_t mirror_at = (attention_workspace_floats(a) + 63) / 64 * 64;
+    uint64_t stage_at = mirror_at + (B * S * H * D + 63) / 64 * 64;
+    float* stage[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+    float** const inter_ptr[5] = {&a.q_split, &a.k_split, &a.v_split, &a.q_rot, &a.k_rot};
+    for (int x = 0; x < 5; ++x) {
+        if (!live[x]) continue;
+        if (staged[x]) {
+            if (stage_at + inter[x].len > ws.floats) return 0;
+            stage[x] = ws.data + stage_at;
+            stage_at += (inter[x].len + 63) / 64 * 64;
+            *inter_ptr[x] = stage[x];
+        } else {
+            *inter_ptr[x] = fptr(d, inter[x]);
+        }
+    }
+
+    // the output projection (and its residual Add) reading the mirror
     const bool chain = chainable && mirror_at + B * S * H * D <= ws.floats;
     if (chain) a.mirror = ws.data + mirror_at;
     hipError_t e = launch_attention_fused(a, ws, d->stream);
     if (e == hipErrorNotSupported) return 0;
+    if (e != hipSuccess) {
+        *err = e;
+        return used;
+    }
+    // staged intermediates to their place: the ranges that the unit's later
+    // commands (the other intermediates, the attention output, MergeHeads)
+    // leave holding them, before the chained projection writes anything
+    const size_t unit_end = i + (mh != nullptr ? 7 : 6);
+    for (int x = 0; x < 5 && e == hipSuccess; ++x) {
+        if (stage[x] == nullptr) continue;
+        std::vector<std::pair<uint64_t, uint64_t>> keep{{inter[x].offset, inter[x].offset + inter[x].len}};
+        for (size_t j = i + x + 1; j < unit_end; ++j) {
+            const sl_buffer_ref& o = d->log[j].out;
+            if (o.buffer != inter[x].buffer || o.len == 0) continue;
+            std::vector<std::pair<uint64_t, uint64_t>> rest;
+            for (const auto& iv : keep) {
+                if (o.offset > iv.first) rest.push_back({iv.first, o.offset < iv.second ? o.offset : iv.second});
+                if (o.offset + o.len < iv.second)
+                    rest.push_back({o.offset + o.len > iv.first ? o.offset + o.len : iv.first, iv.second});
+            }
+            keep.clear();
+            for (const auto& iv : rest)
+                if (iv.first < iv.second) keep.push_back(iv);
+        }
+        for (const auto& iv : keep) {
+            sl_buffer_ref part = inter[x];
+            part.offset = iv.first;
+            part.len = iv.second - iv.first;
+            e = launch_copy(stage[x] + (iv.first - inter[x].offset), fptr(d, part), part.len, d->stream);
+            if (e != hipSuccess) break;
+        }
+    }
     if (e != hipSuccess) {
         *err = e;
         return used;
@@ -701,6 +765,25 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
     return used;
 }
 
+// Silu(x) -> t then Mul(t, u) -> out as one pass, out = silu(x) * u, when t
+// is dead after the Mul (every element overwritten before any read): the
+// product's two IEEE multiplies are the unfused ones (a * b == b * a), so
+// the result is bit-identical and t is never written. The outputs of both
+// commands are disjoint from their inputs (validated); x may be out itself.
+size_t try_fuse_silu_mul(Device* d, size_t i, hipError_t* err) {
+    if (i + 2 > d->log.size()) return 0;
+    const Logged &sc = d->log[i], &mc = d->log[i + 1];
+    if (sc.plan.code != SL_OP_SILU || mc.plan.code != SL_OP_MUL || sc.plan.len != mc.plan.len) return 0;
+    const sl_buffer_ref& t = sc.out;
+    const int other = same_ref(mc.in[0], t) ? 1 : same_ref(mc.in[1], t) ? 0 : -1;
+    if (other < 0) return 0;
+    const sl_buffer_ref &x = sc.in[0], &u = mc.in[other], &out = mc.out;
+    if (overlaps(u, t) || (overlaps(out, x) && !same_ref(out, x)) || !dead_after(d, i + 1, t, i + 1)) return 0;
+    *err = launch_silu_mul(fptr(d, x), fptr(d, u), fptr(d, out), sc.plan.len, d->stream);
+    d->stats.fused_commands += 2;
+    return 2;
+}
+
 hipError_t run_log(Device* d) {
     d->rope.valid = false;
     for (size_t i = 0; i < d->log.size();) {
@@ -709,6 +792,7 @@ hipError_t run_log(Device* d) {
         if (d->options & SL_HIP_OPT_FUSION) {
             used = try_fuse_attention(d, i, &e);
             if (used == 0 && e == hipSuccess) used = try_fuse(d, i, &e);
+            if (used == 0 && e == hipSuccess) used = try_fuse_silu_mul(d, i, &e);
         }
         if (e != hipSuccess) return e;
         if (used == 0) {
@@ -728,6 +812,7 @@ void drop_graphs(Device* d) {
         if (g.graph) (void)hipGraphDestroy(g.graph);
     }
     d->graphs.clear();
+    d->last_graph = SIZE_MAX;
     d->prev_key.clear();
 }
 
@@ -759,10 +844,20 @@ void build_key(Device* d) {
     }
 }
 
+// FNV-style over 8 interleaved lanes: one chain of dependent multiplies
+// per lane rather than one for the whole key (tens of thousands of words
+// per decode step).
 uint64_t key_hash(const std::vector<uint64_t>& k) {
-    uint64_t h = 1469598103934665603ull;
-    for (uint64_t v : k) h = (h ^ v) * 1099511628211ull;
-    return h;
+    constexpr size_t kLanes = 8;
+    uint64_t h[kLanes];
+    for (size_t l = 0; l < kLanes; ++l) h[l] = 1469598103934665603ull + l;
+    const size_t n = k.size(), body = n / kLanes * kLanes;
+    for (size_t i = 0; i < body; i += kLanes)
+        for (size_t l = 0; l < kLanes; ++l) h[l] = (h[l] ^ k[i + l]) * 1099511628211ull;
+    for (size_t i = body; i < n; ++i) h[0] = (h[0] ^ k[i]) * 1099511628211ull;
+    uint64_t r = n;
+    for (size_t l = 0; l < kLanes; ++l) r = (r ^ h[l]) * 1099511628211ull;
+    return r;
 }
 
 // Enqueues the logged commands; the log is empty afterwards either way.
@@ -794,14 +889,22 @@ hipError_t submit(Device* d) {
     d->stats.submissions += 1;
     d->stats.commands += d->log.size();
     build_key(d);
-    const uint64_t hash = key_hash(d->key);
+    // A decode loop submits the same commands every step: the entry the
+    // previous submission used is tried first, by its key alone.
     GraphEntry* hit = nullptr;
-    for (GraphEntry& g : d->graphs)
-        if (g.hash == hash && g.key == d->key) hit = &g;
+    uint64_t hash = 0;
+    if (d->last_graph < d->graphs.size() && d->graphs[d->last_graph].key == d->key) {
+        hit = &d->graphs[d->last_graph];
+    } else {
+        hash = key_hash(d->key);
+        for (GraphEntry& g : d->graphs)
+            if (g.hash == hash && g.key == d->key) hit = &g;
+    }
     if (e != hipSuccess) {
         // nothing more
     } else if (hit) {
         hit->last_use = ++d->use_clock;
+        d->last_graph = static_cast<size_t>(hit - d->graphs.data());
         e = hipGraphLaunch(hit->exec, d->stream);
         d->stats.graph_replays += 1;
     } else if ((d->options & SL_HIP_OPT_GRAPHS) && d->key == d->prev_key) {
@@ -828,6 +931,7 @@ hipError_t submit(Device* d) {
             g.hash = hash;
             g.last_use = ++d->use_clock;
             d->graphs.push_back(g);
+            d->last_graph = d->graphs.size() - 1;
             e = hipGraphLaunch(d->graphs.back().exec, d->stream);
             d->stats.graph_captures += 1;
         } else {

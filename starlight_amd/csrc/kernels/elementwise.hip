@@ -12,7 +12,7 @@
 namespace slhip {
 namespace {
 
-enum class Ew { Add, Mul, Scale, Silu, SiluMul, Zero };
+enum class Ew { Add, Mul, Scale, Silu, SiluMul, Zero, Copy };
 
 template <Ew OP>
 __device__ __forceinline__ float apply(float a, float b, float factor) {
@@ -22,6 +22,7 @@ __device__ __forceinline__ float apply(float a, float b, float factor) {
     // silu_scalar (elementwise.rs:10-12): x * (1 / (1 + exp(-x)))
     if constexpr (OP == Ew::Silu) return a * (1.0f / (1.0f + expf(-a)));
     if constexpr (OP == Ew::SiluMul) return (a * (1.0f / (1.0f + expf(-a)))) * b;
+    if constexpr (OP == Ew::Copy) return a;
     return 0.0f;
 }
 
@@ -121,6 +122,9 @@ hipError_t launch_set_words(uint32_t* dst, const uint32_t* values, uint64_t coun
 
 hipError_t launch_fill_zero(float* out, uint64_t n, hipStream_t s) {
     return launch_ew<Ew::Zero>(nullptr, nullptr, out, n, 0.f, s);
+}
+hipError_t launch_copy(const float* src, float* dst, uint64_t n, hipStream_t s) {
+    return launch_ew<Ew::Copy>(src, nullptr, dst, n, 0.f, s);
 }
 
 }  // namespace slhip

@@ -33,6 +33,8 @@ hipError_t launch_mul(const float* a, const float* b, float* out, uint64_t n, hi
 hipError_t launch_scale(const float* x, float* out, uint64_t n, float factor, hipStream_t s);
 hipError_t launch_silu(const float* x, float* out, uint64_t n, hipStream_t s);
 hipError_t launch_fill_zero(float* out, uint64_t n, hipStream_t s);
+// dst[i] = src[i] (bit copies; the ranges must not overlap).
+hipError_t launch_copy(const float* src, float* dst, uint64_t n, hipStream_t s);
 
 // dst[0..count) = values, through kernel arguments (no host buffer lifetime,
 // no memset node when captured).

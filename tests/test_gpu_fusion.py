@@ -147,3 +147,130 @@ def test_attention_group_with_live_intermediate_fuses_and_writes_it(hip, case):
 def test_attention_group_keeps_every_live_intermediate(hip, case):
     fused = run_group(hip, case, consume_intermediate=False, keep_all=True)
     assert fused >= 7 if fusable(case) else fused == 0
+
+
+# The scratch layout of the last layer of an 8B-shaped decode step as the
+# memory plan lays it out (floats): q/k/v projections, then the split and
+# rotated heads reusing their space. The rotated q overlaps the q tail, k and
+# v, which the fused kernel still reads, and MergeHeads leaves its last 1024
+# floats holding it when nothing after the group overwrites them.
+LAST_LAYER = {"q": (8192, 4096), "k": (12288, 1024), "v": (13312, 1024), "qh": (4096, 4096),
+              "kh": (8192, 1024), "vh": (9216, 1024), "qr": (10240, 4096), "kr": (4096, 1024),
+              "att": (5120, 4096), "merged": (9216, 4096)}
+
+
+@pytest.mark.parametrize("projection_after", [True, False])
+def test_attention_group_stages_rotated_q_that_overlaps_its_inputs(hip, projection_after):
+    B, H, Hkv, S, past, D, max_seq = 1, 32, 8, 1, 1000, 128, 1100
+    theta, scale = 500000.0, float(np.float32(1.0 / math.sqrt(D)))
+    r = np.random.default_rng(31)
+    nq, nk, total = B * S * H * D, B * S * Hkv * D, 14336
+    q = r.uniform(-1, 1, nq).astype(np.float32)
+    k = r.uniform(-1, 1, nk).astype(np.float32)
+    v = r.uniform(-1, 1, nk).astype(np.float32)
+    cache = r.uniform(-1, 1, B * 2 * max_seq * Hkv * D).astype(np.float32)
+    pos = np.full(B * S, past, np.uint32)
+    init = np.zeros(total, np.float32)
+    for name, arr in (("q", q), ("k", k), ("v", v)):
+        o, n = LAST_LAYER[name]
+        init[o:o + n] = arr
+    scratch = hip.upload_new_f32(init)
+    cb = hip.upload_new_f32(cache)
+    pb = hip.upload_new_u32(pos)
+    proj = r.uniform(-1, 1, 4096).astype(np.float32)
+    pr = hip.upload_new_f32(proj)
+    ref = {name: BufferRef(scratch, o, n) for name, (o, n) in LAST_LAYER.items()}
+    posr = BufferRef(pb, 0, B * S)
+    qf, kf = Value.f32([B, S, H * D]), Value.f32([B, S, Hkv * D])
+    q4, k4 = Value.f32([B, H, S, D]), Value.f32([B, Hkv, S, D])
+    pv = Value.u32([B, S])
+    before = hip.stats()
+    hip.dispatch(Op.split_heads(H, D), [ref["q"]], [qf], [ref["qh"]], [q4])
+    hip.dispatch(Op.split_heads(Hkv, D), [ref["k"]], [kf], [ref["kh"]], [k4])
+    hip.dispatch(Op.split_heads(Hkv, D), [ref["v"]], [kf], [ref["vh"]], [k4])
+    hip.dispatch(Op.rope(RopeVariant.NEOX, theta), [ref["qh"], posr], [q4, pv], [ref["qr"]], [q4])
+    hip.dispatch(Op.rope(RopeVariant.NEOX, theta), [ref["kh"], posr], [k4, pv], [ref["kr"]], [k4])
+    hip.dispatch(Op.causal_attention(0, H, Hkv, D, scale),
+                 [ref["qr"], ref["kr"], ref["vh"], BufferRef(cb, 0, cache.size)],
+                 [q4, k4, k4, Value.f32([B, 1, 2, max_seq, Hkv, D], ValueRole.STATE)],
+                 [ref["att"]], [q4], [past])
+    hip.dispatch(Op.merge_heads(H, D), [ref["att"]], [q4], [ref["merged"]], [qf])
+    if projection_after:
+        # in place of the output projection, which writes [4096, 8192)
+        pvv = Value.f32([4096])
+        hip.dispatch(Op.scale_by(2.0), [BufferRef(pr, 0, 4096)], [pvv], [BufferRef(scratch, 4096, 4096)], [pvv])
+    hip.synchronize()
+    after = hip.stats()
+    assert after["fused_commands"] - before["fused_commands"] >= 7
+
+    # the op sequence on the oracle, writing the same layout in order
+    qh = oracle.split_heads(q, B, S, H, D)
+    kh = oracle.split_heads(k, B, S, Hkv, D)
+    vh = oracle.split_heads(v, B, S, Hkv, D)
+    qr = oracle.rope(qh, pos, B, H, S, D, theta, "neox")
+    kr = oracle.rope(kh, pos, B, Hkv, S, D, theta, "neox")
+    att, want_cache = oracle.causal_attention(qr, kr, vh, cache, B, 1, 0, H, Hkv, S, past, D, max_seq, scale)
+    merged = oracle.merge_heads(att, B, S, H, D)
+    want = init.copy()
+    kind = np.zeros(total, np.int8)  # 0 exact, 1 Rope, 2 attention
+    steps = [("qh", qh, 0), ("kh", kh, 0), ("vh", vh, 0), ("qr", qr, 1), ("kr", kr, 1), ("att", att, 2),
+             ("merged", merged, 2)]
+    for name, val, kd in steps:
+        o, n = LAST_LAYER[name]
+        want[o:o + n] = val
+        kind[o:o + n] = kd
+    if projection_after:
+        want[4096:8192] = proj * np.float32(2.0)
+        kind[4096:8192] = 0
+    got = hip.read_f32(scratch, total)
+    np.testing.assert_array_equal(got[kind == 0], want[kind == 0])
+    assert rel_l2(got[kind == 1], want[kind == 1]) <= 1e-6
+    assert_normwise(got[kind == 2], want[kind == 2])
+    # the rotated q tail is what the staged copy wrote
+    assert np.count_nonzero(kind == 1) >= 1024
+    assert rel_l2(hip.read_f32(cb, cache.size), want_cache) <= 1e-6
+
+
+@pytest.mark.parametrize("silu_first", [True, False])
+@pytest.mark.parametrize("dead", [True, False])
+def test_silu_then_mul_fuses_only_when_the_silu_result_is_dead(hip, silu_first, dead):
+    n = 10007  # ragged: vector body plus a scalar tail
+    r = np.random.default_rng(41 + silu_first + 2 * dead)
+    x = (r.standard_normal(n) * 4).astype(np.float32)
+    u = r.standard_normal(n).astype(np.float32)
+    src = r.standard_normal(n).astype(np.float32)
+    # scratch layout: x | u | t | out | src
+    stride = (n + 63) // 64 * 64
+    init = np.zeros(5 * stride, np.float32)
+    init[0:n], init[stride:stride + n], init[4 * stride:4 * stride + n] = x, u, src
+    v = Value.f32([n])
+
+    def run(fusion):
+        buf = hip.upload_new_f32(init)
+        xr, ur, tr, outr, srcr = [BufferRef(buf, i * stride, n) for i in range(5)]
+        hip.set_options(fusion=fusion)
+        before = hip.stats()
+        hip.dispatch(Op.silu(), [xr], [v], [tr], [v])
+        hip.dispatch(Op.mul(), [tr, ur] if silu_first else [ur, tr], [v, v], [outr], [v])
+        if dead:
+            hip.dispatch(Op.scale_by(0.5), [srcr], [v], [tr], [v])  # overwrites every element of t
+        hip.synchronize()
+        fused = hip.stats()["fused_commands"] - before["fused_commands"]
+        hip.set_options()
+        got = hip.read_f32(buf, 5 * stride)
+        return fused, got[3 * stride:3 * stride + n], got[2 * stride:2 * stride + n]
+
+    fused, out, t = run(True)
+    assert fused == (2 if dead else 0)
+    unfused, out_ref, t_ref = run(False)
+    assert unfused == 0
+    # the same IEEE operations as the op pair: bit-identical to it
+    np.testing.assert_array_equal(out, out_ref)
+    np.testing.assert_array_equal(t, t_ref)
+    t_want = oracle.silu(x)
+    want = oracle.mul(t_want, u, n) if silu_first else oracle.mul(u, t_want, n)
+    assert rel_l2(out, want) <= 1e-6
+    if dead:
+        np.testing.assert_array_equal(t, oracle.scale(src, 0.5))
+    else:
+        assert rel_l2(t, t_want) <= 1e-6

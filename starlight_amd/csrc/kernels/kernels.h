@@ -145,6 +145,11 @@ uint64_t quant_tile_scale_floats(uint64_t n, uint64_t k, uint32_t group, QuantLa
 hipError_t launch_scale_repack(const float* scales, float* tile_scales, uint64_t n, uint64_t k, uint32_t group,
                                hipStream_t s);
 // out[m, n] = sum_k a[m, k] * dequant(w)[n, k]  (a: [m, k] row-major)
+// m > 16 on the Mfma layout (k % 128 == 0): fp16 matrix cores on activations
+// split into two fp16 parts per element; hipErrorNotSupported when the
+// shape or the workspace does not fit (nothing launched).
+hipError_t launch_qgemm_mfma(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
+                             hipStream_t s);
 hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
                           hipStream_t s);
 // The MFMA decode path (m <= 16, Mfma layout); returns hipErrorNotSupported

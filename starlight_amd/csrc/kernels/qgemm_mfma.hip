@@ -1,0 +1,265 @@
+// Group-quantized MatMulNT for many activation rows (prefill):
+// out[m, n] = sum_k a[m, k] * (q[n, k] * s[n, k / G]), on the fp16 matrix
+// cores, from the Mfma tile layout of the weights.
+//
+// Exactness plan. The codes q are small integers, exact in fp16. Each
+// activation row is scaled by 2^(15 - E) (|a| < 2^E over the row, so the
+// scaled values stay below the fp16 maximum) and split into a high and a
+// low fp16 part, a' = hi + lo, which keeps about 22 significant bits of
+// every element (elements far below the row maximum keep an absolute error
+// below 2^-25 of it). v_mfma_f32_16x16x32_f16 forms hi * q and lo * q exactly
+// and sums them in f32 over one quantization group; the group's sum is then
+// multiplied by its scale and added to the f32 result, and the result is
+// scaled back by 2^(E - 15). Against matmul_nt(a, dequant(q, s))
+// (reference/matmul.rs:29-59, dequant one f32 multiply q * s) the only
+// differences are f32 rounding (summation order, the scale applied per
+// group instead of per weight) and the split's 2^-22: about 1e-6 normwise,
+// inside the 1e-4 bound.
+//
+// Kernels
+//  * split_rows: one block per row: E, then hi/lo in fp16 ([m][k] each)
+//    and E per row into the workspace;
+//  * qgemm_mfma: 128 x 128 output tiles, 4 waves of 64 x 64 (4 x 4 MFMA
+//    tiles of 16 x 16), k in steps of 32 through double-buffered LDS. The
+//    weight step is read from the tile layout (per 16-row tile and 128-k
+//    superblock; the 32-k step is half of one 64-k half: 32 lanes x 8 bytes
+//    for INT4, x 16 bytes for INT8) and converted to fp16 codes in LDS.
+#include "common.h"
+#include "kernels.h"
+#include "starlight_hip.h"
+
+namespace slhip {
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 128;     // output rows and columns per block
+constexpr int kStepK = 32;     // k per MFMA step and per LDS stage
+constexpr int kRowPad = 40;    // halves per LDS row: 80 bytes, conflict-free 16-byte lane reads
+constexpr int kExpBias = 15;   // scaled rows stay below 2^15
+
+// Row r: E with max |a| < 2^E (0 for an all-zero row), then hi/lo of
+// a * 2^(15 - E). k % 4 == 0 and a row 16-byte aligned.
+__global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, _Float16* __restrict__ hi,
+                                                  _Float16* __restrict__ lo, int* __restrict__ row_exp,
+                                                  uint32_t k) {
+    __shared__ float scratch[4];
+    const uint64_t r = blockIdx.x;
+    const float4* row = reinterpret_cast<const float4*>(a + r * k);
+    const uint32_t k4 = k / 4;
+    float mx = 0.f;
+    for (uint32_t i = threadIdx.x; i < k4; i += 256) {
+        const float4 v = row[i];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    mx = block_max(mx, scratch);
+    int e = 0;
+    if (mx != 0.f) frexpf(mx, &e);  // mx < 2^e
+    if (threadIdx.x == 0) row_exp[r] = e;
+    const int shift = kExpBias - e;
+    for (uint32_t i = threadIdx.x; i < k4; i += 256) {
+        const float4 v = row[i];
+        const float x[4] = {ldexpf(v.x, shift), ldexpf(v.y, shift), ldexpf(v.z, shift), ldexpf(v.w, shift)};
+        _Float16 h[4], l[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h[j] = static_cast<_Float16>(x[j]);
+            l[j] = static_cast<_Float16>(x[j] - static_cast<float>(h[j]));  // the subtraction is exact
+        }
+        typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<v4h*>(hi + r * k + 4 * i) = v4h{h[0], h[1], h[2], h[3]};
+        *reinterpret_cast<v4h*>(lo + r * k + 4 * i) = v4h{l[0], l[1], l[2], l[3]};
+    }
+}
+
+struct GemmArgs {
+    const _Float16* ahi;
+    const _Float16* alo;
+    const int* row_exp;
+    const uint8_t* tiles;   // Mfma layout
+    const float* scales;    // [n, k / group], row-major
+    float* out;             // [m, n]
+    uint32_t m, n, k, group, groups, sb_total, n_tiles;
+};
+
+// A signed nibble (two's complement) of byte b, bit offset 0 or 4, as fp16.
+__device__ __forceinline__ _Float16 nib(uint32_t word, int shift) {
+    return static_cast<_Float16>(static_cast<int>(word << (28 - shift)) >> 28);
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void qgemm_mfma(GemmArgs p) {
+    prefetch_kernarg<arg_bytes<GemmArgs>()>();
+    __shared__ __align__(16) _Float16 as[2][2][kTile][kRowPad];  // [stage][hi, lo][row][k]
+    __shared__ __align__(16) _Float16 bs[2][kTile][kRowPad];     // [stage][column][k]
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int wm = wave / 2, wn = wave % 2;
+    const uint32_t m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+    const uint32_t steps = p.k / kStepK, group_steps = p.group / kStepK;
+
+    // This thread's share of a stage: two 16-byte chunks of each of hi and
+    // lo (row c / 4, halves 8 (c % 4) ..), and one 32-lane slice of a
+    // weight tile (tile tid / 32, lane within the slice tid % 32).
+    // (plain variables, not arrays: an array the lambdas capture would be
+    // placed in LDS by the compiler)
+    const uint32_t c0 = tid, c1 = tid + 256;
+    const uint64_t aoff0 = static_cast<uint64_t>(min(m0 + c0 / 4, p.m - 1)) * p.k + 8 * (c0 % 4);
+    const uint64_t aoff1 = static_cast<uint64_t>(min(m0 + c1 / 4, p.m - 1)) * p.k + 8 * (c1 % 4);
+    const uint32_t bt = min(n0 / 16 + tid / 32, p.n_tiles - 1), bi = tid % 32;
+    uint4 rh0, rl0, rh1, rl1, rb;
+    auto load_stage = [&](uint32_t st) {
+        const uint32_t k0 = st * kStepK;
+        rh0 = *reinterpret_cast<const uint4*>(p.ahi + aoff0 + k0);
+        rl0 = *reinterpret_cast<const uint4*>(p.alo + aoff0 + k0);
+        rh1 = *reinterpret_cast<const uint4*>(p.ahi + aoff1 + k0);
+        rl1 = *reinterpret_cast<const uint4*>(p.alo + aoff1 + k0);
+        const uint32_t sb = k0 / 128, t = (k0 % 128) / kStepK, s = t / 2;
+        const uint32_t L = (2 * (t % 2) + bi / 16) * 16 + bi % 16;
+        const uint64_t tile = static_cast<uint64_t>(bt) * p.sb_total + sb;
+        if constexpr (BITS == 4) {
+            const uint2 w = *reinterpret_cast<const uint2*>(p.tiles + tile * 1024 + L * 16 + s * 8);
+            rb = make_uint4(w.x, w.y, 0u, 0u);
+        } else {
+            rb = *reinterpret_cast<const uint4*>(p.tiles + tile * 2048 + s * 1024 + L * 16);
+        }
+    };
+    auto store_stage = [&](int buf) {
+        *reinterpret_cast<uint4*>(&as[buf][0][c0 / 4][8 * (c0 % 4)]) = rh0;
+        *reinterpret_cast<uint4*>(&as[buf][1][c0 / 4][8 * (c0 % 4)]) = rl0;
+        *reinterpret_cast<uint4*>(&as[buf][0][c1 / 4][8 * (c1 % 4)]) = rh1;
+        *reinterpret_cast<uint4*>(&as[buf][1][c1 / 4][8 * (c1 % 4)]) = rl1;
+        // 16 codes of column (tid / 32) * 16 + bi % 16, k 16 (bi / 16) .. + 15
+        v8h q0, q1;
+        if constexpr (BITS == 4) {
+            // byte b of word 0: k = b (low nibble), 4 + b (high); word 1: 8 + b, 12 + b
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                q0[b] = nib(rb.x, 8 * b);
+                q0[4 + b] = nib(rb.x, 8 * b + 4);
+                q1[b] = nib(rb.y, 8 * b);
+                q1[4 + b] = nib(rb.y, 8 * b + 4);
+            }
+        } else {
+            const uint32_t w[4] = {rb.x, rb.y, rb.z, rb.w};
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {
+                const _Float16 v = static_cast<_Float16>(static_cast<int>(w[b / 4] << (24 - 8 * (b % 4))) >> 24);
+                if (b < 8) q0[b] = v;
+                else q1[b - 8] = v;
+            }
+        }
+        _Float16* dst = &bs[buf][(tid / 32) * 16 + bi % 16][16 * (bi / 16)];
+        *reinterpret_cast<v8h*>(dst) = q0;
+        *reinterpret_cast<v8h*>(dst + 8) = q1;
+    };
+
+    v4f acc[4][4], tmp[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+            tmp[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    // the scale column of this lane in each of the wave's 4 column tiles
+    uint32_t scol[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) scol[j] = min(n0 + 64 * wn + 16 * j + lane % 16, p.n - 1);
+    float sv[4];
+
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    for (uint32_t st = 0; st < steps; ++st) {
+        const int buf = st & 1;
+        if (st + 1 < steps) load_stage(st + 1);
+        if (st % group_steps == 0) {
+            const uint32_t g = st / group_steps;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sv[j] = p.scales[static_cast<uint64_t>(scol[j]) * p.groups + g];
+        }
+        // operands: A rows 64 wm + 16 i + lane % 16, B columns 64 wn + 16 j + lane % 16,
+        // k 8 (lane / 16) .. + 7 of the step
+        const int kq = 8 * (lane / 16);
+        v8h bq[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bq[j] = *reinterpret_cast<const v8h*>(&bs[buf][64 * wn + 16 * j + lane % 16][kq]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const v8h ah = *reinterpret_cast<const v8h*>(&as[buf][0][64 * wm + 16 * i + lane % 16][kq]);
+            const v8h al = *reinterpret_cast<const v8h*>(&as[buf][1][64 * wm + 16 * i + lane % 16][kq]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[j], tmp[i][j], 0, 0, 0);
+                tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[j], tmp[i][j], 0, 0, 0);
+            }
+        }
+        if (st % group_steps == group_steps - 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(tmp[i][j][e], sv[j], acc[i][j][e]);
+                    tmp[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+        if (st + 1 < steps) store_stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    // lane holds rows 4 (lane / 16) + e of each row tile, column lane % 16
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t row = m0 + 64 * wm + 16 * i + 4 * (lane / 16) + e;
+            if (row >= p.m) continue;
+            const int sh = p.row_exp[row] - kExpBias;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t col = n0 + 64 * wn + 16 * j + lane % 16;
+                if (col < p.n) p.out[static_cast<uint64_t>(row) * p.n + col] = ldexpf(acc[i][j][e], sh);
+            }
+        }
+}
+
+}  // namespace
+
+hipError_t launch_qgemm_mfma(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
+                             hipStream_t s) {
+    if (w.layout != QuantLayout::Mfma || w.k % 128 != 0 || w.group % kStepK != 0 || w.k % w.group != 0 ||
+        !aligned16(a) || m == 0 || m > 0xffffffffull || w.n > 0xffffffffull || w.k > 0xffffffffull)
+        return hipErrorNotSupported;
+    // workspace: hi and lo (fp16, m x k each), then the row exponents
+    const uint64_t half_floats = (m * w.k + 1) / 2;  // one array of m * k halves, in floats
+    const uint64_t hi_at = 0, lo_at = (half_floats + 63) / 64 * 64, exp_at = lo_at + (half_floats + 63) / 64 * 64;
+    if (exp_at + m > ws.floats) return hipErrorNotSupported;
+    _Float16* hi = reinterpret_cast<_Float16*>(ws.data + hi_at);
+    _Float16* lo = reinterpret_cast<_Float16*>(ws.data + lo_at);
+    int* row_exp = reinterpret_cast<int*>(ws.data + exp_at);
+    split_rows<<<static_cast<unsigned>(m), 256, 0, s>>>(a, hi, lo, row_exp, static_cast<uint32_t>(w.k));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    GemmArgs p;
+    p.ahi = hi;
+    p.alo = lo;
+    p.row_exp = row_exp;
+    p.tiles = w.tiles;
+    p.scales = w.scales;
+    p.out = out;
+    p.m = static_cast<uint32_t>(m);
+    p.n = static_cast<uint32_t>(w.n);
+    p.k = static_cast<uint32_t>(w.k);
+    p.group = w.group;
+    p.groups = static_cast<uint32_t>(w.k / w.group);
+    p.sb_total = static_cast<uint32_t>(w.k / 128);
+    p.n_tiles = static_cast<uint32_t>((w.n + 15) / 16);
+    const dim3 grid(static_cast<unsigned>((w.n + kTile - 1) / kTile), static_cast<unsigned>((m + kTile - 1) / kTile));
+    if (w.format == SL_QFORMAT_INT4) qgemm_mfma<4><<<grid, 256, 0, s>>>(p);
+    else qgemm_mfma<8><<<grid, 256, 0, s>>>(p);
+    return hipGetLastError();
+}
+
+}  // namespace slhip

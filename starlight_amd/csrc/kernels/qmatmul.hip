@@ -21,8 +21,10 @@
 //  * qgemv_valu — m <= 16 on the RowMajor layout: one wave owns 4 weight
 //    rows; lanes walk 16-byte chunks of those rows, so a wave's load covers
 //    1 KiB of one row contiguously; x chunks are shared by the 4 rows;
-//  * qgemm_tiled — large m: the SGEMM tile loop with the B tile decoded into
-//    LDS as f32 (either layout);
+//  * qgemm_mfma (qgemm_mfma.hip) — m > 16 on the Mfma layout: fp16 matrix
+//    cores on split activations;
+//  * qgemm_tiled — large m otherwise: the SGEMM tile loop with the B tile
+//    decoded into LDS as f32 (either layout);
 //  * qmm_generic — any geometry (correctness path, either layout).
 #include "common.h"
 #include "kernels.h"
@@ -352,6 +354,10 @@ hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint
         e = launch_qgemv_mfma(a, w, out, m, ws, s);
         if (e != hipErrorNotSupported) return e;
         (void)hipGetLastError();
+    }
+    if (mfma && m > 16) {
+        const hipError_t e = launch_qgemm_mfma(a, w, out, m, ws, s);
+        if (e != hipErrorNotSupported) return e;
     }
     const uint32_t ck = bits == 4 ? 32 : 16;
     const bool fast = !mfma && w.k % ck == 0 && w.group % ck == 0 && w.k % w.group == 0 && aligned16(a) &&

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import assert_elementwise, assert_normwise
+from conftest import assert_elementwise, assert_normwise, rel_l2
 from starlight_amd import quant
 from starlight_amd.device import DeviceError
 from starlight_amd.ir import BufferRef, Op, QuantFormat, RopeVariant, Value, ValueRole
@@ -340,6 +340,33 @@ def test_quantized_matmul_parity(hip, fmt, m, n, k, group):
     got = read(hip, orf).reshape(m, n)
     for i in range(m):
         assert_normwise(got[i], want.reshape(m, n)[i])
+
+
+@pytest.mark.parametrize("fmt,m,n,k,group", [(QuantFormat.INT4, 17, 100, 128, 128), (QuantFormat.INT8, 130, 257, 512, 64),
+                                              (QuantFormat.INT4, 300, 512, 1024, 256),
+                                              (QuantFormat.INT8, 200, 96, 2048, 128),
+                                              (QuantFormat.INT4, 512, 512, 4096, 128)])
+def test_quantized_matmul_many_rows_on_matrix_cores(hip, fmt, m, n, k, group):
+    """m > 16: the fp16 matrix-core path on split activations. Rows span nine
+    orders of magnitude (each is split against its own maximum) and row 0 is
+    all zeros."""
+    r = rng(m + n + k + group)
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    mag = (10.0 ** r.uniform(-6, 3, m)).astype(np.float32)
+    a = (r.standard_normal((m, k)).astype(np.float32) * mag[:, None]).astype(np.float32)
+    a[0] = 0.0
+    wr, wv, deq = quant_weight(hip, w, fmt, group)
+    _, ar = put(hip, a.ravel())
+    _, orf = out_buf(hip, m * n)
+    hip.dispatch(Op.matmul_nt(), [ar, wr], [Value.f32([1, m, k]), wv], [orf], [Value.f32([1, m, n])])
+    want = oracle.matmul_nt(a.ravel(), deq, 1, m, k, n).reshape(m, n)
+    got = read(hip, orf).reshape(m, n)
+    np.testing.assert_array_equal(got[0], np.zeros(n, np.float32))
+    for i in range(1, m):
+        assert_normwise(got[i], want[i])
+    # the split keeps about 22 bits per element: far inside the bound
+    worst = max(rel_l2(got[i], want[i]) for i in range(1, m))
+    assert worst <= 2e-5, worst
 
 
 @pytest.mark.parametrize("fmt", [QuantFormat.INT4, QuantFormat.INT8])

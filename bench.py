@@ -24,8 +24,17 @@ The JSON line also carries
                  host: one 8B-shaped layer decoding at 1024 cached positions
                  plus a slice of lm_head, extrapolated to a full token.
 
+--model 1b runs the 1B-class shape instead (16 layers, hidden 2048, 32/8
+heads of 64, ffn 8192, vocab 32000): 512-token prompt, 128 timed steps, KV
+cache 2048 positions; its roofline leg is the [8192 x 2048] q-GEMV over 64
+weight copies.
+
 --mode roofline runs only the q-GEMV leg and --mode copy only a plain
-copy (Scale by 1 over 64 Mi floats), for the counter runs.
+copy (Scale by 1 over 64 Mi floats), for the counter runs. --mode micro
+prints one JSON line per microbenchmark: Softmax [32 x 2048 x 2048], Add and
+fused SiLU(gate)*up [4096 x 14336], RoPE [1, 32, 4096, 128], RMSNorm, the
+q-GEMV at M = 1 (both 8B shapes, INT4 and INT8) and M = 8, and the M = 512
+q-GEMM on the fp16 matrix cores.
 """
 from __future__ import annotations
 
@@ -382,10 +391,10 @@ def cpu_model():
     return "unknown CPU"
 
 
-def cpu_baseline(cfg, budget_s=25.0):
+def cpu_baseline(cfg, prompt_len=PROMPT_LEN, label="8B", budget_s=25.0):
     """Times the oracle (scalar C restatement of backend-cpu, one core) on one
-    8B-shaped layer decoding with 1024 positions already cached, plus a
-    lm_head slice, and extrapolates to a full token."""
+    layer of the model's shape decoding with prompt_len positions already
+    cached, plus a lm_head slice, and extrapolates to a full token."""
     import oracle
     from oracle.cpu_device import OracleDevice
     from starlight_amd import engine, graph
@@ -402,16 +411,16 @@ def cpu_baseline(cfg, budget_s=25.0):
         weights[spec.name] = (np.ones(spec.shape, np.float32) if spec.kind == "norm" else
                               (rng.standard_normal(spec.shape, dtype=np.float32) * np.float32(0.02)))
     bufs = engine.upload_weights(dev, one, weights)
-    pre = graph.lower_llama(one, 1, 1, PROMPT_LEN + 8)
+    pre = graph.lower_llama(one, 1, 1, prompt_len + 8)
     eng = engine.Engine(dev, engine.compile_program(pre, bufs), engine.compile_program(pre, bufs), 1,
-                        PROMPT_LEN + 8)
+                        prompt_len + 8)
     kv = eng.states[pre.kv_cache]
     dev.f32[kv][:] = rng.uniform(-1, 1, dev.f32[kv].size).astype(np.float32)
     logits = np.zeros(8, np.float32)
     t0 = time.perf_counter()
     steps = 0
     while steps < 3 and time.perf_counter() - t0 < budget_s * 0.6:
-        eng.step(eng.DECODE, [1], [PROMPT_LEN + steps], 1, PROMPT_LEN + steps, logits)
+        eng.step(eng.DECODE, [1], [prompt_len + steps], 1, prompt_len + steps, logits)
         steps += 1
     per_layer = (time.perf_counter() - t0) / steps
     # lm_head: a 1/16 row slice of [vocab, hidden] through oracle matmul_nt
@@ -423,7 +432,7 @@ def cpu_baseline(cfg, budget_s=25.0):
     lm_head = (time.perf_counter() - t1) * 16
     per_token = per_layer * cfg.layers + lm_head
     return {"value": round(1.0 / per_token, 5), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": (f"oracle decode of one 8B-shaped layer (dequantized INT4 weights, 1024 cached positions) "
+            "sample": (f"oracle decode of one {label}-shaped layer (dequantized weights, {prompt_len} cached positions) "
                        f"x {steps} steps = {per_layer:.3f} s/layer, x{cfg.layers} layers + lm_head "
                        f"(1/16 slice timed, x16) = {per_token:.2f} s/token; extrapolated; single-threaded on "
                        f"{cpu_model()} ({os.cpu_count()} logical CPUs visible)")}
@@ -435,7 +444,9 @@ def cpu_baseline(cfg, budget_s=25.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--model", choices=["8b", "1b"], default="8b",
+                    help="8b: Llama-3-8B shape, 1024-token prompt; 1b: 1B-class shape, 512-token prompt")
+    ap.add_argument("--steps", type=int, default=None, help="timed decode steps (default 256 for 8b, 128 for 1b)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--int8", action="store_true", help="INT8 g128 weights instead of INT4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -467,25 +478,35 @@ def main():
     from starlight_amd.device import HipDevice
     from starlight_amd.ir import QuantFormat
 
-    cfg = graph.LLAMA_8B_INT8 if args.int8 else graph.LLAMA_8B_INT4
-    assert PROMPT_LEN + args.warmup + args.steps <= MAX_SEQ
+    if args.model == "1b":
+        import dataclasses
+        cfg = dataclasses.replace(graph.LLAMA_1B_INT4, quant=QuantFormat.INT8 if args.int8 else QuantFormat.INT4)
+        prompt_len, max_seq, label = 512, 2048, "1B"
+        gemv_shape = dict(n=8192, k=2048, copies=64)  # gate/up projection, 64 x 8.4 MB
+    else:
+        cfg = graph.LLAMA_8B_INT8 if args.int8 else graph.LLAMA_8B_INT4
+        prompt_len, max_seq, label = PROMPT_LEN, MAX_SEQ, "8B"
+        gemv_shape = {}
+    if args.steps is None:
+        args.steps = 128 if args.model == "1b" else 256
+    assert prompt_len + args.warmup + args.steps <= max_seq
     torch.cuda.init()
     dev = HipDevice(0)
     t0 = time.perf_counter()
     bufs = upload_synthetic_weights(dev, cfg, seed=0)
     log(f"weights generated and uploaded in {time.perf_counter() - t0:.1f} s")
-    pre = engine.compile_program(graph.lower_llama(cfg, 1, PROMPT_LEN, MAX_SEQ), bufs)
-    dec = engine.compile_program(graph.lower_llama(cfg, 1, 1, MAX_SEQ), bufs)
-    eng = engine.NativeEngine(dev, pre, dec, 1, MAX_SEQ)
+    pre = engine.compile_program(graph.lower_llama(cfg, 1, prompt_len, max_seq), bufs)
+    dec = engine.compile_program(graph.lower_llama(cfg, 1, 1, max_seq), bufs)
+    eng = engine.NativeEngine(dev, pre, dec, 1, max_seq)
 
-    prompt = synth.prompt(cfg.vocab, PROMPT_LEN, 0)
+    prompt = synth.prompt(cfg.vocab, prompt_len, 0)
     logits = np.zeros(cfg.vocab, np.float32)
     t0 = time.perf_counter()
-    eng.step(eng.PREFILL, prompt, np.arange(PROMPT_LEN, dtype=np.uint32), PROMPT_LEN, 0, logits)
+    eng.step(eng.PREFILL, prompt, np.arange(prompt_len, dtype=np.uint32), prompt_len, 0, logits)
     prefill_s = time.perf_counter() - t0
-    log(f"prefill {PROMPT_LEN} tokens: {prefill_s * 1000:.1f} ms")
+    log(f"prefill {prompt_len} tokens: {prefill_s * 1000:.1f} ms")
     token = int(np.argmax(logits))
-    past = PROMPT_LEN
+    past = prompt_len
     warm = eng.decode(token, past, args.warmup)
     token, past = int(warm[-1]) if args.warmup else token, past + args.warmup
 
@@ -514,17 +535,17 @@ def main():
     step_bytes = linear + cfg.hidden * 4 + kv_bytes
     hbm_frac = step_bytes / (ms_per_step * 1e-3) / (HBM_PEAK_GBS * 1e9)
 
-    roof = qgemv_roofline(dev)
+    roof = qgemv_roofline(dev, int8=args.int8, **gemv_shape)
     log(f"q-GEMV roofline: {roof}")
     norm = rmsnorm_roofline(dev)
     log(f"RMSNorm: {norm}")
-    cpu = None if args.no_cpu else cpu_baseline(cfg)
+    cpu = None if args.no_cpu else cpu_baseline(cfg, prompt_len, label)
     if cpu:
         log(f"cpu baseline: {cpu}")
 
     quant_name = "INT8" if args.int8 else "INT4"
     result = {
-        "metric": f"decode tok/s (8B-shape {quant_name} g128, bs=1)",
+        "metric": f"decode tok/s ({label}-shape {quant_name} g128, bs=1)",
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -536,15 +557,15 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"Llama-3-8B-shaped llama-dense decode, {quant_name} g128 linear weights "
-                               f"(lm_head {quant_name}, embeddings/norms f32), batch 1, {PROMPT_LEN}-token prompt, "
-                               f"KV cache 4096 positions",
+        "config": {"workload": f"{'Llama-3-8B' if label == '8B' else '1B-class'}-shaped llama-dense decode, "
+                               f"{quant_name} g128 linear weights (lm_head {quant_name}, embeddings/norms f32), "
+                               f"batch 1, {prompt_len}-token prompt, KV cache {max_seq} positions",
                    "layers": cfg.layers, "hidden": cfg.hidden, "heads": cfg.heads, "kv_heads": cfg.kv_heads,
                    "head_dim": cfg.head_dim, "ffn": cfg.ffn, "vocab": cfg.vocab, "batch": 1,
-                   "prompt_len": PROMPT_LEN, "kv_capacity": MAX_SEQ},
+                   "prompt_len": prompt_len, "kv_capacity": max_seq},
         "decode_step_bytes": int(step_bytes),
         "decode_hbm_frac": round(hbm_frac, 4),
-        "prefill_tok_s": round(PROMPT_LEN / prefill_s, 1),
+        "prefill_tok_s": round(prompt_len / prefill_s, 1),
         "roofline": roof,
         "rmsnorm": norm,
         "cpu_baseline": cpu,

@@ -67,16 +67,16 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* global_ptr(T* p)
     return (__attribute__((address_space(1))) T*)p;
 }
 
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / kWave;
-constexpr int kMaxF4 = 8;  // float4 of activations per thread, at most (F4: this launch's)
+// W waves per block (8 or 16): a block holds at most kMaxElems activations,
+// 64 / W float4 per thread (F4: this launch's count).
+constexpr int kMaxWaves = 16;
 // Bytes between consecutive rows of the limb matrices beyond k: the A
 // operand of a 64-k step reads the same 16-byte columns of several rows,
 // and rows a multiple of the bank width apart would all hit the same banks.
 constexpr uint32_t kLimbPad = 64;
-constexpr uint32_t kMaxElems = kThreads * 4 * kMaxF4;
-// static LDS of the kernel: red, row_val, cfac, wres
-constexpr size_t kStaticLds = sizeof(float) * (kMaxF4 * kWaves + 16 + kMaxElems / 256 + 2 * kWaves * 16 * 16);
+constexpr uint32_t kMaxElems = 16384;
+// static LDS of the kernel with W waves: red, row_val, cfac, wres
+constexpr size_t static_lds(int w) { return sizeof(float) * ((64 / w) * w + 16 + kMaxElems / 256 + 2 * w * 16 * 16); }
 
 struct Seg {
     const uint8_t* tiles;
@@ -111,8 +111,10 @@ struct Item {
 // counted at run time). LR (m <= 4): the three limbs of every activation row
 // share one MFMA as its A rows 4 * m + limb, so a 64-k step is one LDS read
 // and one MFMA; otherwise (m <= 16) each limb matrix is an MFMA of its own.
-template <int BITS, int NT, int SPG, bool LR, int F4>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(Args p) {
+template <int BITS, int NT, int SPG, bool LR, int F4, int W>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(Args p) {
+    constexpr int kThreads = W * kWave, kWaves = W, kMaxF4 = 64 / W;
+    static_assert(F4 <= kMaxF4, "activations per thread beyond the block's budget");
     constexpr int GPS = SPG == 1 ? 2 : 1;
     constexpr int PF = 4;  // superblocks in flight per wave
     constexpr int WPT = kWaves / NT;  // waves per tile
@@ -568,7 +570,16 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     if (f.epilogue == kFusedPair) tiles = static_cast<uint32_t>((w0.n + 15) / 16);
     p.tiles_total = tiles;
     const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, lr = p.m <= 4;
-    const uint32_t wpt = f.epilogue == kFusedPair ? kWaves / 2 : kWaves;
+    // Waves per block: 16 for long k (the down projection, k = 14336), which
+    // doubles the weight loads in flight per CU and halves each thread's
+    // share of the activation prologue; 8 otherwise.
+#ifndef SL_GEMV_WAVES
+    const int waves = p.k >= 8192 ? 16 : 8;
+#else
+    const int waves = SL_GEMV_WAVES;
+#endif
+    const uint32_t threads = static_cast<uint32_t>(waves) * kWave;
+    const uint32_t wpt = f.epilogue == kFusedPair ? waves / 2 : waves;
     const uint32_t sb_per_group = p.group >= 128 ? p.group / 128 : 1;
     uint32_t per = (p.sb_total + wpt - 1) / wpt;
     per = (per + sb_per_group - 1) / sb_per_group * sb_per_group;
@@ -588,7 +599,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
         blocks = tiles < compute_units() ? tiles : compute_units();
         per_block = (tiles + blocks - 1) / blocks;
     } else {
-        const uint32_t max_blocks = 2 * compute_units();
+        const uint32_t max_blocks = (waves == 16 ? 1 : 2) * compute_units();
         per_block = (tiles + max_blocks - 1) / max_blocks;
         blocks = 0;
     }
@@ -599,17 +610,19 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     if (blocks == 0 || per_block == cap) blocks = (tiles + per_block - 1) / per_block;
     const size_t lds = static_cast<size_t>(3) * p.m * (p.k + kLimbPad) +
                        sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m;
-    if (lds + kStaticLds > max_lds_per_block()) return hipErrorNotSupported;
+    if (lds + static_lds(waves) > max_lds_per_block()) return hipErrorNotSupported;
     const int spg = p.group == 64 ? 1 : p.group == 128 ? 2 : 0;
     // Float4 of activations per thread, a compile-time count: the prologue
     // is straight-line code run once per wave, fetched cold by every CU at
     // each launch, so its length shows in the launch time (about 1 us for
     // the RMSNorm prologue at 8 float4 per thread against 2).
-    const uint32_t f4 = (p.m * p.k / 4 + kThreads - 1) / kThreads;
-#define SL_QGEMV_FUSED_F(B, T, G, L)                                                   \
-    (f4 <= 2   ? qgemv_fused<B, T, G, L, 2><<<blocks, kThreads, lds, s>>>(p)            \
-     : f4 <= 4 ? qgemv_fused<B, T, G, L, 4><<<blocks, kThreads, lds, s>>>(p)            \
-               : qgemv_fused<B, T, G, L, 8><<<blocks, kThreads, lds, s>>>(p))
+    const uint32_t f4 = (p.m * p.k / 4 + threads - 1) / threads;
+#define SL_QGEMV_FUSED_F(B, T, G, L)                                                                  \
+    (waves == 16 ? (f4 <= 2 ? qgemv_fused<B, T, G, L, 2, 16><<<blocks, threads, lds, s>>>(p)           \
+                            : qgemv_fused<B, T, G, L, 4, 16><<<blocks, threads, lds, s>>>(p))          \
+     : f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 8><<<blocks, threads, lds, s>>>(p)                       \
+     : f4 <= 4   ? qgemv_fused<B, T, G, L, 4, 8><<<blocks, threads, lds, s>>>(p)                       \
+                 : qgemv_fused<B, T, G, L, 8, 8><<<blocks, threads, lds, s>>>(p))
 #define SL_QGEMV_FUSED(B, T, G) (lr ? SL_QGEMV_FUSED_F(B, T, G, true) : SL_QGEMV_FUSED_F(B, T, G, false))
 #define SL_QGEMV_FUSED_G(B, T) \
     (spg == 1 ? SL_QGEMV_FUSED(B, T, 1) : spg == 2 ? SL_QGEMV_FUSED(B, T, 2) : SL_QGEMV_FUSED(B, T, 0))

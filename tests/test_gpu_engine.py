@@ -136,3 +136,25 @@ def test_8b_shaped_decode_fuses_and_replays(hip):
     assert after["fused_commands"] > before["fused_commands"]
     assert after["graph_captures"] > before["graph_captures"]
     assert after["graph_replays"] >= before["graph_replays"] + 3
+
+
+def test_model_from_a_saved_checkpoint_on_gpu(hip, tmp_path):
+    """A quantized Safetensors checkpoint (starlight_amd.formats) loaded and
+    uploaded: the same ids and logits as the f32 weights quantized on upload."""
+    from starlight_amd import formats
+    cfg = LlamaConfig(layers=2, hidden=512, heads=8, kv_heads=2, head_dim=64, ffn=1024, vocab=3000,
+                      theta=500_000.0, quant=QuantFormat.INT4)
+    weights = synth.llama_weights(cfg, 6)
+    prompt = synth.prompt(cfg.vocab, 6, 6)
+    path = str(tmp_path / "model.safetensors")
+    formats.save(path, *formats.quantize_model(cfg, weights))
+
+    def run(bufs):
+        eng = engine.NativeEngine(hip, engine.compile_program(graph.lower_llama(cfg, 1, 6, 32), bufs),
+                                  engine.compile_program(graph.lower_llama(cfg, 1, 1, 32), bufs), 1, 32)
+        return eng.generate(prompt, 4, cfg.vocab)
+
+    t_ref, l_ref = run(engine.upload_weights(hip, cfg, weights))
+    t_ck, l_ck = run(formats.upload(hip, cfg, *formats.load(path)))
+    np.testing.assert_array_equal(np.asarray(t_ck), np.asarray(t_ref))
+    np.testing.assert_array_equal(np.asarray(l_ck), np.asarray(l_ref))

@@ -73,6 +73,12 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, _
     }
 }
 
+// One stage's share of a thread: two 16-byte chunks of each of hi and lo,
+// and the weight bytes (INT4: the first 8).
+struct StageRegs {
+    uint4 h0, l0, h1, l1, b;
+};
+
 struct GemmArgs {
     const _Float16* ahi;
     const _Float16* alo;
@@ -107,28 +113,32 @@ __global__ __launch_bounds__(256) void qgemm_mfma(GemmArgs p) {
     const uint64_t aoff0 = static_cast<uint64_t>(min(m0 + c0 / 4, p.m - 1)) * p.k + 8 * (c0 % 4);
     const uint64_t aoff1 = static_cast<uint64_t>(min(m0 + c1 / 4, p.m - 1)) * p.k + 8 * (c1 % 4);
     const uint32_t bt = min(n0 / 16 + tid / 32, p.n_tiles - 1), bi = tid % 32;
-    uint4 rh0, rl0, rh1, rl1, rb;
-    auto load_stage = [&](uint32_t st) {
+    // (slots travel by value: a slot passed by reference would be placed in
+    // LDS by the compiler)
+    auto load_stage = [&](uint32_t st) -> StageRegs {
+        StageRegs r;
         const uint32_t k0 = st * kStepK;
-        rh0 = *reinterpret_cast<const uint4*>(p.ahi + aoff0 + k0);
-        rl0 = *reinterpret_cast<const uint4*>(p.alo + aoff0 + k0);
-        rh1 = *reinterpret_cast<const uint4*>(p.ahi + aoff1 + k0);
-        rl1 = *reinterpret_cast<const uint4*>(p.alo + aoff1 + k0);
+        r.h0 = *reinterpret_cast<const uint4*>(p.ahi + aoff0 + k0);
+        r.l0 = *reinterpret_cast<const uint4*>(p.alo + aoff0 + k0);
+        r.h1 = *reinterpret_cast<const uint4*>(p.ahi + aoff1 + k0);
+        r.l1 = *reinterpret_cast<const uint4*>(p.alo + aoff1 + k0);
         const uint32_t sb = k0 / 128, t = (k0 % 128) / kStepK, s = t / 2;
         const uint32_t L = (2 * (t % 2) + bi / 16) * 16 + bi % 16;
         const uint64_t tile = static_cast<uint64_t>(bt) * p.sb_total + sb;
         if constexpr (BITS == 4) {
             const uint2 w = *reinterpret_cast<const uint2*>(p.tiles + tile * 1024 + L * 16 + s * 8);
-            rb = make_uint4(w.x, w.y, 0u, 0u);
+            r.b = make_uint4(w.x, w.y, 0u, 0u);
         } else {
-            rb = *reinterpret_cast<const uint4*>(p.tiles + tile * 2048 + s * 1024 + L * 16);
+            r.b = *reinterpret_cast<const uint4*>(p.tiles + tile * 2048 + s * 1024 + L * 16);
         }
+        return r;
     };
-    auto store_stage = [&](int buf) {
-        *reinterpret_cast<uint4*>(&as[buf][0][c0 / 4][8 * (c0 % 4)]) = rh0;
-        *reinterpret_cast<uint4*>(&as[buf][1][c0 / 4][8 * (c0 % 4)]) = rl0;
-        *reinterpret_cast<uint4*>(&as[buf][0][c1 / 4][8 * (c1 % 4)]) = rh1;
-        *reinterpret_cast<uint4*>(&as[buf][1][c1 / 4][8 * (c1 % 4)]) = rl1;
+    auto store_stage = [&](int buf, StageRegs r) {
+        const uint4 rb = r.b;
+        *reinterpret_cast<uint4*>(&as[buf][0][c0 / 4][8 * (c0 % 4)]) = r.h0;
+        *reinterpret_cast<uint4*>(&as[buf][1][c0 / 4][8 * (c0 % 4)]) = r.l0;
+        *reinterpret_cast<uint4*>(&as[buf][0][c1 / 4][8 * (c1 % 4)]) = r.h1;
+        *reinterpret_cast<uint4*>(&as[buf][1][c1 / 4][8 * (c1 % 4)]) = r.l1;
         // 16 codes of column (tid / 32) * 16 + bi % 16, k 16 (bi / 16) .. + 15
         v8h q0, q1;
         if constexpr (BITS == 4) {
@@ -168,12 +178,16 @@ __global__ __launch_bounds__(256) void qgemm_mfma(GemmArgs p) {
     for (int j = 0; j < 4; ++j) scol[j] = min(n0 + 64 * wn + 16 * j + lane % 16, p.n - 1);
     float sv[4];
 
-    load_stage(0);
-    store_stage(0);
+    // Stages go global -> registers -> LDS through a ring of four register
+    // slots: the loads of stage st + 4 are issued at step st, three steps of
+    // MFMA work before their LDS store (one step is about 500 cycles, short
+    // of a memory round trip). steps (k / 32) is a multiple of 4.
+    StageRegs r0 = load_stage(0), r1 = load_stage(1), r2 = load_stage(2), r3 = load_stage(3);
+    store_stage(0, r0);
     __syncthreads();
-    for (uint32_t st = 0; st < steps; ++st) {
+    auto step = [&](uint32_t st, StageRegs mine, StageRegs next) -> StageRegs {
         const int buf = st & 1;
-        if (st + 1 < steps) load_stage(st + 1);
+        if (st + 4 < steps) mine = load_stage(st + 4);  // this slot's stage is in LDS already
         if (st % group_steps == 0) {
             const uint32_t g = st / group_steps;
 #pragma unroll
@@ -205,8 +219,15 @@ __global__ __launch_bounds__(256) void qgemm_mfma(GemmArgs p) {
                     tmp[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
                 }
         }
-        if (st + 1 < steps) store_stage(buf ^ 1);
+        if (st + 1 < steps) store_stage(buf ^ 1, next);
         __syncthreads();
+        return mine;
+    };
+    for (uint32_t st = 0; st < steps; st += 4) {
+        r0 = step(st, r0, r1);
+        r1 = step(st + 1, r1, r2);
+        r2 = step(st + 2, r2, r3);
+        r3 = step(st + 3, r3, r0);
     }
 
     // lane holds rows 4 (lane / 16) + e of each row tile, column lane % 16

@@ -214,7 +214,7 @@ def qgemv_roofline(dev, n=14336, k=4096, copies=16, launches=200, graphs=True, m
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic() if (n, k, m, int8) == (14336, 4096, 1, False) else None,
-            "kernel": f"{'qgemv_fused' if m * k <= 16384 else 'qgemv_mfma'} (q-GEMV {name} g128 [{n}x{k}] M={m})",
+            "kernel": f"{'qgemv_fused' if m * k <= 32768 else 'qgemv_mfma'} (q-GEMV {name} g128 [{n}x{k}] M={m})",
             "bytes_per_launch": algorithmic, "avg_launch_us": round(avg_us, 3)}
 
 

@@ -67,16 +67,18 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* global_ptr(T* p)
     return (__attribute__((address_space(1))) T*)p;
 }
 
-// W waves per block (8 or 16): a block holds at most kMaxElems activations,
-// 64 / W float4 per thread (F4: this launch's count).
+// W waves per block (8 or 16); each thread holds at most kMaxF4 float4 of
+// activations (F4: this launch's count), so a block holds max_elems(W).
 constexpr int kMaxWaves = 16;
 // Bytes between consecutive rows of the limb matrices beyond k: the A
 // operand of a 64-k step reads the same 16-byte columns of several rows,
 // and rows a multiple of the bank width apart would all hit the same banks.
 constexpr uint32_t kLimbPad = 64;
-constexpr uint32_t kMaxElems = 16384;
+constexpr int kMaxF4 = 8;  // float4 of activations per thread, at most
+// activations a block holds: 16384 with 8 waves, 32768 with 16
+constexpr uint32_t max_elems(int w) { return static_cast<uint32_t>(w) * kWave * 4 * kMaxF4; }
 // static LDS of the kernel with W waves: red, row_val, cfac, wres
-constexpr size_t static_lds(int w) { return sizeof(float) * ((64 / w) * w + 16 + kMaxElems / 256 + 2 * w * 16 * 16); }
+constexpr size_t static_lds(int w) { return sizeof(float) * (kMaxF4 * w + 16 + max_elems(w) / 256 + 2 * w * 16 * 16); }
 
 struct Seg {
     const uint8_t* tiles;
@@ -113,7 +115,7 @@ struct Item {
 // and one MFMA; otherwise (m <= 16) each limb matrix is an MFMA of its own.
 template <int BITS, int NT, int SPG, bool LR, int F4, int W>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(Args p) {
-    constexpr int kThreads = W * kWave, kWaves = W, kMaxF4 = 64 / W;
+    constexpr int kThreads = W * kWave, kWaves = W;
     static_assert(F4 <= kMaxF4, "activations per thread beyond the block's budget");
     constexpr int GPS = SPG == 1 ? 2 : 1;
     constexpr int PF = 4;  // superblocks in flight per wave
@@ -122,7 +124,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     extern __shared__ __align__(16) int8_t limbs[];  // [3][m][k + kLimbPad], tres [tiles][16][m]
     __shared__ float red[kMaxF4][kWaves];
     __shared__ float row_val[16];
-    __shared__ float cfac[kMaxElems / 256];  // per 256-element chunk: 2^(E-22)
+    __shared__ float cfac[max_elems(W) / 256];  // per 256-element chunk: 2^(E-22)
     __shared__ float wres[2][kWaves][16][16];
 
     prefetch_kernarg<arg_bytes<Args>()>();
@@ -281,10 +283,14 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     auto row_reduce = [&](bool is_max) {
         __syncthreads();
         for (uint32_t r = wave; r < M; r += kWaves) {
+            // kMaxF4 x W partials, one per lane for 8 waves, two for 16
             float x = 0.f;
-            const int u = lane / kWaves, w = lane % kWaves;
-            const uint32_t fb = static_cast<uint32_t>(w) * kWave + kThreads * u;
-            if (fb < total4 && fb / K4 == r) x = red[u][w];
+#pragma unroll
+            for (int e0 = 0; e0 < kMaxF4 * kWaves; e0 += kWave) {
+                const int e = e0 + lane, u = e / kWaves, w = e % kWaves;
+                const uint32_t fb = static_cast<uint32_t>(w) * kWave + kThreads * u;
+                if (fb < total4 && fb / K4 == r) x = e0 == 0 ? red[u][w] : (is_max ? fmaxf(x, red[u][w]) : x + red[u][w]);
+            }
             x = is_max ? wave_max(x) : wave_sum(x);
             if (lane == 0) row_val[r] = x;
         }
@@ -540,7 +546,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const QuantWeight& w0 = *f.w[0];
     const uint64_t k = w0.k;
     if (w0.layout != QuantLayout::Mfma || k % 256 != 0 || w0.group % 64 != 0 || k % w0.group != 0 ||
-        !(w0.group == 64 || w0.group == 128 || w0.group % 256 == 0) || f.m * k > kMaxElems || !aligned16(f.a) || (f.gamma != nullptr && !aligned16(f.gamma)) ||
+        !(w0.group == 64 || w0.group == 128 || w0.group % 256 == 0) || f.m * k > max_elems(16) || !aligned16(f.a) || (f.gamma != nullptr && !aligned16(f.gamma)) ||
         (f.normed != nullptr && !aligned16(f.normed)))
         return hipErrorNotSupported;
     if (f.epilogue == kFusedPair && f.nseg != 2) return hipErrorNotSupported;
@@ -574,7 +580,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     // doubles the weight loads in flight per CU and halves each thread's
     // share of the activation prologue; 8 otherwise.
 #ifndef SL_GEMV_WAVES
-    const int waves = p.k >= 8192 ? 16 : 8;
+    const int waves = p.k >= 8192 || p.m * p.k > max_elems(8) ? 16 : 8;
 #else
     const int waves = SL_GEMV_WAVES;
 #endif
@@ -618,8 +624,9 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     // the RMSNorm prologue at 8 float4 per thread against 2).
     const uint32_t f4 = (p.m * p.k / 4 + threads - 1) / threads;
 #define SL_QGEMV_FUSED_F(B, T, G, L)                                                                  \
-    (waves == 16 ? (f4 <= 2 ? qgemv_fused<B, T, G, L, 2, 16><<<blocks, threads, lds, s>>>(p)           \
-                            : qgemv_fused<B, T, G, L, 4, 16><<<blocks, threads, lds, s>>>(p))          \
+    (waves == 16 ? (f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 16><<<blocks, threads, lds, s>>>(p)         \
+                    : f4 <= 4 ? qgemv_fused<B, T, G, L, 4, 16><<<blocks, threads, lds, s>>>(p)         \
+                              : qgemv_fused<B, T, G, L, 8, 16><<<blocks, threads, lds, s>>>(p))        \
      : f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 8><<<blocks, threads, lds, s>>>(p)                       \
      : f4 <= 4   ? qgemv_fused<B, T, G, L, 4, 8><<<blocks, threads, lds, s>>>(p)                       \
                  : qgemv_fused<B, T, G, L, 8, 8><<<blocks, threads, lds, s>>>(p))

@@ -327,7 +327,10 @@ def quant_weight(hip, w, fmt, group):
                                          (3, 64, 4096, 128), (17, 128, 256, 128), (64, 96, 512, 64),
                                          (2, 33, 130, 2), (1, 1024, 4096, 128), (2, 512, 1024, 128),
                                          (4, 48, 2048, 256), (12, 160, 1024, 128), (16, 64, 512, 64),
-                                         (1, 4096, 14336, 128), (5, 17, 896, 128)])
+                                         (1, 4096, 14336, 128), (5, 17, 896, 128),
+                                         # 16384 < m * k <= 32768: the fused GEMV with 16 waves per block
+                                         (8, 256, 4096, 128), (2, 128, 14336, 128), (16, 96, 2048, 64),
+                                         (6, 100, 4096, 256)])
 def test_quantized_matmul_parity(hip, fmt, m, n, k, group):
     r = rng(m * n + k)
     w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
@@ -340,6 +343,43 @@ def test_quantized_matmul_parity(hip, fmt, m, n, k, group):
     got = read(hip, orf).reshape(m, n)
     for i in range(m):
         assert_normwise(got[i], want.reshape(m, n)[i])
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_rms_norm_then_quantized_projections_fuse(hip, m):
+    """RmsNorm and two MatMulNT reading its output run as one fused GEMV with
+    the norm as its prologue (at m = 8 and k = 4096, 16 waves per block and
+    two partial sums per lane in the norm's reduction); the norm output is
+    still written."""
+    k, n1, n2 = 4096, 512, 256
+    r = rng(70 + m)
+    x = r.standard_normal(m * k).astype(np.float32)
+    gamma = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    w1 = (r.standard_normal((n1, k)) * 0.02).astype(np.float32)
+    w2 = (r.standard_normal((n2, k)) * 0.02).astype(np.float32)
+    r1, v1, d1 = quant_weight(hip, w1, QuantFormat.INT4, 128)
+    r2, v2, d2 = quant_weight(hip, w2, QuantFormat.INT4, 128)
+    _, xr = put(hip, x)
+    _, gr = put(hip, gamma)
+    _, nr = out_buf(hip, m * k)
+    _, o1 = out_buf(hip, m * n1)
+    _, o2 = out_buf(hip, m * n2)
+    xv = Value.f32([1, m, k])
+    before = hip.stats()
+    hip.dispatch(Op.rms_norm(1e-5), [xr, gr], [xv, Value.f32([k], ValueRole.PARAM)], [nr], [xv])
+    hip.dispatch(Op.matmul_nt(), [nr, r1], [xv, v1], [o1], [Value.f32([1, m, n1])])
+    hip.dispatch(Op.matmul_nt(), [nr, r2], [xv, v2], [o2], [Value.f32([1, m, n2])])
+    hip.synchronize()
+    assert hip.stats()["fused_commands"] - before["fused_commands"] == 3
+    normed = oracle.rms_norm(x, gamma, m, k, 1e-5)
+    got_n = read(hip, nr).reshape(m, k)
+    for i in range(m):
+        assert_normwise(got_n[i], normed.reshape(m, k)[i])
+    for orf, deq, n in ((o1, d1, n1), (o2, d2, n2)):
+        want = oracle.matmul_nt(normed, deq, 1, m, k, n).reshape(m, n)
+        got = read(hip, orf).reshape(m, n)
+        for i in range(m):
+            assert_normwise(got[i], want[i])
 
 
 @pytest.mark.parametrize("fmt,m,n,k,group", [(QuantFormat.INT4, 17, 100, 128, 128), (QuantFormat.INT8, 130, 257, 512, 64),

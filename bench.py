@@ -29,6 +29,10 @@ heads of 64, ffn 8192, vocab 32000): 512-token prompt, 128 timed steps, KV
 cache 2048 positions; its roofline leg is the [8192 x 2048] q-GEMV over 64
 weight copies.
 
+--batch B decodes B sequences together (B prompts of the same length, one
+past_len for the batch as Engine::step takes it); `value` counts the tokens
+of all B, and the step bytes count the weights once and the KV cache B times.
+
 --mode roofline runs only the q-GEMV leg and --mode copy only a plain
 copy (Scale by 1 over 64 Mi floats), for the counter runs. --mode micro
 prints one JSON line per microbenchmark: Softmax [32 x 2048 x 2048], Add and
@@ -449,6 +453,7 @@ def main():
     ap.add_argument("--steps", type=int, default=None, help="timed decode steps (default 256 for 8b, 128 for 1b)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--int8", action="store_true", help="INT8 g128 weights instead of INT4")
+    ap.add_argument("--batch", type=int, default=1, help="sequences decoded together (value counts all of them)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--mode", choices=["full", "roofline", "copy", "micro"], default="full")
     ap.add_argument("--no-graphs", action="store_true", help="roofline/copy modes: launch eagerly")
@@ -495,31 +500,33 @@ def main():
     t0 = time.perf_counter()
     bufs = upload_synthetic_weights(dev, cfg, seed=0)
     log(f"weights generated and uploaded in {time.perf_counter() - t0:.1f} s")
-    pre = engine.compile_program(graph.lower_llama(cfg, 1, prompt_len, max_seq), bufs)
-    dec = engine.compile_program(graph.lower_llama(cfg, 1, 1, max_seq), bufs)
-    eng = engine.NativeEngine(dev, pre, dec, 1, max_seq)
+    B = args.batch
+    pre = engine.compile_program(graph.lower_llama(cfg, B, prompt_len, max_seq), bufs)
+    dec = engine.compile_program(graph.lower_llama(cfg, B, 1, max_seq), bufs)
+    eng = engine.NativeEngine(dev, pre, dec, B, max_seq)
 
-    prompt = synth.prompt(cfg.vocab, prompt_len, 0)
-    logits = np.zeros(cfg.vocab, np.float32)
+    prompt = np.concatenate([synth.prompt(cfg.vocab, prompt_len, b) for b in range(B)])
+    logits = np.zeros(B * cfg.vocab, np.float32)
     t0 = time.perf_counter()
-    eng.step(eng.PREFILL, prompt, np.arange(prompt_len, dtype=np.uint32), prompt_len, 0, logits)
+    eng.step(eng.PREFILL, prompt, np.tile(np.arange(prompt_len, dtype=np.uint32), B), prompt_len, 0, logits)
     prefill_s = time.perf_counter() - t0
-    log(f"prefill {prompt_len} tokens: {prefill_s * 1000:.1f} ms")
-    token = int(np.argmax(logits))
+    log(f"prefill {B} x {prompt_len} tokens: {prefill_s * 1000:.1f} ms")
+    tokens = logits.reshape(B, cfg.vocab).argmax(axis=1).astype(np.uint32)
     past = prompt_len
-    warm = eng.decode(token, past, args.warmup)
-    token, past = int(warm[-1]) if args.warmup else token, past + args.warmup
+    if args.warmup:
+        tokens = eng.decode_batch(tokens, past, args.warmup)[-1]
+    past += args.warmup
 
     dev.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    timed = eng.decode(token, past, args.steps)
+    timed = eng.decode_batch(tokens, past, args.steps) if B > 1 else eng.decode(int(tokens[0]), past, args.steps)
     dev.synchronize()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1000.0 / args.steps
-    tok_s = args.steps / elapsed
-    log(f"decode: {tok_s:.1f} tok/s ({ms_per_step:.3f} ms/step); last tokens {timed[-4:].tolist()}")
+    tok_s = B * args.steps / elapsed
+    log(f"decode: {tok_s:.1f} tok/s ({ms_per_step:.3f} ms/step, batch {B}); last tokens {timed[-4:].tolist()}")
 
     # bytes one decode step must move at least (weights + KV read at the timed positions)
     linear = 0
@@ -532,20 +539,20 @@ def main():
             linear += spec.shape[0] * 4
     avg_keys = past + (args.steps + 1) / 2
     kv_bytes = avg_keys * cfg.layers * 2 * cfg.kv_heads * cfg.head_dim * 4
-    step_bytes = linear + cfg.hidden * 4 + kv_bytes
+    step_bytes = linear + B * (cfg.hidden * 4 + kv_bytes)
     hbm_frac = step_bytes / (ms_per_step * 1e-3) / (HBM_PEAK_GBS * 1e9)
 
     roof = qgemv_roofline(dev, int8=args.int8, **gemv_shape)
     log(f"q-GEMV roofline: {roof}")
     norm = rmsnorm_roofline(dev)
     log(f"RMSNorm: {norm}")
-    cpu = None if args.no_cpu else cpu_baseline(cfg, prompt_len, label)
+    cpu = None if args.no_cpu or B > 1 else cpu_baseline(cfg, prompt_len, label)
     if cpu:
         log(f"cpu baseline: {cpu}")
 
     quant_name = "INT8" if args.int8 else "INT4"
     result = {
-        "metric": f"decode tok/s ({label}-shape {quant_name} g128, bs=1)",
+        "metric": f"decode tok/s ({label}-shape {quant_name} g128, bs={B})",
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -559,13 +566,13 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{'Llama-3-8B' if label == '8B' else '1B-class'}-shaped llama-dense decode, "
                                f"{quant_name} g128 linear weights (lm_head {quant_name}, embeddings/norms f32), "
-                               f"batch 1, {prompt_len}-token prompt, KV cache {max_seq} positions",
+                               f"batch {B}, {prompt_len}-token prompt, KV cache {max_seq} positions",
                    "layers": cfg.layers, "hidden": cfg.hidden, "heads": cfg.heads, "kv_heads": cfg.kv_heads,
-                   "head_dim": cfg.head_dim, "ffn": cfg.ffn, "vocab": cfg.vocab, "batch": 1,
+                   "head_dim": cfg.head_dim, "ffn": cfg.ffn, "vocab": cfg.vocab, "batch": B,
                    "prompt_len": prompt_len, "kv_capacity": max_seq},
         "decode_step_bytes": int(step_bytes),
         "decode_hbm_frac": round(hbm_frac, 4),
-        "prefill_tok_s": round(prompt_len / prefill_s, 1),
+        "prefill_tok_s": round(B * prompt_len / prefill_s, 1),
         "roofline": roof,
         "rmsnorm": norm,
         "cpu_baseline": cpu,

@@ -100,6 +100,14 @@ sl_status sl_engine_generate(sl_engine *engine, const uint32_t *prompt, size_t p
 sl_status sl_engine_decode(sl_engine *engine, uint32_t token, uint32_t past_len, uint32_t steps,
                            uint32_t *tokens_out);
 
+/* Greedy decode of a batch compiled into the decode program (batch rows of
+ * one token each, all at position `past_len + step`, as Engine::step takes
+ * one past_len for the batch): `tokens` holds the batch's first tokens;
+ * tokens_out receives steps x batch ids, step-major. Each step is
+ * sl_engine_step followed by each row's first maximum logit. */
+sl_status sl_engine_decode_batch(sl_engine *engine, const uint32_t *tokens, uint32_t past_len, uint32_t steps,
+                                 uint32_t *tokens_out);
+
 /* The BufferId the engine allocated for a State value (e.g. to inspect or
  * reset the KV cache), or UINT32_MAX. */
 uint32_t sl_engine_state_buffer(const sl_engine *engine, uint32_t value);

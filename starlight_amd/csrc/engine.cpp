@@ -317,19 +317,34 @@ sl_status sl_engine_generate(sl_engine* e, const uint32_t* prompt, size_t prompt
     return SL_OK;
 }
 
-sl_status sl_engine_decode(sl_engine* e, uint32_t token, uint32_t past_len, uint32_t steps,
-                           uint32_t* tokens_out) {
+sl_status sl_engine_decode_batch(sl_engine* e, const uint32_t* tokens, uint32_t past_len, uint32_t steps,
+                                 uint32_t* tokens_out) {
     Program& dc = e->programs[SL_STEP_DECODE];
-    if (dc.batch != 1 || dc.seq != 1) return SL_ERR_EXECUTION;
-    const size_t vocab = dc.logits_elements;
+    const size_t batch = dc.batch;
+    if (dc.seq != 1 || dc.token_elements != batch || (dc.has_positions && dc.position_elements != batch) ||
+        dc.logits_elements % batch != 0)
+        return SL_ERR_EXECUTION;
+    const size_t vocab = dc.logits_elements / batch;
+    std::vector<uint32_t> cur(tokens, tokens + batch), pos(batch);
     for (uint32_t s = 0; s < steps; ++s) {
         const uint32_t past = past_len + s;
-        sl_status st = sl_engine_step(e, SL_STEP_DECODE, &token, 1, &past, 1, 1, past, e->logits_host.data(), vocab);
+        for (size_t b = 0; b < batch; ++b) pos[b] = past;
+        sl_status st = sl_engine_step(e, SL_STEP_DECODE, cur.data(), batch, pos.data(), batch, 1, past,
+                                      e->logits_host.data(), dc.logits_elements);
         if (st != SL_OK) return st;
-        token = first_argmax(e->logits_host.data(), vocab);
-        tokens_out[s] = token;
+        for (size_t b = 0; b < batch; ++b) {
+            cur[b] = first_argmax(e->logits_host.data() + b * vocab, vocab);
+            tokens_out[static_cast<size_t>(s) * batch + b] = cur[b];
+        }
     }
     return SL_OK;
+}
+
+sl_status sl_engine_decode(sl_engine* e, uint32_t token, uint32_t past_len, uint32_t steps,
+                           uint32_t* tokens_out) {
+    const Program& dc = e->programs[SL_STEP_DECODE];
+    if (dc.batch != 1 || dc.seq != 1) return SL_ERR_EXECUTION;
+    return sl_engine_decode_batch(e, &token, past_len, steps, tokens_out);
 }
 
 uint32_t sl_engine_state_buffer(const sl_engine* e, uint32_t value) {

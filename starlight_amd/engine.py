@@ -130,6 +130,8 @@ def _declare_engine(lib):
     lib.sl_engine_generate.restype = ctypes.c_int
     lib.sl_engine_decode.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, U32P]
     lib.sl_engine_decode.restype = ctypes.c_int
+    lib.sl_engine_decode_batch.argtypes = [P, U32P, ctypes.c_uint32, ctypes.c_uint32, U32P]
+    lib.sl_engine_decode_batch.restype = ctypes.c_int
     lib.sl_engine_state_buffer.argtypes = [P, ctypes.c_uint32]
     lib.sl_engine_state_buffer.restype = ctypes.c_uint32
     lib.sl_engine_destroy.argtypes = [P]
@@ -202,6 +204,13 @@ class NativeEngine:
         tokens = np.zeros(max(steps, 1), np.uint32)
         self._raise(self._lib.sl_engine_decode(self._h, token, past_len, steps, _u32p(tokens)))
         return tokens[:steps]
+
+    def decode_batch(self, tokens, past_len: int, steps: int) -> np.ndarray:
+        """Greedy decode of the compiled batch: ids [steps, batch]."""
+        first = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.zeros((max(steps, 1), first.size), np.uint32)
+        self._raise(self._lib.sl_engine_decode_batch(self._h, _u32p(first), past_len, steps, _u32p(out)))
+        return out[:steps]
 
     def state_buffer(self, value: int) -> int:
         return int(self._lib.sl_engine_state_buffer(self._h, value))

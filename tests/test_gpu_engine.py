@@ -158,3 +158,32 @@ def test_model_from_a_saved_checkpoint_on_gpu(hip, tmp_path):
     t_ck, l_ck = run(formats.upload(hip, cfg, *formats.load(path)))
     np.testing.assert_array_equal(np.asarray(t_ck), np.asarray(t_ref))
     np.testing.assert_array_equal(np.asarray(l_ck), np.asarray(l_ref))
+
+
+def test_batched_decode_matches_a_step_loop(hip):
+    """sl_engine_decode_batch: two sequences decoded together give the ids of
+    a loop of engine steps with each row's first maximum taken by numpy."""
+    cfg, B, prompt_len, steps, max_seq = graph.TINY, 2, 6, 5, 32
+    weights = synth.llama_weights(cfg, 8)
+    bufs = engine.upload_weights(hip, cfg, weights)
+    prompts = np.concatenate([synth.prompt(cfg.vocab, prompt_len, 8 + b) for b in range(B)])
+    positions = np.tile(np.arange(prompt_len, dtype=np.uint32), B)
+
+    def fresh():
+        eng = engine.NativeEngine(hip, engine.compile_program(graph.lower_llama(cfg, B, prompt_len, max_seq), bufs),
+                                  engine.compile_program(graph.lower_llama(cfg, B, 1, max_seq), bufs), B, max_seq)
+        logits = np.zeros(B * cfg.vocab, np.float32)
+        eng.step(eng.PREFILL, prompts, positions, prompt_len, 0, logits)
+        return eng, logits.reshape(B, cfg.vocab).argmax(axis=1).astype(np.uint32)
+
+    eng, first = fresh()
+    got = eng.decode_batch(first, prompt_len, steps)
+    eng, cur = fresh()
+    want = []
+    logits = np.zeros(B * cfg.vocab, np.float32)
+    for s in range(steps):
+        past = prompt_len + s
+        eng.step(eng.DECODE, cur, np.full(B, past, np.uint32), 1, past, logits)
+        cur = logits.reshape(B, cfg.vocab).argmax(axis=1).astype(np.uint32)
+        want.append(cur.copy())
+    np.testing.assert_array_equal(got, np.stack(want))

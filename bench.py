@@ -414,6 +414,7 @@ def cpu_baseline(cfg, prompt_len=PROMPT_LEN, label="8B", budget_s=25.0):
     for spec in weight_specs(one):
         weights[spec.name] = (np.ones(spec.shape, np.float32) if spec.kind == "norm" else
                               (rng.standard_normal(spec.shape, dtype=np.float32) * np.float32(0.02)))
+    oracle.set_threads(1)  # the reference is single-threaded
     bufs = engine.upload_weights(dev, one, weights)
     pre = graph.lower_llama(one, 1, 1, prompt_len + 8)
     eng = engine.Engine(dev, engine.compile_program(pre, bufs), engine.compile_program(pre, bufs), 1,

@@ -114,6 +114,12 @@ uint32_t sl_engine_state_buffer(const sl_engine *engine, uint32_t value);
 
 void sl_engine_destroy(sl_engine *engine);
 
+/* The greedy choice the loops above make over one row of logits: the first
+ * index of the largest value (strict >, so ties keep the first; a NaN is
+ * never taken past index 0), as one sequential scan gives it. Host code
+ * only (no device call). */
+uint32_t sl_engine_first_argmax(const float *logits, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

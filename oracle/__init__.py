@@ -94,9 +94,23 @@ def _declare(l: ctypes.CDLL) -> None:
         fn = getattr(l, name)
         fn.argtypes = args
         fn.restype = ctypes.c_int
+    l.slr_set_threads.argtypes = [ctypes.c_int]
+    l.slr_set_threads.restype = None
+    l.slr_get_threads.argtypes = []
+    l.slr_get_threads.restype = ctypes.c_int
     l.slr_lcg_next_u32.restype = ctypes.c_uint32
     l.slr_lcg_fill.restype = None
     l.slr_lcg_below.restype = ctypes.c_size_t
+
+
+def set_threads(n: int) -> None:
+    """Threads for the oracle's independent outputs (1 = the reference's
+    sequential execution; results are bit-identical for any count)."""
+    lib().slr_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().slr_get_threads())
 
 
 def _f32(a) -> np.ndarray:

@@ -65,7 +65,9 @@ class OracleDevice:
         return b
 
     def bind_quantized(self, payload, scales, qformat, group, n, k):
-        self.dequant[payload] = quant.dequantize(self.u32[payload], self.f32[scales], n, k, group, qformat)
+        bits = 4 if quant.QuantFormat(qformat) == quant.QuantFormat.INT4 else 8
+        self.dequant[payload] = oracle.dequantize_groupwise(self.u32[payload].view(np.uint8), self.f32[scales], n, k,
+                                                            group, bits)
 
     # -- dispatch ------------------------------------------------------------
     def _in(self, ref, value):

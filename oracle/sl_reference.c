@@ -19,8 +19,16 @@
  * The quantization helpers at the end have no counterpart in the reference
  * (sl-precision is absent from it); they restate the convention this project
  * adopts and are pinned by closed-form tests, not by reference vectors.
+ *
+ * Threads: the reference is single-threaded, and so is this library by
+ * default (the CPU-baseline timing runs it that way). slr_set_threads(n)
+ * lets the tests spread the independent outputs of matmul, attention,
+ * swiglu and rms_norm_matmul over n OpenMP threads; every output element is
+ * still computed by one thread in the reference's order, so the results are
+ * bit-identical for any n.
  */
 #include <math.h>
+#include <stdlib.h>
 #include <stddef.h>
 #include <stdint.h>
 #include <string.h>
@@ -32,6 +40,12 @@ enum {
     SLR_INVALID_SHAPE = 3,
     SLR_UNSUPPORTED = 4,
 };
+
+static int g_threads = 1;
+
+/* Number of OpenMP threads the parallel loops use (1: sequential). */
+void slr_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int slr_get_threads(void) { return g_threads; }
 
 static const char *const MSG_LENGTH = "kernel received a slice of the wrong length";
 static const char *const MSG_OVERFLOW = "tensor shape product overflows usize";
@@ -96,6 +110,7 @@ int slr_matmul_nt(const float *a, size_t a_len, const float *b, size_t b_len, fl
         const float *ab = a + bi * m * k;
         const float *bb = b + bi * n * k;
         float *ob = out + bi * m * n;
+#pragma omp parallel for collapse(2) schedule(static) num_threads(g_threads) if (g_threads > 1 && m * n > 64)
         for (size_t row = 0; row < m; ++row)
             for (size_t col = 0; col < n; ++col)
                 ob[row * n + col] = dot(ab + row * k, bb + col * k, k);
@@ -117,6 +132,7 @@ int slr_matmul_nn(const float *a, size_t a_len, const float *b, size_t b_len, fl
         const float *ab = a + bi * m * k;
         const float *bb = b + bi * k * n;
         float *ob = out + bi * m * n;
+#pragma omp parallel for collapse(2) schedule(static) num_threads(g_threads) if (g_threads > 1 && m * n > 64)
         for (size_t row = 0; row < m; ++row) {
             for (size_t col = 0; col < n; ++col) {
                 float sum = 0.0f;
@@ -422,6 +438,7 @@ int slr_causal_attention(const float *q, size_t q_len, const float *k_new, size_
     size_t parity_stride = max_seq * time_stride;
     size_t layer_stride = 2 * parity_stride;
     size_t batch_stride = layers * layer_stride;
+#pragma omp parallel for collapse(2) schedule(dynamic) num_threads(g_threads) if (g_threads > 1 && batch * heads > 1)
     for (size_t b = 0; b < batch; ++b)
         for (size_t h = 0; h < heads; ++h) {
             size_t kv_head = h / group;
@@ -473,20 +490,31 @@ int slr_swiglu(const float *x, size_t x_len, const float *w_gate, size_t g_len, 
     SHAPE(ld, hidden, inter);
     EXPECT(d_len, ld);
     EXPECT(out_len, lt);
+    /* The reference runs i outer, j inner; out[r, j] sees the same sequence
+     * of additions (i ascending) with j outer, which lets the threaded
+     * version give each thread whole output elements. */
+    float *weights = (float *)malloc((inter ? inter : 1) * sizeof(float));
+    if (weights == NULL) INVALID("swiglu could not allocate its row buffer");
     for (size_t r = 0; r < rows; ++r) {
         const float *xr = x + r * hidden;
         float *orow = out + r * hidden;
-        for (size_t j = 0; j < hidden; ++j) orow[j] = 0.0f;
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
         for (size_t i = 0; i < inter; ++i) {
             float gate = silu_scalar(dot(xr, w_gate + i * hidden, hidden));
             float up = dot(xr, w_up + i * hidden, hidden);
-            float weight = gate * up;
-            for (size_t j = 0; j < hidden; ++j) {
-                float term = weight * w_down[j * inter + i];
-                orow[j] = orow[j] + term;
+            weights[i] = gate * up;
+        }
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
+        for (size_t j = 0; j < hidden; ++j) {
+            float acc = 0.0f;
+            for (size_t i = 0; i < inter; ++i) {
+                float term = weights[i] * w_down[j * inter + i];
+                acc = acc + term;
             }
+            orow[j] = acc;
         }
     }
+    free(weights);
     return SLR_OK;
 }
 
@@ -514,6 +542,7 @@ int slr_rms_norm_matmul(const float *x, size_t x_len, const float *weight, size_
         }
         float mean_square = ss / (float)hidden;
         float inverse_rms = 1.0f / sqrtf(mean_square + eps);
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)
         for (size_t c = 0; c < out_features; ++c) {
             const float *wr = w + c * hidden;
             float sum = 0.0f;
@@ -584,6 +613,7 @@ int slr_quantize_groupwise(const float *w, size_t n, size_t k, size_t group, int
     size_t groups = k / group;
     size_t row_bytes = bits == 4 ? (k + 1) / 2 : k;
     memset(payload, 0, n * row_bytes);
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1 && n > 1)
     for (size_t r = 0; r < n; ++r) {
         for (size_t g = 0; g < groups; ++g) {
             const float *src = w + r * k + g * group;
@@ -642,6 +672,7 @@ int slr_dequantize_groupwise(const uint8_t *payload, const float *scales, size_t
     }
     size_t groups = k / group;
     size_t row_bytes = bits == 4 ? (k + 1) / 2 : k;
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1 && n > 1)
     for (size_t r = 0; r < n; ++r)
         for (size_t c = 0; c < k; ++c) {
             int q;

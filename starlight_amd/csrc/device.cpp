@@ -98,8 +98,7 @@ struct Device : BufferView {
     // deferred submission
     std::vector<Logged> log;
     uint32_t options = SL_HIP_OPT_FUSION | SL_HIP_OPT_GRAPHS;
-    uint32_t* dyn = nullptr;  // device past_len slots
-    uint32_t dyn_cap = 0;
+    uint32_t* dyn = nullptr;  // device past_len slots, kLogFlushLength of them
     std::vector<uint32_t> dyn_values;
     std::vector<uint64_t> key, prev_key;
     std::vector<GraphEntry> graphs;
@@ -390,13 +389,17 @@ bool mfma_weight(const Device* d, const Logged& c, size_t port) {
 // the fused epilogue writes o then resid + o to each element from the same
 // thread, leaving what the two commands leave) but must not otherwise
 // overlap `o`, and must not overlap the inputs the fused kernel still reads.
+// The residual operand is read early by every block, so it must not overlap
+// `written`, a region the fused kernel writes before its epilogue (the norm
+// output block 0 writes in its prologue).
 int residual_port(const Logged& a, const sl_buffer_ref& o, uint64_t count, const sl_buffer_ref* reads,
-                  size_t n_reads) {
+                  size_t n_reads, const sl_buffer_ref* written = nullptr) {
     if (a.plan.code != SL_OP_ADD || a.plan.len != count) return -1;
     int other = same_ref(a.in[1], o) ? 0 : same_ref(a.in[0], o) ? 1 : -1;
     if (other < 0 || overlaps(a.in[other], o) || (overlaps(a.out, o) && !same_ref(a.out, o)) ||
         (overlaps(a.out, a.in[other]) && !same_ref(a.out, a.in[other])))
         return -1;
+    if (written != nullptr && overlaps(a.in[other], *written)) return -1;
     for (size_t i = 0; i < n_reads; ++i)
         if (overlaps(a.out, reads[i])) return -1;
     return other;
@@ -454,7 +457,7 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
         f.epilogue = kFusedPlain;
         if (cnt == 1 && j + 1 < n) {
             const Logged& a = d->log[j + 1];
-            const int other = residual_port(a, outs[0], rows * w[0].n, reads, n_reads);
+            const int other = residual_port(a, outs[0], rows * w[0].n, reads, n_reads, norm ? &norm->out : nullptr);
             if (other >= 0) {
                 f.epilogue = kFusedResidual;
                 f.resid[0] = fptr(d, a.in[other]);
@@ -630,20 +633,25 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
     }
     const sl_buffer_ref att = at.out;
     const bool att_dead = mh != nullptr && dead_after(d, i + used, att);
-    // the projection chained below reads the mirror, not MergeHeads' output
+    AttentionArgs a{fptr(d, sq.in[0]), fptr(d, sk.in[0]), fptr(d, sv.in[0]), fptr(d, cache),
+                    att_dead ? nullptr : fptr(d, att), B, ap.layers, ap.layer, H, Hkv, S, ap.past_len, D,
+                    ap.max_seq, ap.scale, dyn_of(d, at)};
+    // Workspace: the decode partials, the mirror of the merged heads, then
+    // the staged intermediates.
+    const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
+    const uint64_t mirror_at = (attention_workspace_floats(a) + 63) / 64 * 64;
+    // The output projection is chained (it reads the mirror, not MergeHeads'
+    // output) only when the mirror fits; otherwise it runs on its own and
+    // reads MergeHeads' output, which must then be written.
     const Logged* mm = mh && i + used < n ? &d->log[i + used] : nullptr;
-    const bool chainable = mm && mm->plan.code == SL_OP_MATMUL_NT && same_ref(mm->in[0], mh->out) &&
-                           mfma_weight(d, *mm, 1) && mm->plan.batch * mm->plan.m == B * S && mm->plan.k == H * D;
-    const bool merged_needed =
-        mh != nullptr && !dead_after(d, i + used, mh->out, chainable ? i + used : SIZE_MAX);
+    const bool chain = mm && mm->plan.code == SL_OP_MATMUL_NT && same_ref(mm->in[0], mh->out) &&
+                       mfma_weight(d, *mm, 1) && mm->plan.batch * mm->plan.m == B * S && mm->plan.k == H * D &&
+                       mirror_at + B * S * H * D <= ws.floats;
+    const bool merged_needed = mh != nullptr && !dead_after(d, i + used, mh->out, chain ? i + used : SIZE_MAX);
     // outputs of the merge kernel: no overlap with the cache, or with each other
     if (overlaps(att, cache) || (mh && overlaps(mh->out, cache)) ||
         (mh && !att_dead && merged_needed && overlaps(att, mh->out) && !same_ref(att, mh->out)))
         return 0;
-
-    AttentionArgs a{fptr(d, sq.in[0]), fptr(d, sk.in[0]), fptr(d, sv.in[0]), fptr(d, cache),
-                    att_dead ? nullptr : fptr(d, att), B, ap.layers, ap.layer, H, Hkv, S, ap.past_len, D,
-                    ap.max_seq, ap.scale, dyn_of(d, at)};
     a.positions = uptr(d, rq.in[1]);
     a.theta = rq.plan.theta;
     a.rope_variant = rq.plan.rope_variant;
@@ -672,10 +680,6 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
         }
         a.rope_table = d->rope_tab;
     }
-    // Workspace: the decode partials, the mirror of the merged heads, then
-    // the staged intermediates.
-    const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
-    const uint64_t mirror_at = (attention_workspace_floats(a) + 63) / 64 * 64;
     uint64_t stage_at = mirror_at + (B * S * H * D + 63) / 64 * 64;
     float* stage[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
     float** const inter_ptr[5] = {&a.q_split, &a.k_split, &a.v_split, &a.q_rot, &a.k_rot};
@@ -692,7 +696,6 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
     }
 
     // the output projection (and its residual Add) reading the mirror
-    const bool chain = chainable && mirror_at + B * S * H * D <= ws.floats;
     if (chain) a.mirror = ws.data + mirror_at;
     hipError_t e = launch_attention_fused(a, ws, d->stream);
     if (e == hipErrorNotSupported) return 0;
@@ -864,23 +867,11 @@ uint64_t key_hash(const std::vector<uint64_t>& k) {
 hipError_t submit(Device* d) {
     if (d->log.empty()) return hipSuccess;
     hipError_t e = hipSuccess;
+    // One past_len slot per logged command that reads it; the log never
+    // exceeds kLogFlushLength commands, the array's size (allocated with the
+    // device, so a submission allocates nothing for it).
     uint32_t slots = 0;
     for (Logged& c : d->log) c.dyn_slot = reads_past(c.plan.code) ? static_cast<int32_t>(slots++) : -1;
-    if (slots > d->dyn_cap) {
-        // Graphs hold the old array's address.
-        e = hipStreamSynchronize(d->stream);
-        drop_graphs(d);
-        if (d->dyn) (void)hipFree(d->dyn);
-        d->dyn = nullptr;
-        d->dyn_cap = 0;
-        const uint32_t cap = (slots + 255) / 256 * 256;
-        if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&d->dyn), cap * sizeof(uint32_t));
-        if (e != hipSuccess) {
-            d->log.clear();
-            return e;
-        }
-        d->dyn_cap = cap;
-    }
     d->dyn_values.clear();
     for (const Logged& c : d->log)
         if (c.dyn_slot >= 0) d->dyn_values.push_back(static_cast<uint32_t>(c.plan.past_len));
@@ -995,7 +986,10 @@ sl_status sl_hip_device_create(int ordinal, sl_hip_device** out) {
         delete d;
         return SL_ERR_OUT_OF_MEMORY;
     }
-    if (hipMalloc(reinterpret_cast<void**>(&d->rope_tab), slhip::kRopeTableFloats * 4) != hipSuccess) {
+    if (hipMalloc(reinterpret_cast<void**>(&d->rope_tab), slhip::kRopeTableFloats * 4) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&d->dyn), slhip::kLogFlushLength * sizeof(uint32_t)) != hipSuccess) {
+        (void)hipGetLastError();
+        if (d->rope_tab) (void)hipFree(d->rope_tab);
         (void)hipFree(d->counters);
         (void)hipFree(d->workspace);
         (void)hipStreamDestroy(d->stream);

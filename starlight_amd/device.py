@@ -12,6 +12,7 @@ there is no fallback: if it is missing, loading raises.
 from __future__ import annotations
 
 import ctypes
+import glob
 import os
 import re
 from typing import Optional, Sequence
@@ -128,10 +129,13 @@ class HipStats(ctypes.Structure):
 
 
 def exported_symbols() -> list:
-    """Every `sl_hip_*` function the public header declares."""
-    with open(HEADER_PATH) as f:
-        text = f.read()
-    return sorted(set(re.findall(r"\b(sl_hip_[a-z0-9_]+)\s*\(", text)))
+    """Every `sl_hip_*` / `sl_engine_*` function the public headers
+    (include/*.h) declare."""
+    names = set()
+    for path in sorted(glob.glob(os.path.join(os.path.dirname(HEADER_PATH), "*.h"))):
+        with open(path) as f:
+            names |= set(re.findall(r"\b(sl_(?:hip|engine)_[a-z0-9_]+)\s*\(", f.read()))
+    return sorted(names)
 
 
 def load_library() -> ctypes.CDLL:

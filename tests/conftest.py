@@ -29,6 +29,17 @@ def assert_close(actual, expected, abs_tol=1e-4, rel_tol=1e-5):
     )
 
 
+@pytest.fixture(scope="session", autouse=True)
+def _oracle_threads():
+    """The oracle spreads independent outputs over up to 16 threads in the
+    tests (bit-identical to one thread; tests/test_oracle_threads.py)."""
+    import oracle as o
+
+    o.lib()
+    o.set_threads(min(16, os.cpu_count() or 1))
+    yield
+
+
 @pytest.fixture(scope="session")
 def oracle():
     import oracle as o

@@ -95,7 +95,8 @@ def torch_pack_int4(q):
 
 def upload_synthetic_weights(dev, cfg, seed=0):
     """Generates every weight of `cfg` on the GPU and uploads it through the
-    device contract; returns name -> BufferId."""
+    device contract; returns role -> BufferId (a quantized weight's payload
+    and its `<role>.__scales` Param; the engine's build binds them)."""
     import torch
 
     from starlight_amd.graph import weight_specs
@@ -120,10 +121,8 @@ def upload_synthetic_weights(dev, cfg, seed=0):
             words = torch_pack_int4(q)
         else:
             words = q.contiguous().view(torch.int32).view(-1)
-        pb = dev.upload_new_u32(words.cpu().numpy().view(np.uint32))
-        sb = dev.upload_new_f32(scales.cpu().numpy())
-        dev.bind_quantized(pb, sb, cfg.quant, cfg.group, spec.shape[0], spec.shape[1])
-        bufs[spec.name] = pb
+        bufs[spec.name] = dev.upload_new_u32(words.cpu().numpy().view(np.uint32))
+        bufs[spec.scales] = dev.upload_new_f32(scales.cpu().numpy())
         del q, scales, words
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -502,8 +501,10 @@ def main():
     bufs = upload_synthetic_weights(dev, cfg, seed=0)
     log(f"weights generated and uploaded in {time.perf_counter() - t0:.1f} s")
     B = args.batch
-    pre = engine.compile_program(graph.lower_llama(cfg, B, prompt_len, max_seq), bufs)
-    dec = engine.compile_program(graph.lower_llama(cfg, B, 1, max_seq), bufs)
+    from starlight_amd import device as hipdev
+    caps = graph.DeviceCapabilities.from_c(hipdev.capabilities())
+    pre = engine.compile_program(graph.compile_for(graph.lower_llama(cfg, B, prompt_len, max_seq), caps), bufs)
+    dec = engine.compile_program(graph.compile_for(graph.lower_llama(cfg, B, 1, max_seq), caps), bufs)
     eng = engine.NativeEngine(dev, pre, dec, B, max_seq)
 
     prompt = np.concatenate([synth.prompt(cfg.vocab, prompt_len, b) for b in range(B)])

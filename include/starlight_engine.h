@@ -56,7 +56,10 @@ typedef struct sl_command_buffer {
 } sl_command_buffer;
 
 /* sl_core::CompiledProgram (ARCH-0007 §3.2). A negative optional id means
- * "absent". Weights are (ValueId, BufferId) pairs uploaded beforehand. */
+ * "absent". Weights are (ValueId, BufferId) pairs uploaded beforehand; they
+ * include the scale Param of every group-quantized Param (a separate f32
+ * [n, k / group] Param, "<role>.__scales", ARCH-0006:147), paired with it in
+ * quant_params[i] -> quant_scales[i] (ValueIds). */
 typedef struct sl_compiled_program {
     sl_command_buffer ir;
     const uint32_t *weight_values;
@@ -67,6 +70,9 @@ typedef struct sl_compiled_program {
     uint32_t seq_len;
     int32_t past_len;
     uint32_t logits;
+    const uint32_t *quant_params;
+    const uint32_t *quant_scales;
+    size_t n_quant;
 } sl_compiled_program;
 
 typedef enum sl_step_mode { SL_STEP_PREFILL = 0, SL_STEP_DECODE = 1 } sl_step_mode;
@@ -74,7 +80,10 @@ typedef enum sl_step_mode { SL_STEP_PREFILL = 0, SL_STEP_DECODE = 1 } sl_step_mo
 typedef struct sl_engine sl_engine;
 
 /* Engine::build (ARCH-0007 §3.2 build responsibilities 1-4). The two
- * programs share State values with the same ValueId (the KV cache). */
+ * programs share State values with the same ValueId (the KV cache). Every
+ * group-quantized Param is bound to its scale Param's buffer here
+ * (sl_hip_bind_quantized); a quantized Param without a bound scale Param of
+ * shape [n, k / group] fails the build with Execution. */
 sl_status sl_engine_build(sl_hip_device *device, const sl_compiled_program *prefill,
                           const sl_compiled_program *decode, uint32_t max_batch, uint32_t max_context,
                           sl_engine **out);

@@ -160,7 +160,9 @@ typedef struct sl_buffer_ref {
 typedef struct sl_hip_device sl_hip_device;
 
 /* CpuDevice::new() (device.rs:41-45). Opens HIP device `ordinal`, creates the
- * device's stream and its fixed workspace. */
+ * device's stream and its fixed workspace (512 MiB, or the byte count in the
+ * environment variable SL_HIP_WORKSPACE_BYTES, at least 64 KiB; fused
+ * launches that do not fit a smaller workspace run unfused). */
 sl_status sl_hip_device_create(int ordinal, sl_hip_device **out);
 void sl_hip_device_destroy(sl_hip_device *device);
 

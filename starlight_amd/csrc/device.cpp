@@ -38,6 +38,7 @@
 #include <vector>
 
 #include "kernels/kernels.h"
+#include "internal.h"
 #include "plan.h"
 #include "starlight_hip.h"
 
@@ -279,12 +280,11 @@ WeightRef weight_ref(Device* d, const sl_buffer_ref& r, const QuantOperand& q) {
     return w;
 }
 
-// Enqueues the kernels of one validated command; `dyn`, when set, is the
-// device word its kernels read past_len from.
+// Enqueues the kernels of one validated command with `ws` as their scratch
+// memory; `dyn`, when set, is the device word its kernels read past_len from.
 hipError_t launch(Device* d, const Plan& p, const sl_buffer_ref* in, const sl_buffer_ref* out,
-                  const uint32_t* dyn) {
+                  const uint32_t* dyn, const Workspace& ws) {
     hipStream_t s = d->stream;
-    const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
     switch (p.code) {
         case SL_OP_MATMUL_NT:
         case SL_OP_MATMUL_NN: {
@@ -343,19 +343,19 @@ hipError_t launch(Device* d, const Plan& p, const sl_buffer_ref* in, const sl_bu
     }
 }
 
-// Limits of the launch paths that validation does not know about; checked
-// before anything is enqueued so a rejected call still changes nothing.
-bool device_limits(Device* d, const Plan& p, Error* err) {
-    (void)d;
+// Limits of the launch paths that validation does not know about, for a
+// scratch area of `ws_floats`; checked before anything is enqueued so a
+// rejected call still changes nothing.
+bool device_limits(const Plan& p, uint64_t ws_floats, Error* err) {
     if (p.code == SL_OP_CAUSAL_ATTENTION && p.head_dim > 256) {
         *err = Error::unimplemented("head_dim above 256 is not supported by HipDevice");
         return false;
     }
-    if (p.code == SL_OP_SWIGLU && 2 * p.inter > d->workspace_floats / 2) {
+    if (p.code == SL_OP_SWIGLU && 2 * p.inter > ws_floats / 2) {
         *err = Error::unimplemented("swiglu inter size exceeds the device workspace");
         return false;
     }
-    if (p.code == SL_OP_RMS_NORM_MATMUL && p.hidden > d->workspace_floats / 2) {
+    if (p.code == SL_OP_RMS_NORM_MATMUL && p.hidden > ws_floats / 2) {
         *err = Error::unimplemented("rms_norm_matmul hidden size exceeds the device workspace");
         return false;
     }
@@ -384,21 +384,17 @@ bool mfma_weight(const Device* d, const Logged& c, size_t port) {
 }
 
 // An Add right after a command that wrote `o` (rows * n values), adding it to
-// another operand: returns the port of that other operand, or -1. The add's
-// output may be `o` itself (the memory plan reuses a dead value's region;
-// the fused epilogue writes o then resid + o to each element from the same
-// thread, leaving what the two commands leave) but must not otherwise
-// overlap `o`, and must not overlap the inputs the fused kernel still reads.
-// The residual operand is read early by every block, so it must not overlap
+// another operand: returns the port of that other operand, or -1. The Add's
+// output overlaps neither of its inputs (dispatch validation rejects that)
+// and must not overlap the inputs the fused kernel still reads. The residual
+// operand is read early by every block, so it must not overlap `o` or
 // `written`, a region the fused kernel writes before its epilogue (the norm
 // output block 0 writes in its prologue).
 int residual_port(const Logged& a, const sl_buffer_ref& o, uint64_t count, const sl_buffer_ref* reads,
                   size_t n_reads, const sl_buffer_ref* written = nullptr) {
     if (a.plan.code != SL_OP_ADD || a.plan.len != count) return -1;
     int other = same_ref(a.in[1], o) ? 0 : same_ref(a.in[0], o) ? 1 : -1;
-    if (other < 0 || overlaps(a.in[other], o) || (overlaps(a.out, o) && !same_ref(a.out, o)) ||
-        (overlaps(a.out, a.in[other]) && !same_ref(a.out, a.in[other])))
-        return -1;
+    if (other < 0 || overlaps(a.in[other], o) || overlaps(a.out, o) || overlaps(a.out, a.in[other])) return -1;
     if (written != nullptr && overlaps(a.in[other], *written)) return -1;
     for (size_t i = 0; i < n_reads; ++i)
         if (overlaps(a.out, reads[i])) return -1;
@@ -800,7 +796,8 @@ hipError_t run_log(Device* d) {
         if (e != hipSuccess) return e;
         if (used == 0) {
             const Logged& c = d->log[i];
-            e = launch(d, c.plan, c.in, &c.out, dyn_of(d, c));
+            e = launch(d, c.plan, c.in, &c.out, dyn_of(d, c),
+                       Workspace{d->workspace, d->workspace_floats, d->counters, kCounterWords});
             if (e != hipSuccess) return e;
             used = 1;
         }
@@ -939,6 +936,20 @@ hipError_t submit(Device* d) {
     return e;
 }
 
+// The device workspace size: SL_HIP_WORKSPACE_BYTES when set (at least
+// 64 KiB, rounded up to 256 bytes), else 512 MiB. Fused paths that do not
+// fit a smaller workspace fall back to their unfused kernels.
+uint64_t workspace_bytes_setting() {
+    const char* v = std::getenv("SL_HIP_WORKSPACE_BYTES");
+    if (v == nullptr || *v == 0) return kWorkspaceBytes;
+    char* end = nullptr;
+    const unsigned long long n = std::strtoull(v, &end, 10);
+    if (end == v || *end != 0) return kWorkspaceBytes;
+    const uint64_t lo = 64ull << 10;
+    const uint64_t b = n < lo ? lo : n;
+    return (b + 255) / 256 * 256;
+}
+
 sl_status flush(Device* d) {
     const hipError_t e = submit(d);
     if (e != hipSuccess) return d->hip_fail(e);
@@ -973,12 +984,13 @@ sl_status sl_hip_device_create(int ordinal, sl_hip_device** out) {
         delete d;
         return SL_ERR_EXECUTION;
     }
-    if (hipMalloc(reinterpret_cast<void**>(&d->workspace), slhip::kWorkspaceBytes) != hipSuccess) {
+    const uint64_t ws_bytes = slhip::workspace_bytes_setting();
+    if (hipMalloc(reinterpret_cast<void**>(&d->workspace), ws_bytes) != hipSuccess) {
         (void)hipStreamDestroy(d->stream);
         delete d;
         return SL_ERR_OUT_OF_MEMORY;
     }
-    d->workspace_floats = slhip::kWorkspaceBytes / 4;
+    d->workspace_floats = ws_bytes / 4;
     if (hipMalloc(reinterpret_cast<void**>(&d->counters), slhip::kCounterWords * 4) != hipSuccess ||
         hipMemset(d->counters, 0, slhip::kCounterWords * 4) != hipSuccess) {
         (void)hipFree(d->workspace);
@@ -1052,7 +1064,7 @@ sl_status sl_hip_dispatch(sl_hip_device* d, const sl_op* op, const sl_buffer_ref
     if (!slhip::validate_dispatch(*d, *op, inputs, input_values, n_inputs, outputs, output_values, n_outputs,
                                   scalars, n_scalars, &plan, &err))
         return d->fail(err);
-    if (!slhip::device_limits(d, plan, &err)) return d->fail(err);
+    if (!slhip::device_limits(plan, d->workspace_floats, &err)) return d->fail(err);
     if (plan.code == SL_OP_GATHER && !slhip::gather_ids_in_range(d, inputs[1], plan.vocab, &err))
         return d->fail(err);
     slhip::Logged c;
@@ -1110,6 +1122,12 @@ sl_status sl_hip_bind_quantized(sl_hip_device* d, uint32_t payload, uint32_t sca
         return d->fail(Error::execution("quantized payload size does not match [n, k]"));
     if (d->buffers[scales].desc.elements != static_cast<uint64_t>(n) * (k / group_size))
         return d->fail(Error::execution("quantized scale count does not match [n, k / group_size]"));
+    // The same binding again (Engine build binds every quantized Param of
+    // each program it builds): nothing changes. The tile copy is already
+    // current, since re-uploads of the payload or scales refresh it.
+    if (pb.tiles != nullptr && pb.desc.quantized && pb.scales == scales && pb.desc.qformat == qformat &&
+        pb.desc.group_size == group_size && pb.desc.qn == n && pb.desc.qk == k)
+        return SL_OK;
     // Logged commands read the old binding; the graphs hold its tile address.
     if (slhip::flush(d) != SL_OK) return d->last.status;
     slhip::drop_graphs(d);
@@ -1150,6 +1168,14 @@ sl_status sl_hip_bind_quantized(sl_hip_device* d, uint32_t payload, uint32_t sca
 }
 
 void* sl_hip_stream(const sl_hip_device* d) { return d->stream; }
+
+}  // extern "C"
+
+sl_status slhip_fail_execution(sl_hip_device* d, const char* message) {
+    return d->fail(Error::execution(message));
+}
+
+extern "C" {
 
 void sl_hip_capabilities(sl_capabilities* out) {
     out->backend = "hip-gfx950";

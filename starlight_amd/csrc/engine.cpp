@@ -9,6 +9,7 @@
 #include <new>
 #include <vector>
 
+#include "internal.h"
 #include "starlight_engine.h"
 #include "starlight_hip.h"
 
@@ -80,9 +81,46 @@ struct BuildError {
     sl_status status;
 };
 
+// The BufferId bound to ValueId `vid` in the program's weight table.
+bool weight_buffer(const sl_compiled_program* p, uint32_t vid, uint32_t* buf) {
+    for (size_t i = 0; i < p->n_weights; ++i)
+        if (p->weight_values[i] == vid) {
+            *buf = p->weight_buffers[i];
+            return true;
+        }
+    return false;
+}
+
+// Binds every group-quantized Param of `p` to its scale Param: both must be
+// in the weight table, and the scale Param must be f32 [n, k / group].
+sl_status bind_quantized_params(sl_engine* e, const sl_compiled_program* p) {
+    const sl_command_buffer& ir = p->ir;
+    for (size_t vid = 0; vid < ir.n_values; ++vid) {
+        const sl_value& v = ir.values[vid];
+        if (v.encoding != SL_ENCODING_GROUPWISE_QUANTIZED) continue;
+        uint32_t sid = UINT32_MAX, pbuf = 0, sbuf = 0;
+        for (size_t i = 0; i < p->n_quant; ++i)
+            if (p->quant_params[i] == vid) sid = p->quant_scales[i];
+        if (v.role != SL_ROLE_PARAM || v.rank != 2 || v.group_size == 0 || v.dims[1] % v.group_size != 0 ||
+            sid >= ir.n_values || !weight_buffer(p, static_cast<uint32_t>(vid), &pbuf) ||
+            !weight_buffer(p, sid, &sbuf))
+            return slhip_fail_execution(e->device, "quantized Param has no bound scale Param");
+        const sl_value& sv = ir.values[sid];
+        if (sv.dtype != SL_DTYPE_F32 || sv.role != SL_ROLE_PARAM || sv.rank != 2 || sv.dims[0] != v.dims[0] ||
+            sv.dims[1] != v.dims[1] / v.group_size)
+            return slhip_fail_execution(e->device, "scale Param shape is not [n, k / group_size]");
+        const sl_status st = sl_hip_bind_quantized(e->device, pbuf, sbuf, v.qformat, v.group_size, v.dims[0],
+                                                   v.dims[1]);
+        if (st != SL_OK) return st;
+    }
+    return SL_OK;
+}
+
 sl_status resolve_program(sl_engine* e, const sl_compiled_program* p, Program* out) {
     const sl_command_buffer& ir = p->ir;
     if (ir.ir_version != SL_IR_VERSION) return SL_ERR_EXECUTION;
+    const sl_status bq = bind_quantized_params(e, p);
+    if (bq != SL_OK) return bq;
     const size_t nv = ir.n_values;
     // ValueId -> BufferRef for every non-scalar value the commands touch.
     std::vector<sl_buffer_ref> refs(nv);

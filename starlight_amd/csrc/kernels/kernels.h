@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "starlight_hip.h"
+
 namespace slhip {
 
 // Device-owned scratch passed to kernels that need it: `data` for partial

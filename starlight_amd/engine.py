@@ -29,25 +29,53 @@ class CompiledProgram:
 
 def upload_weights(device, cfg: LlamaConfig, tensors: Dict[str, np.ndarray]) -> Dict[str, int]:
     """Uploads every weight of `cfg` (float32 arrays by name) and returns
-    name -> BufferId. Linear weights marked quantized are quantized with the
-    group-wise convention, uploaded as u32 payload + f32 scales and bound."""
+    role -> BufferId. Linear weights marked quantized are quantized with the
+    group-wise convention and uploaded as two Params: the u32 payload under
+    the weight's role and the f32 scales under `<role>.__scales`
+    (ARCH-0006:147); Engine build binds the pair."""
     buffers: Dict[str, int] = {}
     for spec in weight_specs(cfg):
         w = np.ascontiguousarray(tensors[spec.name], dtype=np.float32)
         assert w.shape == spec.shape, (spec.name, w.shape, spec.shape)
         if spec.quantized:
             words, scales = quant.quantize(w, cfg.group, cfg.quant)
-            pb = device.upload_new_u32(words)
-            sb = device.upload_new_f32(scales)
-            device.bind_quantized(pb, sb, cfg.quant, cfg.group, spec.shape[0], spec.shape[1])
-            buffers[spec.name] = pb
+            buffers[spec.name] = device.upload_new_u32(words)
+            buffers[spec.scales] = device.upload_new_f32(scales)
         else:
             buffers[spec.name] = device.upload_new_f32(w)
     return buffers
 
 
 def compile_program(lowered: Lowered, weight_buffers: Dict[str, int]) -> CompiledProgram:
-    return CompiledProgram(lowered, {lowered.weights[name]: buf for name, buf in weight_buffers.items()})
+    """Binds a compiled program's Params to uploaded buffers by role."""
+    return CompiledProgram(lowered, {lowered.weights[name]: buf for name, buf in weight_buffers.items()
+                                     if name in lowered.weights})
+
+
+class BuildError(Exception):
+    """A program the engine cannot build on its device (Engine::build)."""
+
+
+def quantized_bindings(prog: CompiledProgram):
+    """(payload BufferId, scales BufferId, qformat, group, n, k) for every
+    group-quantized Param of the program; raises BuildError when a quantized
+    Param or its scale Param has no buffer, or the scale Param's shape is
+    not [n, k / group]."""
+    cb = prog.lowered.ir
+    out = []
+    for vid, v in enumerate(cb.values):
+        if v.encoding != ir.Encoding.GROUPWISE_QUANTIZED:
+            continue
+        if v.role != ir.ValueRole.PARAM or vid not in prog.weights:
+            raise BuildError(f"quantized value {vid} is not a bound Param")
+        sid = prog.lowered.quant_scales.get(vid)
+        if sid is None or sid not in prog.weights:
+            raise BuildError(f"quantized Param {vid} has no bound scale Param")
+        n, k = v.shape
+        if v.group_size <= 0 or k % v.group_size or cb.values[sid].shape != (n, k // v.group_size):
+            raise BuildError(f"scale Param {sid} does not have shape [n, k / group] for Param {vid}")
+        out.append((prog.weights[vid], prog.weights[sid], v.qformat, v.group_size, n, k))
+    return out
 
 
 # ------------------------------------------------------------ native ------
@@ -75,7 +103,9 @@ class CCompiledProgram(ctypes.Structure):
     _fields_ = [("ir", CCommandBuffer), ("weight_values", ctypes.POINTER(ctypes.c_uint32)),
                 ("weight_buffers", ctypes.POINTER(ctypes.c_uint32)), ("n_weights", ctypes.c_size_t),
                 ("token_ids", ctypes.c_uint32), ("positions", ctypes.c_int32), ("seq_len", ctypes.c_uint32),
-                ("past_len", ctypes.c_int32), ("logits", ctypes.c_uint32)]
+                ("past_len", ctypes.c_int32), ("logits", ctypes.c_uint32),
+                ("quant_params", ctypes.POINTER(ctypes.c_uint32)), ("quant_scales", ctypes.POINTER(ctypes.c_uint32)),
+                ("n_quant", ctypes.c_size_t)]
 
 
 def _to_c_program(prog: CompiledProgram):
@@ -111,7 +141,10 @@ def _to_c_program(prog: CompiledProgram):
     lw = prog.lowered
     c.token_ids, c.positions, c.seq_len, c.past_len, c.logits = lw.token_ids, lw.positions, lw.seq_len, \
         lw.past_len, lw.logits
-    return c, [values, cmds, slots, wv, wb]
+    qp = (ctypes.c_uint32 * max(len(lw.quant_scales), 1))(*lw.quant_scales.keys())
+    qs = (ctypes.c_uint32 * max(len(lw.quant_scales), 1))(*lw.quant_scales.values())
+    c.quant_params, c.quant_scales, c.n_quant = qp, qs, len(lw.quant_scales)
+    return c, [values, cmds, slots, wv, wb, qp, qs]
 
 
 def _declare_engine(lib):
@@ -227,6 +260,13 @@ class Engine:
     def __init__(self, device, prefill: CompiledProgram, decode: CompiledProgram, max_batch: int, max_context: int):
         self.device = device
         self.max_context = max_context
+        # Quantized Params: each payload bound to its scale Param, once.
+        bound = {}
+        for prog in (prefill, decode):
+            for b in quantized_bindings(prog):
+                if bound.get(b[0]) != b:
+                    device.bind_quantized(*b)
+                    bound[b[0]] = b
         scratch = max(prefill.lowered.ir.plan.scratchpad_bytes, decode.lowered.ir.plan.scratchpad_bytes)
         self.scratch = device.allocate_f32((scratch + 3) // 4, 256) if scratch else None
         self.states: Dict[int, int] = {}

@@ -13,17 +13,18 @@ parity unpinned against sl-precision.
   <name>           INT4: U8 [n, ceil(k / 2)], two's-complement nibbles,
                    element k of a row in byte k // 2, even k in the low nibble;
                    INT8: I8 [n, k]; row-major
-  <name>.scale     F32 [n, k / group_size]
+  <name>.__scales  F32 [n, k / group_size] (the scale Param's role,
+                   ARCH-0006:147)
   any other tensor F32, stored as given
   metadata["starlight.quantization"] = JSON
       {"version": 1,
        "tensors": {"<name>": {"format": "int4" | "int8", "group_size": G,
-                              "shape": [n, k], "scale": "<name>.scale"}}}
+                              "shape": [n, k], "scale": "<name>.__scales"}}}
 
-On upload, a quantized tensor becomes the u32 payload words the device
-takes (the bytes, padded to a multiple of 4, little-endian) plus its f32
-scales, bound with `bind_quantized`; the device builds its private tile
-layout from them.
+On upload, a quantized tensor becomes two Params: the u32 payload words the
+device takes (the bytes, padded to a multiple of 4, little-endian) under the
+weight's role and its f32 scales under `<role>.__scales`; the engine's build
+binds the pair, and the device builds its private tile layout from them.
 """
 from __future__ import annotations
 
@@ -34,7 +35,7 @@ from typing import Dict, Mapping, Tuple
 import numpy as np
 
 from . import quant
-from .graph import LlamaConfig, weight_specs
+from .graph import SCALES_SUFFIX, LlamaConfig, weight_specs
 from .ir import QuantFormat
 
 METADATA_KEY = "starlight.quantization"
@@ -89,7 +90,7 @@ def save(path: str, dense: Mapping[str, np.ndarray], quantized: Mapping[str, Qua
     for name, a in dense.items():
         tensors[name] = np.ascontiguousarray(a, dtype=np.float32)
     for name, q in quantized.items():
-        scale_name = name + ".scale"
+        scale_name = name + SCALES_SUFFIX
         if name in tensors or scale_name in tensors:
             raise ValueError(f"tensor name {name!r} is used twice")
         tensors[name] = np.ascontiguousarray(q.payload)
@@ -123,7 +124,7 @@ def load(path: str) -> Tuple[Dict[str, np.ndarray], Dict[str, QuantTensor]]:
                 raise ValueError(f"{name}: unknown format {e.get('format')!r}")
             n, k = (int(v) for v in e["shape"])
             group = int(e["group_size"])
-            scale_name = e.get("scale", name + ".scale")
+            scale_name = e.get("scale", name + SCALES_SUFFIX)
             if name not in names or scale_name not in names:
                 raise ValueError(f"{name}: payload or scale tensor missing")
             if group <= 0 or k % group:
@@ -164,9 +165,10 @@ def quantize_model(cfg: LlamaConfig, weights: Mapping[str, np.ndarray]
 
 def upload(device, cfg: LlamaConfig, dense: Mapping[str, np.ndarray],
            quantized: Mapping[str, QuantTensor]) -> Dict[str, int]:
-    """Uploads a loaded checkpoint for `cfg` and returns name -> BufferId, as
-    engine.upload_weights does for f32 weights: every quantized weight of
-    cfg must be present with cfg's format, group and shape."""
+    """Uploads a loaded checkpoint for `cfg` and returns role -> BufferId
+    (scale Params under `<role>.__scales`), as engine.upload_weights does for
+    f32 weights: every quantized weight of cfg must be present with cfg's
+    format, group and shape."""
     buffers: Dict[str, int] = {}
     for spec in weight_specs(cfg):
         if spec.quantized:
@@ -176,10 +178,8 @@ def upload(device, cfg: LlamaConfig, dense: Mapping[str, np.ndarray],
             if q.fmt != cfg.quant or q.group != cfg.group or (q.n, q.k) != tuple(spec.shape):
                 raise ValueError(f"{spec.name}: {_FORMAT_NAMES[q.fmt]} g{q.group} [{q.n}, {q.k}] does not match "
                                  f"the model ({_FORMAT_NAMES[cfg.quant]} g{cfg.group} {list(spec.shape)})")
-            pb = device.upload_new_u32(q.words())
-            sb = device.upload_new_f32(q.scales)
-            device.bind_quantized(pb, sb, q.fmt, q.group, q.n, q.k)
-            buffers[spec.name] = pb
+            buffers[spec.name] = device.upload_new_u32(q.words())
+            buffers[spec.scales] = device.upload_new_f32(q.scales)
         else:
             a = dense.get(spec.name)
             if a is None or tuple(a.shape) != tuple(spec.shape):

@@ -18,12 +18,14 @@ CommandBuffer on both devices.
 """
 from __future__ import annotations
 
+import dataclasses
+import enum
 import math
 from dataclasses import dataclass, field
-from typing import Dict, List, Optional, Tuple
+from typing import Dict, FrozenSet, List, Optional, Tuple
 
-from .ir import (IR_VERSION, Command, CommandBuffer, DType, Effect, KvCacheDecl, MemoryPlan, Op, QuantFormat,
-                 RopeVariant, Slot, Value, ValueRole)
+from .ir import (IR_VERSION, Command, CommandBuffer, DType, Effect, KvCacheDecl, MemoryPlan, Op, OpCode,
+                 QuantFormat, RopeVariant, Slot, Value, ValueRole)
 
 PLAN_ALIGN = 256
 
@@ -61,6 +63,12 @@ class WeightSpec:
     shape: Tuple[int, ...]
     quantized: bool  # stored group-quantized (payload + scales)
     kind: str        # "embed" | "norm" | "linear"
+    # role of the separate f32 scale Param [n, k / group] of a quantized
+    # weight (ARCH-0006:147: "<role>.__scales", not carried in the encoding)
+    scales: Optional[str] = None
+
+
+SCALES_SUFFIX = ".__scales"
 
 
 def weight_specs(cfg: LlamaConfig) -> List[WeightSpec]:
@@ -83,6 +91,9 @@ def weight_specs(cfg: LlamaConfig) -> List[WeightSpec]:
         ]
     specs += [WeightSpec("final_norm", (H,), False, "norm"),
               WeightSpec("lm_head", (cfg.vocab, H), q and cfg.quant_lm_head, "linear")]
+    for spec in specs:
+        if spec.quantized:
+            spec.scales = spec.name + SCALES_SUFFIX
     return specs
 
 
@@ -92,13 +103,15 @@ class Lowered:
     CompiledProgram metadata of ARCH-0007 §3.2)."""
 
     ir: CommandBuffer
-    weights: Dict[str, int]        # weight name -> ValueId
+    weights: Dict[str, int]        # weight role (scale Params included) -> ValueId
     token_ids: int
     positions: int
     seq_len: int
     past_len: int
     logits: int
     kv_cache: int
+    # quantized Param ValueId -> ValueId of its scale Param
+    quant_scales: Dict[int, int] = field(default_factory=dict)
 
 
 class _Builder:
@@ -129,12 +142,15 @@ def lower_llama(cfg: LlamaConfig, batch: int, seq: int, max_seq: int) -> Lowered
     kv = b.value(Value.f32([batch, cfg.layers, 2, max_seq, Hkv, D], ValueRole.STATE))
 
     weights: Dict[str, int] = {}
+    quant_scales: Dict[int, int] = {}
     for spec in weight_specs(cfg):
         if spec.quantized:
-            v = Value.quantized(spec.shape, cfg.quant, cfg.group)
+            weights[spec.name] = b.value(Value.quantized(spec.shape, cfg.quant, cfg.group))
+            n, k = spec.shape
+            weights[spec.scales] = b.value(Value.f32([n, k // cfg.group], ValueRole.PARAM))
+            quant_scales[weights[spec.name]] = weights[spec.scales]
         else:
-            v = Value.f32(spec.shape, ValueRole.PARAM)
-        weights[spec.name] = b.value(v)
+            weights[spec.name] = b.value(Value.f32(spec.shape, ValueRole.PARAM))
 
     h = b.temp([batch, seq, H])
     b.cmd(Op.gather(), [weights["embed"], token_ids], [h])
@@ -179,7 +195,7 @@ def lower_llama(cfg: LlamaConfig, batch: int, seq: int, max_seq: int) -> Lowered
     plan = plan_memory(b.values, b.commands)
     ir = CommandBuffer(IR_VERSION, b.values, b.commands, plan, [token_ids, positions], [logits],
                        [KvCacheDecl(kv, batch, cfg.layers, Hkv, D, max_seq)])
-    return Lowered(ir, weights, token_ids, positions, seq_len, past_len, logits, kv)
+    return Lowered(ir, weights, token_ids, positions, seq_len, past_len, logits, kv, quant_scales)
 
 
 def plan_memory(values: List[Value], commands: List[Command], align: int = PLAN_ALIGN) -> MemoryPlan:
@@ -279,3 +295,158 @@ def lower_fixture(seq: int) -> Lowered:
     ir = CommandBuffer(IR_VERSION, b.values, b.commands, plan, [token_ids], [logits], [])
     # The fixture has no RoPE or KV cache: positions/past_len are absent (-1).
     return Lowered(ir, {"embed": embed, "norm": norm, "lm_head": lm_head}, token_ids, -1, seq_len, -1, logits, -1)
+
+
+# ------------------------------------------------- capability negotiation --
+#
+# The capability step of sl-graph's compile(program, shape_spec, caps)
+# (ARCH-0004 §8, §10 step 3, §11 CompileError; §5.3 decomposition rules):
+#  * a composite the device does not declare is decomposed when a rule
+#    exists (SwiGlu, RmsNormMatMul), else UnsupportedOp { node, op };
+#  * every remaining op must be a core op of the device (UnsupportedOp);
+#  * every value's dtype must be in the device's set (UnsupportedDType);
+#  * a violated shape constraint is CapabilityMismatch { constraint, limit,
+#    actual };
+#  * ir_version must equal the compiler's IR_VERSION (VersionMismatch);
+#  * the plan is made after decomposition, with offsets aligned to
+#    max(64, min_buffer_align) (ARCH-0004 §7), and must fit
+#    max_scratchpad_bytes (PlanOverflow).
+
+COMPOSITES = (OpCode.CAUSAL_ATTENTION, OpCode.SWIGLU, OpCode.RMS_NORM_MATMUL)
+
+
+class ConstraintKind(enum.Enum):
+    HEAD_DIM_MULTIPLE_OF = "head_dim_multiple_of"
+    MATMUL_K_MULTIPLE_OF = "matmul_k_multiple_of"
+    MAX_HEADS = "max_heads"
+
+
+@dataclass(frozen=True)
+class ShapeConstraints:
+    head_dim_multiple_of: int = 1
+    matmul_k_multiple_of: int = 1
+    max_heads: int = 0xFFFFFFFF
+
+
+@dataclass(frozen=True)
+class DeviceCapabilities:
+    """sl_ir::DeviceCapabilities (ARCH-0004 §8); op and dtype sets as frozensets."""
+
+    backend: str
+    ir_version: int
+    core_ops: FrozenSet[OpCode]
+    composite_ops: FrozenSet[OpCode]
+    dtypes: FrozenSet[DType]
+    min_buffer_align: int
+    max_scratchpad_bytes: int
+    max_value_bytes: int
+    constraints: ShapeConstraints = ShapeConstraints()
+
+    @staticmethod
+    def from_c(c: dict) -> "DeviceCapabilities":
+        """From the sl_capabilities struct a backend reports (bitsets over
+        sl_opcode / sl_dtype), e.g. starlight_amd.device.capabilities()."""
+        ops = lambda mask: frozenset(o for o in OpCode if mask >> int(o) & 1)  # noqa: E731
+        return DeviceCapabilities(
+            c["backend"], c["ir_version"], ops(c["core_ops"]), ops(c["composite_ops"]),
+            frozenset(d for d in DType if c["dtypes"] >> int(d) & 1), c["min_buffer_align"],
+            c["max_scratchpad_bytes"], c["max_value_bytes"],
+            ShapeConstraints(c["head_dim_multiple_of"], c["matmul_k_multiple_of"], c["max_heads"]))
+
+    def replace(self, **kw) -> "DeviceCapabilities":
+        return dataclasses.replace(self, **kw)
+
+
+class CompileError(Exception):
+    """sl_graph::CompileError (ARCH-0004 §11): `kind` is the variant name,
+    `fields` its payload."""
+
+    def __init__(self, kind: str, **fields):
+        self.kind = kind
+        self.fields = fields
+        super().__init__(f"{kind} {fields}")
+
+    def __eq__(self, other):
+        return isinstance(other, CompileError) and (self.kind, self.fields) == (other.kind, other.fields)
+
+    __hash__ = Exception.__hash__
+
+
+def _decompose(b: _Builder, c: Command, values: List[Value]) -> Optional[List[Command]]:
+    """The §5.3 rules, or None when the composite has none. Each keeps the
+    reference's arithmetic order, so results are bit-identical to the
+    composite's (swiglu.rs:40-84: silu(dot(x, Wg_i)) * dot(x, Wu_i), then
+    sum over i ascending of (g u)_i Wd[j, i]; fused.rs:41-90: ((x inv) w_i)
+    W[c, i] summed left to right)."""
+    if c.op.code == OpCode.SWIGLU:
+        x, wg, wu, wd = c.inputs
+        lead = values[x].shape[:-1]
+        inter = values[wg].shape[0]
+        g, u, sg, h = (b.temp(list(lead) + [inter]) for _ in range(4))
+        return [Command(Op.matmul_nt(), [x, wg], [g]), Command(Op.matmul_nt(), [x, wu], [u]),
+                Command(Op.silu(), [g], [sg]), Command(Op.mul(), [sg, u], [h]),
+                Command(Op.matmul_nt(), [h, wd], c.outputs)]
+    if c.op.code == OpCode.RMS_NORM_MATMUL:
+        x, w, mat = c.inputs
+        normed = b.temp(values[x].shape)
+        return [Command(Op.rms_norm(c.op.eps), [x, w], [normed]), Command(Op.matmul_nt(), [normed, mat], c.outputs)]
+    return None
+
+
+def _check_constraints(node: int, c: Command, values: List[Value], k: ShapeConstraints) -> None:
+    def mismatch(kind, limit, actual):
+        raise CompileError("CapabilityMismatch", constraint=kind, limit=limit, actual=actual)
+
+    code = c.op.code
+    head_dim = None
+    if code in (OpCode.SPLIT_HEADS, OpCode.MERGE_HEADS, OpCode.CAUSAL_ATTENTION):
+        head_dim = c.op.head_dim
+    elif code == OpCode.ROPE:
+        head_dim = values[c.inputs[0]].shape[-1]
+    if head_dim is not None and head_dim % max(1, k.head_dim_multiple_of):
+        mismatch(ConstraintKind.HEAD_DIM_MULTIPLE_OF, k.head_dim_multiple_of, head_dim)
+    if code in (OpCode.SPLIT_HEADS, OpCode.MERGE_HEADS, OpCode.CAUSAL_ATTENTION) and c.op.heads > k.max_heads:
+        mismatch(ConstraintKind.MAX_HEADS, k.max_heads, c.op.heads)
+    if code in (OpCode.MATMUL_NT, OpCode.MATMUL_NN, OpCode.RMS_NORM_MATMUL):
+        kk = values[c.inputs[0]].shape[-1]
+        if kk % max(1, k.matmul_k_multiple_of):
+            mismatch(ConstraintKind.MATMUL_K_MULTIPLE_OF, k.matmul_k_multiple_of, kk)
+
+
+def compile_for(lowered: Lowered, caps: DeviceCapabilities) -> Lowered:
+    """The capability, plan and emit steps for one device: returns a Lowered
+    whose CommandBuffer the device can run, or raises CompileError."""
+    cb = lowered.ir
+    if caps.ir_version != cb.ir_version:
+        raise CompileError("VersionMismatch", device=caps.ir_version, compiler=cb.ir_version)
+    b = _Builder()
+    b.values = list(cb.values)
+    for node, c in enumerate(cb.commands):
+        emitted = [c]
+        if c.op.code in COMPOSITES and c.op.code not in caps.composite_ops:
+            emitted = _decompose(b, c, b.values)
+            if emitted is None:
+                raise CompileError("UnsupportedOp", node=node, op=c.op.code)
+        for e in emitted:
+            if e.op.code not in caps.core_ops and e.op.code not in caps.composite_ops:
+                raise CompileError("UnsupportedOp", node=node, op=e.op.code)
+            _check_constraints(node, e, b.values, caps.constraints)
+            b.commands.append(e)
+    used = set()
+    for c in b.commands:
+        used.update(c.inputs)
+        used.update(c.outputs)
+        if c.state is not None:
+            used.add(c.state)
+    used.update(lowered.quant_scales.values())
+    for vid in sorted(used):
+        if b.values[vid].dtype not in caps.dtypes:
+            raise CompileError("UnsupportedDType", value=vid, dtype=b.values[vid].dtype)
+    align = max(64, caps.min_buffer_align)
+    plan = plan_memory(b.values, b.commands, align)
+    if plan.scratchpad_bytes > caps.max_scratchpad_bytes:
+        raise CompileError("PlanOverflow", required=plan.scratchpad_bytes, limit=caps.max_scratchpad_bytes)
+    validate_plan(b.values, b.commands, plan, align)
+    ir = CommandBuffer(cb.ir_version, b.values, b.commands, plan, list(cb.inputs), list(cb.outputs),
+                       list(cb.states))
+    return dataclasses.replace(lowered, ir=ir)

@@ -16,6 +16,7 @@ import numpy as np
 import oracle
 from conftest import assert_normwise
 from oracle.cpu_device import OracleDevice
+from starlight_amd import device as hipdevice
 from starlight_amd import engine, formats, graph, synth
 from starlight_amd.graph import LlamaConfig, weight_specs
 from starlight_amd.ir import QuantFormat
@@ -77,8 +78,9 @@ class Pair:
 
     def __init__(self, hip, cfg: LlamaConfig, batch: int, prompt_len: int, max_seq: int, seed: int):
         self.cfg, self.batch, self.prompt_len, self.max_seq = cfg, batch, prompt_len, max_seq
-        pre_l = graph.lower_llama(cfg, batch, prompt_len, max_seq)
-        dec_l = graph.lower_llama(cfg, batch, 1, max_seq)
+        caps = graph.DeviceCapabilities.from_c(hipdevice.capabilities())
+        pre_l = graph.compile_for(graph.lower_llama(cfg, batch, prompt_len, max_seq), caps)
+        dec_l = graph.compile_for(graph.lower_llama(cfg, batch, 1, max_seq), caps)
         gb = upload(hip, cfg, seed)
         self.gpu = engine.NativeEngine(hip, engine.compile_program(pre_l, gb), engine.compile_program(dec_l, gb),
                                        batch, max_seq)

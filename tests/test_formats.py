@@ -43,7 +43,7 @@ def test_round_trip_keeps_payload_scales_and_dense_tensors(tmp_path, fmt, group,
         meta = json.loads(f.metadata()["starlight.quantization"])
         assert meta == {"version": 1, "tensors": {"proj": {"format": "int4" if fmt == QuantFormat.INT4 else "int8",
                                                            "group_size": group, "shape": [n, k],
-                                                           "scale": "proj.scale"}}}
+                                                           "scale": "proj.__scales"}}}
         assert f.get_tensor("proj").dtype == (np.uint8 if fmt == QuantFormat.INT4 else np.int8)
 
 
@@ -73,15 +73,15 @@ def test_malformed_checkpoints_are_rejected(tmp_path, case, message):
     n, k, g = 4, 8, 4
     payload = np.zeros((n, k // 2), np.uint8)
     scales = np.ones((n, k // g), np.float32)
-    entry = {"format": "int4", "group_size": g, "shape": [n, k], "scale": "w.scale"}
-    tensors = {"w": payload, "w.scale": scales}
+    entry = {"format": "int4", "group_size": g, "shape": [n, k], "scale": "w.__scales"}
+    tensors = {"w": payload, "w.__scales": scales}
     meta = {"version": 1, "tensors": {"w": entry}}
     if case == "no_scale":
-        del tensors["w.scale"]
+        del tensors["w.__scales"]
     elif case == "payload_dtype":
         tensors["w"] = payload.view(np.int8)
     elif case == "scale_shape":
-        tensors["w.scale"] = np.ones((n, 1), np.float32)
+        tensors["w.__scales"] = np.ones((n, 1), np.float32)
     elif case == "format":
         entry["format"] = "int3"
     elif case == "version":

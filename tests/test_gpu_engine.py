@@ -203,3 +203,27 @@ def test_batched_decode_matches_a_step_loop(hip):
         cur = logits.reshape(B, cfg.vocab).argmax(axis=1).astype(np.uint32)
         want.append(cur.copy())
     np.testing.assert_array_equal(got, np.stack(want))
+
+
+def test_native_build_binds_scale_params_and_rejects_a_missing_one(hip):
+    """sl_engine_build binds every quantized Param to its `<role>.__scales`
+    Param from the program (ARCH-0006:147) and fails with Execution when
+    one has no bound buffer."""
+    from starlight_amd.device import DeviceError
+    cfg = LlamaConfig(layers=1, hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=384,
+                      theta=500_000.0, quant=QuantFormat.INT4)
+    bufs = engine.upload_weights(hip, cfg, synth.llama_weights(cfg, 5))
+    low = graph.lower_llama(cfg, 1, 1, 16)
+    missing = {k: v for k, v in bufs.items() if k != "layers.0.attn.o.__scales"}
+    with pytest.raises(DeviceError) as e:
+        engine.NativeEngine(hip, engine.compile_program(low, missing), engine.compile_program(low, missing), 1, 16)
+    assert e.value == DeviceError.execution("quantized Param has no bound scale Param")
+    eng = engine.NativeEngine(hip, engine.compile_program(low, bufs), engine.compile_program(low, bufs), 1, 16)
+    out = np.zeros(cfg.vocab, np.float32)
+    eng.step(eng.DECODE, [3], [0], 1, 0, out)
+    cdev = OracleDevice()
+    cb = engine.upload_weights(cdev, cfg, synth.llama_weights(cfg, 5))
+    cpu = engine.Engine(cdev, engine.compile_program(low, cb), engine.compile_program(low, cb), 1, 16)
+    want = np.zeros(cfg.vocab, np.float32)
+    cpu.step(cpu.DECODE, [3], [0], 1, 0, want)
+    assert_normwise(out, want)

@@ -17,6 +17,7 @@ import pytest
 
 import oracle
 from conftest import assert_elementwise, assert_normwise, rel_l2
+from starlight_amd.device import DeviceError
 from starlight_amd.ir import BufferRef, Op, RopeVariant, Value, ValueRole
 
 pytestmark = pytest.mark.gpu
@@ -282,3 +283,162 @@ def test_silu_then_mul_fuses_only_when_the_silu_result_is_dead(hip, silu_first, 
         np.testing.assert_array_equal(t, oracle.scale(src, 0.5))
     else:
         assert_elementwise(t, t_want)
+
+
+def test_projection_after_attention_when_the_mirror_does_not_fit(hip, monkeypatch):
+    """A device whose workspace holds the decode partials but not the copy of
+    the merged heads the chained output projection would read: the
+    projection runs on its own from MergeHeads' output, which must then be
+    written (8B decode shapes at 1000 cached positions, INT4 o-proj, and the
+    residual Add)."""
+    from starlight_amd import quant
+    from starlight_amd.device import HipDevice
+    from starlight_amd.ir import QuantFormat
+
+    B, H, Hkv, S, past, D, max_seq = 1, 32, 8, 1, 1000, 128, 1100
+    parts = (max_seq + 127) // 128
+    partials = B * Hkv * parts * (H // Hkv) * S * (4 + D)  # floats of the decode partials
+    monkeypatch.setenv("SL_HIP_WORKSPACE_BYTES", str((partials + 2048) * 4))
+    small = HipDevice(0)
+    try:
+        theta, scale = 500000.0, float(np.float32(1.0 / math.sqrt(D)))
+        r = np.random.default_rng(77)
+        nq, nk = B * S * H * D, B * S * Hkv * D
+        q, k, v = (r.uniform(-1, 1, n).astype(np.float32) for n in (nq, nk, nk))
+        cache = r.uniform(-1, 1, B * 2 * max_seq * Hkv * D).astype(np.float32)
+        resid = r.standard_normal(4096).astype(np.float32)
+        w = (r.standard_normal((4096, H * D)) * 0.02).astype(np.float32)
+        words, scales = quant.quantize(w, 128, QuantFormat.INT4)
+        wb, sb = small.upload_new_u32(words), small.upload_new_f32(scales)
+        small.bind_quantized(wb, sb, QuantFormat.INT4, 128, 4096, H * D)
+        pos = np.full(B * S, past, np.uint32)
+        names = [("q", nq), ("k", nk), ("v", nk), ("qh", nq), ("kh", nk), ("vh", nk), ("qr", nq), ("kr", nk),
+                 ("att", nq), ("merged", nq), ("o", 4096), ("h2", 4096)]
+        offs, cur = {}, 0
+        for name, n in names:
+            offs[name] = (cur, n)
+            cur += (n + 63) // 64 * 64
+        init = np.zeros(cur, np.float32)
+        for name, arr in (("q", q), ("k", k), ("v", v)):
+            o, n = offs[name]
+            init[o:o + n] = arr
+        scratch = small.upload_new_f32(init)
+        cb, pb, rb = small.upload_new_f32(cache), small.upload_new_u32(pos), small.upload_new_f32(resid)
+        ref = {name: BufferRef(scratch, o, n) for name, (o, n) in offs.items()}
+        posr = BufferRef(pb, 0, B * S)
+        qf, kf = Value.f32([B, S, H * D]), Value.f32([B, S, Hkv * D])
+        q4, k4 = Value.f32([B, H, S, D]), Value.f32([B, Hkv, S, D])
+        hv = Value.f32([B, S, 4096])
+        before = small.stats()
+        small.dispatch(Op.split_heads(H, D), [ref["q"]], [qf], [ref["qh"]], [q4])
+        small.dispatch(Op.split_heads(Hkv, D), [ref["k"]], [kf], [ref["kh"]], [k4])
+        small.dispatch(Op.split_heads(Hkv, D), [ref["v"]], [kf], [ref["vh"]], [k4])
+        small.dispatch(Op.rope(RopeVariant.NEOX, theta), [ref["qh"], posr], [q4, Value.u32([B, S])], [ref["qr"]],
+                       [q4])
+        small.dispatch(Op.rope(RopeVariant.NEOX, theta), [ref["kh"], posr], [k4, Value.u32([B, S])], [ref["kr"]],
+                       [k4])
+        small.dispatch(Op.causal_attention(0, H, Hkv, D, scale),
+                       [ref["qr"], ref["kr"], ref["vh"], BufferRef(cb, 0, cache.size)],
+                       [q4, k4, k4, Value.f32([B, 1, 2, max_seq, Hkv, D], ValueRole.STATE)], [ref["att"]], [q4],
+                       [past])
+        small.dispatch(Op.merge_heads(H, D), [ref["att"]], [q4], [ref["merged"]], [qf])
+        small.dispatch(Op.matmul_nt(), [ref["merged"], BufferRef(wb, 0, words.size)],
+                       [qf, Value.quantized([4096, H * D], QuantFormat.INT4, 128)], [ref["o"]], [hv])
+        small.dispatch(Op.add(), [BufferRef(rb, 0, 4096), ref["o"]], [hv, hv], [ref["h2"]], [hv])
+        small.synchronize()
+        assert small.stats()["fused_commands"] - before["fused_commands"] >= 7
+        got = small.read_f32(scratch, cur)
+    finally:
+        small.close()
+    qh, kh, vh = (oracle.split_heads(x, B, S, h, D) for x, h in ((q, H), (k, Hkv), (v, Hkv)))
+    qr = oracle.rope(qh, pos, B, H, S, D, theta, "neox")
+    kr = oracle.rope(kh, pos, B, Hkv, S, D, theta, "neox")
+    att, _ = oracle.causal_attention(qr, kr, vh, cache, B, 1, 0, H, Hkv, S, past, D, max_seq, scale)
+    merged = oracle.merge_heads(att, B, S, H, D)
+    o_want = oracle.matmul_nt(merged, quant.dequantize(words, scales, 4096, H * D, 128, QuantFormat.INT4), 1, 1,
+                              H * D, 4096)
+    for name, want in (("merged", merged), ("o", o_want)):
+        o, n = offs[name]
+        assert_normwise(got[o:o + n], want)
+    o, n = offs["h2"]
+    og, _ = offs["o"]
+    np.testing.assert_array_equal(got[o:o + n], oracle.add(resid, got[og:og + 4096], 4096))
+
+
+@pytest.mark.parametrize("variant", ["separate", "out_is_gemv_out", "out_is_residual", "swiglu", "norm_reads"])
+def test_gemv_residual_add_fusions(hip, variant):
+    """A quantized MatMulNT (or the SwiGlu down projection) followed by the
+    residual Add runs as one launch with the Add in its epilogue. An Add
+    writing over the GEMV's output or over its residual input never reaches
+    the fusion: dispatch rejects an output overlapping an input
+    (device.rs:338-377). When the residual operand is the output of the
+    RmsNorm fused into the same launch, the Add stays separate: block 0
+    writes that output while other blocks read it."""
+    from starlight_amd import quant
+    from starlight_amd.ir import QuantFormat
+
+    r = np.random.default_rng(90 + len(variant))
+    k, n, inter = 512, 512, 1024
+    x = r.standard_normal(k).astype(np.float32)
+    resid = r.standard_normal(n).astype(np.float32)
+    gamma = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+
+    def qw(rows, cols):
+        w = (r.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        words, scales = quant.quantize(w, 128, QuantFormat.INT4)
+        wb, sb = hip.upload_new_u32(words), hip.upload_new_f32(scales)
+        hip.bind_quantized(wb, sb, QuantFormat.INT4, 128, rows, cols)
+        return (BufferRef(wb, 0, words.size), Value.quantized([rows, cols], QuantFormat.INT4, 128),
+                quant.dequantize(words, scales, rows, cols, 128, QuantFormat.INT4))
+
+    # scratch: x | normed | y | resid | out
+    stride = 1024
+    init = np.zeros(5 * stride, np.float32)
+    init[0:k], init[3 * stride:3 * stride + n] = x, resid
+    buf = hip.upload_new_f32(init)
+    X, NORMED, Y, RES, OUT = (BufferRef(buf, i * stride, n) for i in range(5))
+    gb = hip.upload_new_f32(gamma)
+    xv, yv = Value.f32([1, 1, k]), Value.f32([1, 1, n])
+    before = hip.stats()
+    if variant == "swiglu":
+        g, u, d = qw(inter, k), qw(inter, k), qw(n, inter)
+        hip.dispatch(Op.swiglu(), [X, g[0], u[0], d[0]], [xv, g[1], u[1], d[1]], [Y], [yv])
+        y_want = oracle.swiglu(x, g[2], u[2], d[2], 1, k, inter)
+        add_in, add_out = [RES, Y], OUT
+        resid_want = resid
+    elif variant == "norm_reads":
+        w = qw(n, k)
+        hip.dispatch(Op.rms_norm(1e-5), [X, BufferRef(gb, 0, k)], [xv, Value.f32([k], ValueRole.PARAM)], [NORMED],
+                     [xv])
+        hip.dispatch(Op.matmul_nt(), [NORMED, w[0]], [xv, w[1]], [Y], [yv])
+        normed = oracle.rms_norm(x, gamma, 1, k, 1e-5)
+        y_want = oracle.matmul_nt(normed, w[2], 1, 1, k, n)
+        add_in, add_out = [NORMED, Y], OUT  # the residual operand is the norm's output
+        resid_want = normed
+    else:
+        w = qw(n, k)
+        hip.dispatch(Op.matmul_nt(), [X, w[0]], [xv, w[1]], [Y], [yv])
+        y_want = oracle.matmul_nt(x, w[2], 1, 1, k, n)
+        add_out = {"separate": OUT, "out_is_gemv_out": Y, "out_is_residual": RES}[variant]
+        add_in = [RES, Y]
+        resid_want = resid
+    if add_out is not OUT:
+        with pytest.raises(DeviceError) as e:
+            hip.dispatch(Op.add(), add_in, [yv, yv], [add_out], [yv])
+        assert e.value == DeviceError.execution("a command output aliases an overlapping input range")
+        hip.synchronize()
+        assert_normwise(hip.read_f32(buf, 5 * stride)[Y.offset:Y.offset + n], y_want)
+        return
+    hip.dispatch(Op.add(), add_in, [yv, yv], [add_out], [yv])
+    hip.synchronize()
+    fused = hip.stats()["fused_commands"] - before["fused_commands"]
+    got = hip.read_f32(buf, 5 * stride)
+    y_got = got[Y.offset:Y.offset + n]
+    out_got = got[add_out.offset:add_out.offset + n]
+    assert_normwise(y_got, y_want)
+    np.testing.assert_array_equal(out_got, oracle.add(resid_want, y_got, n))
+    if variant == "norm_reads":
+        assert fused == 2  # RmsNorm + MatMulNT; the Add runs on its own
+        assert_normwise(got[NORMED.offset:NORMED.offset + k], resid_want)
+    else:
+        assert fused == 2  # MatMulNT (or SwiGlu) + Add

@@ -191,6 +191,28 @@ sl_status sl_hip_dispatch(sl_hip_device *device, const sl_op *op, const sl_buffe
                           const sl_value *output_values, size_t n_outputs, const uint32_t *scalars,
                           size_t n_scalars);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): sl_hip_dispatch without the log. It validates exactly
+ * as sl_hip_dispatch does, then enqueues this one command's kernels on the
+ * device's stream at once (no fusion, no graph, past_len taken from the
+ * scalar), and calls no hipMalloc, hipFree or allocating routine. Its
+ * scratch memory (attention partials, SwiGlu intermediates, split-K
+ * partials) is a static array of SL_HIP_STATIC_SCRATCH_BYTES held by each
+ * GPU the library runs on until the process ends, not the device workspace.
+ * Errors: Execution when commands are still logged (call sl_hip_submit
+ * first) or the array's address could not be found at device creation;
+ * Unimplemented when the command needs more scratch than the array holds.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (several devices or streams on it) race. A Gather whose id buffer is
+ * larger than 16 MiB checks its ids with a device-to-host copy and a stream
+ * synchronize, which graph capture does not allow. */
+#define SL_HIP_STATIC_SCRATCH_BYTES (16u << 20)
+sl_status sl_hip_dispatch_noalloc(sl_hip_device *device, const sl_op *op, const sl_buffer_ref *inputs,
+                                  const sl_value *input_values, size_t n_inputs, const sl_buffer_ref *outputs,
+                                  const sl_value *output_values, size_t n_outputs, const uint32_t *scalars,
+                                  size_t n_scalars);
+
 /* Device::synchronize (device.rs:210-212): submits the logged commands,
  * blocks until all of them have finished and reports any execution failure. */
 sl_status sl_hip_synchronize(sl_hip_device *device);

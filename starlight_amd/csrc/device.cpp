@@ -93,6 +93,7 @@ struct Device : BufferView {
     std::vector<Buffer> buffers;
     float* workspace = nullptr;
     uint64_t workspace_floats = 0;
+    float* static_scratch = nullptr;  // this GPU's static array (no-allocation entry point)
     uint32_t* counters = nullptr;
     std::vector<uint32_t> id_scratch;
     Error last;
@@ -1009,6 +1010,13 @@ sl_status sl_hip_device_create(int ordinal, sl_hip_device** out) {
         return SL_ERR_OUT_OF_MEMORY;
     }
     d->id_scratch.resize(slhip::kIdScratchElements);
+    // The static scratch array's address on this GPU (current here); kept
+    // per device, and a failed lookup leaves only the no-allocation entry
+    // point unavailable.
+    if (slhip::static_scratch_address(ordinal, &d->static_scratch) != hipSuccess) {
+        (void)hipGetLastError();
+        d->static_scratch = nullptr;
+    }
     *out = d;
     return SL_OK;
 }
@@ -1074,6 +1082,33 @@ sl_status sl_hip_dispatch(sl_hip_device* d, const sl_op* op, const sl_buffer_ref
     if (n_outputs) c.out = outputs[0];
     d->log.push_back(c);
     if (d->log.size() >= slhip::kLogFlushLength) return slhip::flush(d);
+    return SL_OK;
+}
+
+sl_status sl_hip_dispatch_noalloc(sl_hip_device* d, const sl_op* op, const sl_buffer_ref* inputs,
+                                  const sl_value* input_values, size_t n_inputs, const sl_buffer_ref* outputs,
+                                  const sl_value* output_values, size_t n_outputs, const uint32_t* scalars,
+                                  size_t n_scalars) {
+    slhip::Plan plan;
+    Error err;
+    if (!slhip::validate_dispatch(*d, *op, inputs, input_values, n_inputs, outputs, output_values, n_outputs,
+                                  scalars, n_scalars, &plan, &err))
+        return d->fail(err);
+    if (!slhip::device_limits(plan, slhip::kStaticScratchFloats, &err)) return d->fail(err);
+    if (!d->log.empty())
+        return d->fail(Error::execution("commands are still logged: submit them before sl_hip_dispatch_noalloc"));
+    if (d->static_scratch == nullptr)
+        return d->fail(Error::execution("the static scratch array is not available on this device"));
+    if (plan.code == SL_OP_GATHER && !slhip::gather_ids_in_range(d, inputs[1], plan.vocab, &err))
+        return d->fail(err);
+    sl_buffer_ref out{};
+    if (n_outputs) out = outputs[0];
+    // past_len reaches the kernels as the scalar itself (no device word)
+    const hipError_t e =
+        slhip::launch(d, plan, inputs, &out, nullptr,
+                      slhip::Workspace{d->static_scratch, slhip::kStaticScratchFloats, d->counters,
+                                       slhip::kCounterWords});
+    if (e != hipSuccess) return d->hip_fail(e);
     return SL_OK;
 }
 

@@ -107,6 +107,13 @@ struct AttentionArgs {
 // pow / sin / cos rounded once (reference/rope.rs:32-35).
 hipError_t launch_rope_sincos(const uint32_t* positions, uint64_t tokens, uint64_t head_dim, float theta,
                               float* table, hipStream_t s);
+// Floats of the static per-GPU scratch array of the no-allocation entry
+// point (SL_HIP_STATIC_SCRATCH_BYTES).
+constexpr uint64_t kStaticScratchFloats = SL_HIP_STATIC_SCRATCH_BYTES / 4;
+// Its address on device `ordinal`, which must be the current device at the
+// first call for that ordinal (hipGetSymbolAddress, cached per ordinal).
+hipError_t static_scratch_address(int ordinal, float** out);
+
 // Appends k_new / v_new to the cache and computes the attention output.
 hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStream_t s);
 // SplitHeads x3 + Rope x2 + CausalAttention (+ MergeHeads) as the two decode

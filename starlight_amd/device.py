@@ -164,6 +164,10 @@ def load_library() -> ctypes.CDLL:
                              ctypes.POINTER(ir.CValue), ctypes.c_size_t, ctypes.POINTER(ir.CBufferRef),
                              ctypes.POINTER(ir.CValue), ctypes.c_size_t, U32P, ctypes.c_size_t],
                             ctypes.c_int),
+        "sl_hip_dispatch_noalloc": ([P, ctypes.POINTER(ir.COp), ctypes.POINTER(ir.CBufferRef),
+                                     ctypes.POINTER(ir.CValue), ctypes.c_size_t, ctypes.POINTER(ir.CBufferRef),
+                                     ctypes.POINTER(ir.CValue), ctypes.c_size_t, U32P, ctypes.c_size_t],
+                                    ctypes.c_int),
         "sl_hip_synchronize": ([P], ctypes.c_int),
         "sl_hip_last_error": ([P, ctypes.POINTER(ir.CError)], None),
         "sl_hip_bind_quantized": ([P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
@@ -282,6 +286,20 @@ class HipDevice:
         sc = _scalars(scalars)
         self._check(self._lib.sl_hip_dispatch(self._h, ctypes.byref(c_op), in_refs, in_vals, len(inputs),
                                               out_refs, out_vals, len(outputs), sc, len(scalars)))
+
+    def dispatch_noalloc(self, op: ir.Op, inputs: Sequence[ir.BufferRef], input_values: Sequence[ir.Value],
+                         outputs: Sequence[ir.BufferRef], output_values: Sequence[ir.Value],
+                         scalars: Sequence[int] = ()) -> None:
+        """sl_hip_dispatch_noalloc: validate, then enqueue this command's
+        kernels at once with the static per-GPU scratch (no allocation)."""
+        if len(inputs) != len(input_values) or len(outputs) != len(output_values):
+            raise DeviceError.execution("ports and values have different lengths")
+        c_op = op.to_c()
+        in_refs, in_vals = _port_arrays(inputs, input_values)
+        out_refs, out_vals = _port_arrays(outputs, output_values)
+        sc = _scalars(scalars)
+        self._check(self._lib.sl_hip_dispatch_noalloc(self._h, ctypes.byref(c_op), in_refs, in_vals, len(inputs),
+                                                      out_refs, out_vals, len(outputs), sc, len(scalars)))
 
     def synchronize(self) -> None:
         self._check(self._lib.sl_hip_synchronize(self._h))

@@ -156,7 +156,10 @@ def test_8b_shaped_decode_fuses_and_replays(hip):
 
 def test_model_from_a_saved_checkpoint_on_gpu(hip, tmp_path):
     """A quantized Safetensors checkpoint (starlight_amd.formats) loaded and
-    uploaded: the same ids and logits as the f32 weights quantized on upload."""
+    uploaded: the same ids and logits as the f32 weights quantized on upload,
+    and the oracle device running the same loaded checkpoint agrees with the
+    GPU (every step's logits within 1e-4 normwise, greedy ids equal except at
+    a near-tie)."""
     from starlight_amd import formats
     cfg = LlamaConfig(layers=2, hidden=512, heads=8, kv_heads=2, head_dim=64, ffn=1024, vocab=3000,
                       theta=500_000.0, quant=QuantFormat.INT4)
@@ -174,6 +177,13 @@ def test_model_from_a_saved_checkpoint_on_gpu(hip, tmp_path):
     t_ck, l_ck = run(formats.upload(hip, cfg, *formats.load(path)))
     np.testing.assert_array_equal(np.asarray(t_ck), np.asarray(t_ref))
     np.testing.assert_array_equal(np.asarray(l_ck), np.asarray(l_ref))
+    # the oracle on the same loaded checkpoint
+    cdev = OracleDevice()
+    cb = formats.upload(cdev, cfg, *formats.load(path))
+    cpu = engine.Engine(cdev, engine.compile_program(graph.lower_llama(cfg, 1, 6, 32), cb),
+                        engine.compile_program(graph.lower_llama(cfg, 1, 1, 32), cb), 1, 32)
+    c_tokens, c_logits = cpu.generate(prompt, 4, cfg.vocab)
+    assert check_generation(t_ck, l_ck, c_tokens, c_logits) >= 3
 
 
 def test_batched_decode_matches_a_step_loop(hip):

@@ -239,6 +239,44 @@ void sl_hip_last_error(const sl_hip_device *device, sl_error *out);
 sl_status sl_hip_bind_quantized(sl_hip_device *device, uint32_t payload, uint32_t scales,
                                 uint32_t qformat, uint32_t group_size, uint32_t n, uint32_t k);
 
+/* Paged KV cache (no reference counterpart: gaps G-17 paged KV and G-18
+ * per-request lengths, ARCH-0008:123-124). `pool` is an f32 buffer of
+ * layers * num_pages * 2 * page_size * kv_heads * head_dim elements laid out
+ * [layer][page][K, V][slot][kv_head][head_dim]; position j of batch row b is
+ * slot j % page_size of page block_table[b * pages_per_seq + j / page_size];
+ * `block_table` (u32, batch * pages_per_seq ids) and `seq_lens` (u32, batch
+ * cached lengths) are u32 buffers of at most 16 MiB (the device checks their
+ * contents on the host before launching). page_size is a multiple of 16. */
+typedef struct sl_paged_kv {
+    uint32_t pool;
+    uint32_t block_table;
+    uint32_t seq_lens;
+    uint32_t layers;
+    uint32_t num_pages;
+    uint32_t page_size;
+    uint32_t pages_per_seq;
+    uint32_t reserved;
+} sl_paged_kv;
+
+/* Decode attention over a paged KV cache, one new token per batch row, each
+ * row at its own length (continuous batching): for row b with
+ * L = seq_lens[b], appends k_new / v_new [batch, kv_heads, 1, head_dim] at
+ * position L of layer op->layer, then writes to `out` [batch, heads, 1,
+ * head_dim] the CausalAttention of q [batch, heads, 1, head_dim] over
+ * positions 0..L (reference/attention.rs:129-219 with the cache read
+ * through the block table). `op` is a CausalAttention op (layer, heads,
+ * kv_heads, head_dim, scale). Logged commands are submitted first; the
+ * attention is enqueued at once (no fusion, no graph). Errors: Execution for
+ * a length whose position L falls outside the row's table, a page id not
+ * below num_pages, a row appending into a page another row reads (pages
+ * only read may be shared, e.g. a common prefix), or shapes and buffers
+ * that do not match; Unimplemented for head_dim not a multiple of 64 up to
+ * 256, more than 16 query heads per KV head, or page_size not a multiple of
+ * 16. seq_lens is not advanced: the caller adds 1 per row after the step. */
+sl_status sl_hip_paged_attention(sl_hip_device *device, const sl_op *op, const sl_buffer_ref *q,
+                                 const sl_buffer_ref *k_new, const sl_buffer_ref *v_new, const sl_buffer_ref *out,
+                                 uint32_t batch, const sl_paged_kv *kv);
+
 /* One entry of the buffer table sl_hip_validate_dispatch checks against. */
 typedef enum sl_buffer_kind {
     SL_BUFFER_NONE = 0,

@@ -83,6 +83,7 @@ def _declare(l: ctypes.CDLL) -> None:
         + [ctypes.c_float, _WHY],
         "slr_swiglu": [_F, _SZ] * 5 + [_SZ, _SZ, _SZ, _WHY],
         "slr_rms_norm_matmul": [_F, _SZ] * 4 + [_SZ, _SZ, _SZ, ctypes.c_float, _WHY],
+        "slr_paged_attention_decode": [_F, _F, _F, _F, _SZ, _U32, _U32, _F] + [_SZ] * 9 + [ctypes.c_float, _WHY],
         "slr_quantize_groupwise": [_F, _SZ, _SZ, _SZ, ctypes.c_int, _U8, _F, _WHY],
         "slr_unpack_codes": [_U8, _SZ, _SZ, ctypes.c_int, _I8, _WHY],
         "slr_dequantize_groupwise": [_U8, _F, _SZ, _SZ, _SZ, ctypes.c_int, _F, _WHY],
@@ -279,6 +280,20 @@ def rms_norm_matmul(x, weight, w, rows, hidden, out_features, eps, out_len=None)
 # --------------------------------------------------------------------------
 # Quantization convention (no reference code; parity unpinned vs sl-precision)
 # --------------------------------------------------------------------------
+
+
+def paged_attention_decode(q, k_new, v_new, pool, block_table, seq_lens, batch, layers, layer, num_pages,
+                           page_size, pages_per_seq, heads, kv_heads, head_dim, scale):
+    """Returns (out [batch, heads, head_dim] flat, the pool after the append)."""
+    q, k_new, v_new = _f32(q), _f32(k_new), _f32(v_new)
+    pool = np.array(pool, dtype=np.float32, copy=True)
+    table = np.ascontiguousarray(block_table, dtype=np.uint32)
+    lens = np.ascontiguousarray(seq_lens, dtype=np.uint32)
+    out = np.zeros(batch * heads * head_dim, np.float32)
+    _call("slr_paged_attention_decode", _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(pool), pool.size, _ptr(table, _U32),
+          _ptr(lens, _U32), _ptr(out), batch, layers, layer, num_pages, page_size, pages_per_seq, heads, kv_heads,
+          head_dim, ctypes.c_float(scale))
+    return out, pool
 
 
 def quantize_groupwise(w, n, k, group, bits):

@@ -474,6 +474,93 @@ int slr_causal_attention(const float *q, size_t q_len, const float *k_new, size_
     return SLR_OK;
 }
 
+/* Decode attention over a paged KV cache (no reference counterpart: gaps
+ * G-17/G-18, ARCH-0008:123-124). For each batch row b with L = seq_lens[b]
+ * cached positions: kv_append of the row's new K/V at position L, then the
+ * reference's causal_attention for its one query per head over positions
+ * 0..L (attention.rs:129-219: max, denominator and weighted-sum passes with
+ * the score recomputed each time), reading position j from slot j % page_size
+ * of page block_table[b * pages_per_seq + j / page_size]. The pool is
+ * [layers][num_pages][2][page_size][kv_heads][head_dim]. */
+int slr_paged_attention_decode(const float *q, const float *k_new, const float *v_new, float *pool,
+                               size_t pool_len, const uint32_t *block_table, const uint32_t *seq_lens, float *out,
+                               size_t batch, size_t layers, size_t layer, size_t num_pages, size_t page_size,
+                               size_t pages_per_seq, size_t heads, size_t kv_heads, size_t head_dim, float scale,
+                               const char **why) {
+    if (kv_heads == 0) INVALID("kv_heads must be nonzero");
+    if (heads == 0) INVALID("heads must be nonzero");
+    if (heads % kv_heads != 0) INVALID("heads must be a multiple of kv_heads");
+    if (page_size == 0) INVALID("page_size must be nonzero");
+    if (layer >= layers) INVALID("layer is out of range");
+    size_t want;
+    SHAPE(want, layers, num_pages, 2, page_size, kv_heads, head_dim);
+    EXPECT(pool_len, want);
+    size_t time_stride = kv_heads * head_dim;
+    size_t parity_stride = page_size * time_stride;
+    size_t page_stride = 2 * parity_stride;
+    float *layer_base = pool + layer * num_pages * page_stride;
+    for (size_t b = 0; b < batch; ++b) {
+        size_t L = seq_lens[b];
+        if (L / page_size >= pages_per_seq) INVALID("paged KV length exceeds the row's block table");
+        for (size_t pi = 0; pi <= L / page_size; ++pi)
+            if (block_table[b * pages_per_seq + pi] >= num_pages) INVALID("page id out of range");
+    }
+    for (size_t b = 0; b < batch; ++b) {
+        uint32_t wpage = block_table[b * pages_per_seq + seq_lens[b] / page_size];
+        for (size_t o = 0; o < batch; ++o) {
+            if (o == b) continue;
+            for (size_t pi = 0; pi <= seq_lens[o] / page_size; ++pi)
+                if (block_table[o * pages_per_seq + pi] == wpage) INVALID("a row appends into a page another row reads");
+        }
+    }
+    /* kv_append of every row first, as the reference appends before attending */
+    for (size_t b = 0; b < batch; ++b) {
+        size_t L = seq_lens[b];
+        float *row = layer_base + block_table[b * pages_per_seq + L / page_size] * page_stride +
+                     (L % page_size) * time_stride;
+        for (size_t h = 0; h < kv_heads; ++h) {
+            memcpy(row + h * head_dim, k_new + (b * kv_heads + h) * head_dim, head_dim * sizeof(float));
+            memcpy(row + parity_stride + h * head_dim, v_new + (b * kv_heads + h) * head_dim,
+                   head_dim * sizeof(float));
+        }
+    }
+    size_t group = heads / kv_heads;
+#pragma omp parallel for collapse(2) schedule(dynamic) num_threads(g_threads) if (g_threads > 1 && batch * heads > 1)
+    for (size_t b = 0; b < batch; ++b)
+        for (size_t h = 0; h < heads; ++h) {
+            size_t kv_head = h / group;
+            size_t key_count = seq_lens[b] + 1;
+            const uint32_t *table = block_table + b * pages_per_seq;
+            const float *query = q + (b * heads + h) * head_dim;
+#define PAGED_KEY(j) (layer_base + table[(j) / page_size] * page_stride + ((j) % page_size) * time_stride + \
+                      kv_head * head_dim)
+            float maximum = -INFINITY;
+            for (size_t j = 0; j < key_count; ++j) {
+                float score = dot(query, PAGED_KEY(j), head_dim) * scale;
+                if (score > maximum) maximum = score;
+            }
+            float denominator = 0.0f;
+            for (size_t j = 0; j < key_count; ++j) {
+                float score = dot(query, PAGED_KEY(j), head_dim) * scale;
+                denominator = denominator + expf(score - maximum);
+            }
+            float inverse = 1.0f / denominator;
+            float *orow = out + (b * heads + h) * head_dim;
+            for (size_t d = 0; d < head_dim; ++d) orow[d] = 0.0f;
+            for (size_t j = 0; j < key_count; ++j) {
+                float score = dot(query, PAGED_KEY(j), head_dim) * scale;
+                float probability = expf(score - maximum) * inverse;
+                const float *vrow = PAGED_KEY(j) + parity_stride;
+                for (size_t d = 0; d < head_dim; ++d) {
+                    float term = probability * vrow[d];
+                    orow[d] = orow[d] + term;
+                }
+            }
+#undef PAGED_KEY
+        }
+    return SLR_OK;
+}
+
 /* swiglu (reference/swiglu.rs:40-84): per row, per intermediate index i,
  * g = silu(dot(x, Wg[i])), u = dot(x, Wu[i]), out[r, j] += (g*u) * Wd[j, i]. */
 int slr_swiglu(const float *x, size_t x_len, const float *w_gate, size_t g_len, const float *w_up,

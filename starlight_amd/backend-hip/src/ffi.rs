@@ -172,6 +172,19 @@ pub struct sl_hip_stats {
     pub graph_replays: u64,
 }
 
+#[repr(C)]
+#[derive(Clone, Copy, Debug, Default)]
+pub struct sl_paged_kv {
+    pub pool: u32,
+    pub block_table: u32,
+    pub seq_lens: u32,
+    pub layers: u32,
+    pub num_pages: u32,
+    pub page_size: u32,
+    pub pages_per_seq: u32,
+    pub reserved: u32,
+}
+
 /// Opaque device handle.
 #[repr(C)]
 pub struct sl_hip_device {
@@ -224,6 +237,16 @@ extern "C" {
         group_size: u32,
         n: u32,
         k: u32,
+    ) -> sl_status;
+    pub fn sl_hip_paged_attention(
+        device: *mut sl_hip_device,
+        op: *const sl_op,
+        q: *const sl_buffer_ref,
+        k_new: *const sl_buffer_ref,
+        v_new: *const sl_buffer_ref,
+        out: *const sl_buffer_ref,
+        batch: u32,
+        kv: *const sl_paged_kv,
     ) -> sl_status;
     pub fn sl_hip_validate_dispatch(
         buffers: *const sl_buffer_desc,

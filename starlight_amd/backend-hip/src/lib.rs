@@ -26,6 +26,20 @@ use sl_ir::{
     RopeVariant, ShapeConstraints, TensorEncoding, Value, ValueRole, IR_VERSION,
 };
 
+/// A paged KV cache's device buffers and geometry: `pool` f32
+/// [layer][page][K, V][slot][kv_head][head_dim], `block_table` u32
+/// [batch][pages_per_seq] page ids, `seq_lens` u32 [batch] cached lengths.
+#[derive(Clone, Copy, Debug)]
+pub struct PagedKv {
+    pub pool: BufferId,
+    pub block_table: BufferId,
+    pub seq_lens: BufferId,
+    pub layers: u32,
+    pub num_pages: u32,
+    pub page_size: u32,
+    pub pages_per_seq: u32,
+}
+
 /// The HIP device. Single owner: every method takes `&mut self`, as the
 /// trait does, and the library is not called from two threads at once.
 pub struct HipDevice {
@@ -115,6 +129,36 @@ impl HipDevice {
                 scalars.len(),
             )
         };
+        self.check(status)
+    }
+
+    /// `sl_hip_paged_attention`: one decode step of CausalAttention for
+    /// `batch` rows over a paged KV cache, each row at its own cached length
+    /// (`seq_lens`), reading and appending through its block table. No
+    /// reference counterpart (ARCH-0008:123-124, gaps G-17 and G-18).
+    pub fn paged_attention(
+        &mut self,
+        op: &Op,
+        q: &BufferRef,
+        k_new: &BufferRef,
+        v_new: &BufferRef,
+        out: &BufferRef,
+        batch: u32,
+        kv: &PagedKv,
+    ) -> Result<(), DeviceError> {
+        let op = to_sl_op(op)?;
+        let raw_kv = ffi::sl_paged_kv {
+            pool: kv.pool.0,
+            block_table: kv.block_table.0,
+            seq_lens: kv.seq_lens.0,
+            layers: kv.layers,
+            num_pages: kv.num_pages,
+            page_size: kv.page_size,
+            pages_per_seq: kv.pages_per_seq,
+            reserved: 0,
+        };
+        let (q, k, v, o) = (to_sl_buffer_ref(q), to_sl_buffer_ref(k_new), to_sl_buffer_ref(v_new), to_sl_buffer_ref(out));
+        let status = unsafe { ffi::sl_hip_paged_attention(self.raw, &op, &q, &k, &v, &o, batch, &raw_kv) };
         self.check(status)
     }
 

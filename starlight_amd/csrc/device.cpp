@@ -102,6 +102,7 @@ struct Device : BufferView {
     uint32_t options = SL_HIP_OPT_FUSION | SL_HIP_OPT_GRAPHS;
     uint32_t* dyn = nullptr;  // device past_len slots, kLogFlushLength of them
     std::vector<uint32_t> dyn_values;
+    std::vector<uint32_t> paged_readers;  // host scratch of the paged-attention page check
     std::vector<uint64_t> key, prev_key;
     std::vector<GraphEntry> graphs;
     size_t last_graph = SIZE_MAX;  // entry of graphs the previous replay or capture used
@@ -1108,6 +1109,107 @@ sl_status sl_hip_dispatch_noalloc(sl_hip_device* d, const sl_op* op, const sl_bu
         slhip::launch(d, plan, inputs, &out, nullptr,
                       slhip::Workspace{d->static_scratch, slhip::kStaticScratchFloats, d->counters,
                                        slhip::kCounterWords});
+    if (e != hipSuccess) return d->hip_fail(e);
+    return SL_OK;
+}
+
+sl_status sl_hip_paged_attention(sl_hip_device* d, const sl_op* op, const sl_buffer_ref* q,
+                                 const sl_buffer_ref* k_new, const sl_buffer_ref* v_new, const sl_buffer_ref* out,
+                                 uint32_t batch, const sl_paged_kv* kv) {
+    using slhip::Error;
+    if (op == nullptr || q == nullptr || k_new == nullptr || v_new == nullptr || out == nullptr || kv == nullptr)
+        return d->fail(Error::execution("paged attention received a null argument"));
+    if (op->code != SL_OP_CAUSAL_ATTENTION) return d->fail(Error::unsupported_op(op->code));
+    const uint64_t H = op->heads, Hkv = op->kv_heads, D = op->head_dim, B = batch;
+    if (Hkv == 0 || H == 0 || H % Hkv != 0) return d->fail(Error::execution("heads must be a multiple of kv_heads"));
+    if (D == 0 || D % 64 != 0 || D > 256)
+        return d->fail(Error::unimplemented("paged attention needs head_dim a multiple of 64 up to 256"));
+    if (H / Hkv > 16) return d->fail(Error::unimplemented("paged attention takes at most 16 query heads per KV head"));
+    if (kv->page_size == 0 || kv->page_size % 16 != 0)
+        return d->fail(Error::unimplemented("page_size must be a nonzero multiple of 16"));
+    if (kv->layers == 0 || op->layer >= kv->layers) return d->fail(Error::execution("layer is out of range"));
+    if (kv->num_pages == 0 || kv->pages_per_seq == 0) return d->fail(Error::execution("the page pool is empty"));
+    // ports: f32 ranges of the stated sizes, the output disjoint from the inputs
+    const struct {
+        const sl_buffer_ref* r;
+        uint64_t len;
+    } ports[4] = {{q, B * H * D}, {k_new, B * Hkv * D}, {v_new, B * Hkv * D}, {out, B * H * D}};
+    for (const auto& pt : ports) {
+        const sl_buffer_ref& r = *pt.r;
+        if (r.buffer >= d->buffers.size() || d->buffers[r.buffer].desc.kind != SL_BUFFER_F32)
+            return d->fail(Error::invalid_buffer(r.buffer));
+        if (r.len != pt.len) return d->fail(Error::execution("paged attention port has the wrong length"));
+        if (r.offset > d->buffers[r.buffer].desc.elements || r.len > d->buffers[r.buffer].desc.elements - r.offset)
+            return d->fail(Error::invalid_range(r.buffer, r.offset, r.len));
+    }
+    for (int i = 0; i < 3; ++i)
+        if (slhip::overlaps(*ports[i].r, *out))
+            return d->fail(Error::execution("a command output aliases an overlapping input range"));
+    const uint64_t pool_len = static_cast<uint64_t>(kv->layers) * kv->num_pages * 2 * kv->page_size * Hkv * D;
+    if (kv->pool >= d->buffers.size() || d->buffers[kv->pool].desc.kind != SL_BUFFER_F32)
+        return d->fail(Error::invalid_buffer(kv->pool));
+    if (d->buffers[kv->pool].desc.elements != pool_len)
+        return d->fail(Error::execution("page pool size does not match its layout"));
+    for (const auto& pt : ports)
+        if (pt.r->buffer == kv->pool)
+            return d->fail(Error::execution("a command output aliases an overlapping input range"));
+    for (uint32_t id : {kv->block_table, kv->seq_lens})
+        if (id >= d->buffers.size() || d->buffers[id].desc.kind != SL_BUFFER_U32)
+            return d->fail(Error::invalid_buffer(id));
+    const slhip::Buffer& tb = d->buffers[kv->block_table];
+    const slhip::Buffer& lb = d->buffers[kv->seq_lens];
+    if (!tb.mirrored || !lb.mirrored)
+        return d->fail(Error::unimplemented("block table and lengths must be u32 buffers of at most 16 MiB"));
+    if (tb.desc.elements < B * kv->pages_per_seq || lb.desc.elements < B)
+        return d->fail(Error::execution("block table or lengths buffer is too small for the batch"));
+    // contents, from the host copies: every position 0..L of a row maps to a
+    // page below num_pages
+    for (uint64_t b = 0; b < B; ++b) {
+        const uint64_t L = lb.mirror[b];
+        if (L / kv->page_size >= kv->pages_per_seq)
+            return d->fail(Error::execution("paged KV length exceeds the row's block table"));
+        for (uint64_t pi = 0; pi <= L / kv->page_size; ++pi)
+            if (tb.mirror[b * kv->pages_per_seq + pi] >= kv->num_pages)
+                return d->fail(Error::execution("page id out of range"));
+    }
+    // the page a row appends into is read by no other row (rows run in
+    // parallel; pages shared read-only, such as a common prefix, are fine).
+    // readers[p]: the one row reading page p, kNone, or kShared for several.
+    constexpr uint32_t kNone = 0xffffffffu, kShared = 0xfffffffeu;
+    std::vector<uint32_t>& readers = d->paged_readers;
+    readers.assign(kv->num_pages, kNone);
+    for (uint64_t b = 0; b < B; ++b)
+        for (uint64_t pi = 0; pi <= lb.mirror[b] / kv->page_size; ++pi) {
+            uint32_t& r = readers[tb.mirror[b * kv->pages_per_seq + pi]];
+            r = (r == kNone || r == b) ? static_cast<uint32_t>(b) : kShared;
+        }
+    for (uint64_t b = 0; b < B; ++b)
+        if (readers[tb.mirror[b * kv->pages_per_seq + lb.mirror[b] / kv->page_size]] != b)
+            return d->fail(Error::execution("a row appends into a page another row reads"));
+    if (slhip::flush(d) != SL_OK) return d->last.status;
+    slhip::PagedAttentionArgs a{};
+    a.q = slhip::fptr(d, *q);
+    a.k_new = slhip::fptr(d, *k_new);
+    a.v_new = slhip::fptr(d, *v_new);
+    a.pool = static_cast<float*>(d->buffers[kv->pool].ptr);
+    a.out = slhip::fptr(d, *out);
+    a.block_table = static_cast<const uint32_t*>(tb.ptr);
+    a.seq_lens = static_cast<const uint32_t*>(lb.ptr);
+    a.batch = B;
+    a.layers = kv->layers;
+    a.layer = op->layer;
+    a.heads = H;
+    a.kv_heads = Hkv;
+    a.head_dim = D;
+    a.num_pages = kv->num_pages;
+    a.page_size = kv->page_size;
+    a.pages_per_seq = kv->pages_per_seq;
+    a.scale = op->scale;
+    if (slhip::paged_attention_workspace_floats(a) > d->workspace_floats)
+        return d->fail(Error::unimplemented("paged attention partials exceed the device workspace"));
+    const hipError_t e = slhip::launch_paged_attention(
+        a, slhip::Workspace{d->workspace, d->workspace_floats, d->counters, slhip::kCounterWords}, d->stream);
+    if (e == hipErrorNotSupported) return d->fail(Error::unimplemented("paged attention shape is not supported"));
     if (e != hipSuccess) return d->hip_fail(e);
     return SL_OK;
 }

@@ -53,6 +53,15 @@ struct Geo {
     float* q_rot;
     float* k_rot;
     const float* rope_tab;  // fused form: the sine / cosine table, or null
+    // paged form (attn_decode<.., PAGED>): key j of row b is slot j % page_size
+    // of page block_table[b * pages_per_seq + j / page_size]; a page holds
+    // K then V, [2][page_size][kv_heads][head_dim], page_stride elements, and
+    // the layer's pages start at wcache + layer_offset; row b has seq_past[b]
+    // cached keys before this step
+    const uint32_t* block_table;
+    const uint32_t* seq_past;
+    uint32_t page_size, pages_per_seq;
+    uint64_t page_stride;
 };
 
 __device__ __forceinline__ uint32_t past_of(const Geo& g) { return g.dyn != nullptr ? g.dyn[0] : g.past_len; }
@@ -238,7 +247,7 @@ __global__ __launch_bounds__(256) void rope_sincos(const uint32_t* __restrict__ 
     table[t * D + half + pair] = static_cast<float>(cos(angle));
 }
 
-template <int DV, int RT, bool FUSED>
+template <int DV, int RT, bool FUSED, bool PAGED>
 __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     prefetch_kernarg<arg_bytes<Geo>()>();
     constexpr int D4 = 16 * DV;  // float4 per row
@@ -255,12 +264,21 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     const uint64_t b = blockIdx.z;
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const int grp = lane / kDecodeLanes, li = lane % kDecodeLanes;
-    const uint32_t past = past_of(g), keys = past + S;
+    const uint32_t past = PAGED ? g.seq_past[b] : past_of(g), keys = past + S;
     const uint32_t ntiles = (keys + kDecodeTile - 1) / kDecodeTile;
 
     const uint64_t time_stride = static_cast<uint64_t>(g.kv_heads) * (4 * D4);
-    float* kbase = g.wcache + b * g.batch_stride + g.layer_offset + kvh * (4 * D4);
-    float* vbase = kbase + g.parity_stride;
+    float* kbase = g.wcache + (PAGED ? 0 : b * g.batch_stride) + g.layer_offset + kvh * (4 * D4);
+    // K row j of this KV head (V is parity_stride further): contiguous, or
+    // through the row's block table
+    auto krow = [&](uint32_t j) -> float* {
+        if constexpr (PAGED) {
+            const uint32_t page = g.block_table[b * g.pages_per_seq + j / g.page_size];
+            return kbase + page * g.page_stride + static_cast<uint64_t>(j % g.page_size) * time_stride;
+        } else {
+            return kbase + static_cast<uint64_t>(j) * time_stride;
+        }
+    };
     // K/V rows of a tile for this lane: cached rows from the cache, new rows
     // from k_new / v_new, zeros past the end.
     auto load_tile = [&](uint32_t tile, float4 (&kx)[kDecodeKeys][DV], float4 (&vx)[kDecodeKeys][DV]) {
@@ -271,8 +289,8 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
             // scores are masked to -inf, so they weigh exactly 0), so the
             // loads carry no branch and the waits before their use are exact.
             const uint32_t j = min(j0 + kb, keys - 1);
-            const float* kr = kbase + static_cast<uint64_t>(j) * time_stride;
-            const float* vr = vbase + static_cast<uint64_t>(j) * time_stride;
+            const float* kr = krow(j);
+            const float* vr = kr + g.parity_stride;
             if (j >= past) {
                 // [B, Hkv, S, D], or [B, S, Hkv * D] before SplitHeads (fused)
                 const uint64_t t = j - past;
@@ -440,8 +458,9 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
                 }
 #pragma unroll
                 for (int u = 0; u < DV; ++u) {
-                    reinterpret_cast<float4*>(kbase + j * time_stride)[li + 16 * u] = kv[kb][u];
-                    reinterpret_cast<float4*>(vbase + j * time_stride)[li + 16 * u] = vv[kb][u];
+                    float* const kw = krow(j);
+                    reinterpret_cast<float4*>(kw)[li + 16 * u] = kv[kb][u];
+                    reinterpret_cast<float4*>(kw + g.parity_stride)[li + 16 * u] = vv[kb][u];
                 }
             }
         }
@@ -802,7 +821,8 @@ uint64_t decode_parts(const AttentionArgs& a) {
 
 // The decode kernels (tile + merge); hipErrorNotSupported for shapes they
 // do not take (nothing launched).
-hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hipStream_t s, bool fused) {
+hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hipStream_t s, bool fused,
+                         bool paged = false) {
     const uint64_t rows = static_cast<uint64_t>(g.group) * a.seq;
     const uint64_t dv = a.head_dim / 64;
     const uint64_t rt = rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
@@ -821,8 +841,9 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
     const dim3 grid(static_cast<unsigned>(parts), g.kv_heads, static_cast<unsigned>(a.batch));
     const size_t lds = fused ? a.seq * a.head_dim * sizeof(float) : 0;
 #define SL_DECODE(DVv, RTv)                                                   \
-    (fused ? attn_decode<DVv, RTv, true><<<grid, 256, lds, s>>>(g)            \
-           : attn_decode<DVv, RTv, false><<<grid, 256, lds, s>>>(g))
+    (fused ? attn_decode<DVv, RTv, true, false><<<grid, 256, lds, s>>>(g)     \
+     : paged ? attn_decode<DVv, RTv, false, true><<<grid, 256, lds, s>>>(g)   \
+           : attn_decode<DVv, RTv, false, false><<<grid, 256, lds, s>>>(g))
     switch (dv * 100 + rt) {
         case 104: SL_DECODE(1, 4); break;
         case 108: SL_DECODE(1, 8); break;
@@ -856,6 +877,35 @@ hipError_t launch_rope_sincos(const uint32_t* positions, uint64_t tokens, uint64
 uint64_t attention_workspace_floats(const AttentionArgs& a) {
     const uint64_t rows = a.heads / (a.kv_heads ? a.kv_heads : 1) * a.seq;
     return a.batch * a.kv_heads * decode_parts(a) * rows * (kDecodePartStride + a.head_dim);
+}
+
+hipError_t launch_paged_attention(const PagedAttentionArgs& p, const Workspace& ws, hipStream_t s) {
+    AttentionArgs a{p.q, p.k_new, p.v_new, p.pool, p.out, p.batch, p.layers, p.layer, p.heads, p.kv_heads, 1,
+                    0, p.head_dim, static_cast<uint64_t>(p.pages_per_seq) * p.page_size, p.scale, nullptr};
+    if (a.batch * a.heads == 0 || a.head_dim == 0 || a.kv_heads == 0 || p.page_size % kDecodeTile != 0)
+        return hipErrorNotSupported;
+    Geo g = make_geo(a, ws);
+    const uint64_t row = static_cast<uint64_t>(p.kv_heads) * p.head_dim;
+    g.parity_stride = p.page_size * row;
+    g.page_stride = 2 * g.parity_stride;
+    g.layer_offset = static_cast<uint64_t>(p.layer) * p.num_pages * g.page_stride;
+    g.batch_stride = 0;
+    g.block_table = p.block_table;
+    g.seq_past = p.seq_lens;
+    g.page_size = p.page_size;
+    g.pages_per_seq = p.pages_per_seq;
+    return launch_decode(a, g, ws, s, false, true);
+}
+
+uint64_t paged_attention_workspace_floats(const PagedAttentionArgs& p) {
+    AttentionArgs a{};
+    a.batch = p.batch;
+    a.heads = p.heads;
+    a.kv_heads = p.kv_heads;
+    a.seq = 1;
+    a.head_dim = p.head_dim;
+    a.max_seq = static_cast<uint64_t>(p.pages_per_seq) * p.page_size;
+    return attention_workspace_floats(a);
 }
 
 hipError_t launch_attention_fused(const AttentionArgs& a, const Workspace& ws, hipStream_t s) {

@@ -123,6 +123,30 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
 hipError_t launch_attention_fused(const AttentionArgs& a, const Workspace& ws, hipStream_t s);
 uint64_t attention_workspace_floats(const AttentionArgs& a);
 
+// Decode attention over a paged KV cache (one new token per row): row b has
+// seq_lens[b] cached positions; its new K/V row is appended at position
+// seq_lens[b] and its queries attend to positions 0..seq_lens[b]. The pool is
+// [layers][num_pages][2][page_size][kv_heads][head_dim]; position j of row b
+// lives in page block_table[b * pages_per_seq + j / page_size], slot
+// j % page_size. q / out [batch, heads, 1, head_dim]; k_new / v_new
+// [batch, kv_heads, 1, head_dim]. page_size must be a multiple of 16 and the
+// shapes those of the decode kernel (else hipErrorNotSupported, nothing
+// launched). The caller checks that the table and lengths stay in range.
+struct PagedAttentionArgs {
+    const float* q;
+    const float* k_new;
+    const float* v_new;
+    float* pool;
+    float* out;
+    const uint32_t* block_table;
+    const uint32_t* seq_lens;
+    uint64_t batch, layers, layer, heads, kv_heads, head_dim;
+    uint32_t num_pages, page_size, pages_per_seq;
+    float scale;
+};
+hipError_t launch_paged_attention(const PagedAttentionArgs& p, const Workspace& ws, hipStream_t s);
+uint64_t paged_attention_workspace_floats(const PagedAttentionArgs& p);
+
 // ---- dense f32 matmul (reference/matmul.rs) ----
 // out[b] = a[b or 0] x op(b[b or 0]); op = transpose when `nt`.
 hipError_t launch_matmul(const float* a, const float* b, float* out, uint64_t batch, uint64_t batch_a,

@@ -168,6 +168,9 @@ def load_library() -> ctypes.CDLL:
                                      ctypes.POINTER(ir.CValue), ctypes.c_size_t, ctypes.POINTER(ir.CBufferRef),
                                      ctypes.POINTER(ir.CValue), ctypes.c_size_t, U32P, ctypes.c_size_t],
                                     ctypes.c_int),
+        "sl_hip_paged_attention": ([P, ctypes.POINTER(ir.COp), ctypes.POINTER(ir.CBufferRef),
+                                    ctypes.POINTER(ir.CBufferRef), ctypes.POINTER(ir.CBufferRef),
+                                    ctypes.POINTER(ir.CBufferRef), ctypes.c_uint32, ctypes.c_void_p], ctypes.c_int),
         "sl_hip_synchronize": ([P], ctypes.c_int),
         "sl_hip_last_error": ([P, ctypes.POINTER(ir.CError)], None),
         "sl_hip_bind_quantized": ([P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
@@ -300,6 +303,15 @@ class HipDevice:
         sc = _scalars(scalars)
         self._check(self._lib.sl_hip_dispatch_noalloc(self._h, ctypes.byref(c_op), in_refs, in_vals, len(inputs),
                                                       out_refs, out_vals, len(outputs), sc, len(scalars)))
+
+    def paged_attention(self, op: ir.Op, q: ir.BufferRef, k_new: ir.BufferRef, v_new: ir.BufferRef,
+                        out: ir.BufferRef, batch: int, paged_kv) -> None:
+        """sl_hip_paged_attention (starlight_amd.paged): decode attention
+        over a paged KV cache, one new token per row at its own length."""
+        c_op = op.to_c()
+        refs = [r.to_c() for r in (q, k_new, v_new, out)]
+        self._check(self._lib.sl_hip_paged_attention(self._h, ctypes.byref(c_op), *[ctypes.byref(r) for r in refs],
+                                                      batch, ctypes.addressof(paged_kv)))
 
     def synchronize(self) -> None:
         self._check(self._lib.sl_hip_synchronize(self._h))

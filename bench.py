@@ -20,6 +20,14 @@ The JSON line also carries
                  WRITE_SIZE (scaled by the same counters on a plain copy),
                  read from the committed summary when present;
   rmsnorm      — RMSNorm over [4096 x 4096] f32, the same way;
+  read_floor   — the plainest full-chip read (libstarlight_probe.so) of the
+                 roofline q-GEMV's bytes, one graph-replayed launch each
+                 over 16 regions (gemv; kernel_of_floor = floor time / the
+                 q-GEMV's time), and of one decode step's weights as the
+                 129-launch chain of reads the fused step makes, 4 GB of
+                 distinct regions (decode_step; tok_s is the decode rate
+                 such a chain alone allows, decode_of_floor = its time / the
+                 measured step);
   cpu_baseline — the C oracle (scalar restatement of backend-cpu) on the
                  host: one 8B-shaped layer decoding at 1024 cached positions
                  plus a slice of lm_head, extrapolated to a full token.
@@ -221,6 +229,81 @@ def qgemv_roofline(dev, n=14336, k=4096, copies=16, launches=200, graphs=True, m
             "bytes_per_launch": algorithmic, "avg_launch_us": round(avg_us, 3)}
 
 
+def load_probe():
+    """libstarlight_probe.so: read-floor measurements (not the device path)."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "starlight_amd", "lib", "libstarlight_probe.so"))
+    vp, u32, u64 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64
+    lib.slp_read_floor.argtypes = [vp, u64, u64, u32, u32, vp, vp, ctypes.POINTER(ctypes.c_float)]
+    lib.slp_read_floor.restype = ctypes.c_int
+    lib.slp_read_sequence.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(u64), u32, vp, vp,
+                                      ctypes.POINTER(ctypes.c_float)]
+    lib.slp_read_sequence.restype = ctypes.c_int
+    return lib
+
+
+def decode_read_launches(cfg):
+    """Bytes of the weight reads of one decode step, one entry per launch
+    the fused step makes: per layer q/k/v, o, the gate/up pair and down
+    (codes + scales), then lm_head."""
+    from starlight_amd.graph import weight_specs
+    from starlight_amd.ir import QuantFormat
+
+    def nbytes(spec):
+        n, k = spec.shape
+        if not spec.quantized:
+            return n * k * 4
+        return n * k // (2 if cfg.quant == QuantFormat.INT4 else 1) + n * (k // cfg.group) * 4
+
+    specs = {s.name: s for s in weight_specs(cfg)}
+    out = []
+    for l in range(cfg.layers):
+        p = f"layers.{l}."
+        out += [sum(nbytes(specs[p + r]) for r in ("attn.q", "attn.k", "attn.v")), nbytes(specs[p + "attn.o"]),
+                nbytes(specs[p + "mlp.gate"]) + nbytes(specs[p + "mlp.up"]), nbytes(specs[p + "mlp.down"])]
+    return out + [nbytes(specs["lm_head"])]
+
+
+def read_floors(dev, gemv_bytes, step_launches, copies=16, launches=200):
+    """The plainest full-chip read (libstarlight_probe.so) of the roofline
+    q-GEMV's bytes, one graph-replayed launch each over `copies` regions
+    (no MALL reuse), and of one decode step's weights as the chain of reads
+    the fused step launches (distinct regions, 4 GB for the 8B shape)."""
+    import torch
+
+    lib = load_probe()
+    sink = torch.zeros(2048, dtype=torch.int32, device="cuda")
+    stride = (gemv_bytes + 4095) // 4096 * 4096
+    buf = torch.empty(stride * copies, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    us = ctypes.c_float()
+    rc = lib.slp_read_floor(buf.data_ptr(), gemv_bytes, stride, copies, launches, sink.data_ptr(), dev.stream,
+                            ctypes.byref(us))
+    if rc != 0:
+        raise RuntimeError(f"slp_read_floor failed: hipError {rc}")
+    one = {"bytes": gemv_bytes, "avg_launch_us": round(us.value, 3),
+           "achieved": round(gemv_bytes / (us.value * 1e-6) / 1e9, 1), "unit": "GB/s",
+           "frac": round(gemv_bytes / (us.value * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del buf
+    offsets, total = [], 0
+    for b in step_launches:
+        offsets.append(total)
+        total += (b + 4095) // 4096 * 4096
+    big = torch.empty(total, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    n = len(step_launches)
+    ptrs = (ctypes.c_void_p * n)(*[big.data_ptr() + o for o in offsets])
+    sizes = (ctypes.c_uint64 * n)(*step_launches)
+    rc = lib.slp_read_sequence(ptrs, sizes, n, sink.data_ptr(), dev.stream, ctypes.byref(us))
+    if rc != 0:
+        raise RuntimeError(f"slp_read_sequence failed: hipError {rc}")
+    del big
+    step_bytes = sum(step_launches)
+    step = {"launches": n, "bytes": step_bytes, "us": round(us.value, 1),
+            "frac": round(step_bytes / (us.value * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "tok_s": round(1e6 / us.value, 1)}
+    return one, step
+
+
 def rmsnorm_roofline(dev, rows=4096, hidden=4096, copies=4, launches=40):
     """RMSNorm over [rows x hidden] f32 with weight ~N(1, 0.1), rotating
     input/output copies, graph-replayed and timed with HIP events."""
@@ -415,15 +498,17 @@ def cpu_baseline(cfg, prompt_len=PROMPT_LEN, label="8B", budget_s=25.0):
                               (rng.standard_normal(spec.shape, dtype=np.float32) * np.float32(0.02)))
     oracle.set_threads(1)  # the reference is single-threaded
     bufs = engine.upload_weights(dev, one, weights)
-    pre = graph.lower_llama(one, 1, 1, prompt_len + 8)
+    max_steps = 128
+    pre = graph.lower_llama(one, 1, 1, prompt_len + max_steps)
     eng = engine.Engine(dev, engine.compile_program(pre, bufs), engine.compile_program(pre, bufs), 1,
-                        prompt_len + 8)
+                        prompt_len + max_steps)
     kv = eng.states[pre.kv_cache]
     dev.f32[kv][:] = rng.uniform(-1, 1, dev.f32[kv].size).astype(np.float32)
     logits = np.zeros(8, np.float32)
     t0 = time.perf_counter()
     steps = 0
-    while steps < 3 and time.perf_counter() - t0 < budget_s * 0.6:
+    # decode steps of the layer for about 40% of the budget (at least 3)
+    while steps < max_steps and (steps < 3 or time.perf_counter() - t0 < budget_s * 0.4):
         eng.step(eng.DECODE, [1], [prompt_len + steps], 1, prompt_len + steps, logits)
         steps += 1
     per_layer = (time.perf_counter() - t0) / steps
@@ -548,6 +633,10 @@ def main():
     log(f"q-GEMV roofline: {roof}")
     norm = rmsnorm_roofline(dev)
     log(f"RMSNorm: {norm}")
+    gemv_floor, step_floor = read_floors(dev, roof["bytes_per_launch"], decode_read_launches(cfg))
+    gemv_floor["kernel_of_floor"] = round(gemv_floor["avg_launch_us"] / roof["avg_launch_us"], 4)
+    step_floor["decode_of_floor"] = round(step_floor["us"] / (ms_per_step * 1000.0), 4)
+    log(f"read floors: q-GEMV bytes {gemv_floor}; decode step weights {step_floor}")
     cpu = None if args.no_cpu or B > 1 else cpu_baseline(cfg, prompt_len, label)
     if cpu:
         log(f"cpu baseline: {cpu}")
@@ -577,6 +666,7 @@ def main():
         "prefill_tok_s": round(B * prompt_len / prefill_s, 1),
         "roofline": roof,
         "rmsnorm": norm,
+        "read_floor": {"gemv": gemv_floor, "decode_step": step_floor},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

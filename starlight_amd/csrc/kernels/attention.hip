@@ -18,9 +18,9 @@
 //    fused). One partial (m, l, acc) per block; the merge kernel combines P.
 //  * attn_split / attn_merge — other decode shapes: one wave per
 //    (b, h, t, key chunk), score by wave reduction, then a merge kernel.
-//  * attn_tiled — prefill: a block owns 64 queries of one head, two threads
-//    per query (each half of head_dim), and streams 32-key K/V tiles through
-//    LDS, so each K/V row read from L2 serves 64 queries.
+//  * attn_prefill — prefill (16 or more queries, head_dim 64 or 128): a block
+//    owns 64 queries of one head and streams 32-key K/V tiles through LDS;
+//    both products run on the f32 matrix cores.
 #include "common.h"
 #include "kernels.h"
 #include "starlight_hip.h"
@@ -679,101 +679,145 @@ __global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
     if (g.mirror != nullptr) reinterpret_cast<float4*>(g.mirror + mrow * (4 * D4))[c] = a;
 }
 
-constexpr int kTileQ = 64;  // queries per block
-constexpr int kTileK = 32;  // keys per LDS tile
+// ---- prefill: the f32 matrix cores ----
+//
+// A block of 4 waves owns 64 queries of one head (wave w: queries 16 w ..
+// 16 w + 15 of the block's range) and streams the keys 32 at a time. Each
+// tile of K and V rows goes to LDS (row stride D + 4 floats, so a wave's
+// 16-byte K reads and 4-byte V reads hit 64 distinct banks) while the next
+// tile's rows wait in registers. Per tile a wave forms S^T = K Q^T (keys x
+// its 16 queries) and O^T += V^T P^T (dims x queries) with
+// v_mfma_f32_16x16x4_f32: f32 products and f32 sums, like the VALU form.
+// The accumulator layout puts rows 4 (l / 16) + i, column l % 16 in lane l,
+// so every value a lane holds of S^T and O^T belongs to query l % 16: the
+// online-softmax state (m, l) is per lane, a query's reductions span lanes
+// l % 16 + 16 r (two lane swaps), and P^T is S^T's registers used as the B
+// operand of the second product (the keys of its step i are 4 (l / 16) + i).
+// The reduction over d is taken in a permuted order, the same for both
+// operands: of each 16 dims, step s takes d = 4 (l / 16) + s, so a lane's
+// operands of four steps are one float4 of K in LDS and of Q in registers.
+// Blocks run the longest key ranges first (query tiles in reverse order).
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+constexpr int kPfQ = 64;  // queries per block
+constexpr int kPfK = 32;  // keys per tile
 
 template <int D>
-__global__ __launch_bounds__(128) void attn_tiled(Geo g) {
-    prefetch_kernarg<arg_bytes<Geo>()>();
-    constexpr int H = D / 2;  // dims per thread
-    __shared__ float4 ks[kTileK * D / 4];
-    __shared__ float4 vs[kTileK * D / 4];
+__global__ __launch_bounds__(256) void attn_prefill(Geo g, uint32_t qtiles) {
+    prefetch_kernarg<arg_bytes<Geo, uint32_t>()>();
+    constexpr int LS = D + 4;                // LDS row stride (floats)
+    constexpr int D16 = D / 16;              // float4 of Q per lane, and 16-dim output tiles
+    constexpr int F4 = kPfK * D / 4 / 256;   // float4 of K (and of V) per thread per tile
+    __shared__ __align__(16) float ks[kPfK * LS];
+    __shared__ __align__(16) float vs[kPfK * LS];
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int c = lane % 16, kk = lane / 16;
+    const uint32_t qt = qtiles - 1 - blockIdx.x;
     const uint32_t h = blockIdx.y;
     const uint64_t b = blockIdx.z;
     const uint32_t kvh = h / g.group;
-    const int r = threadIdx.x / 2, half = threadIdx.x % 2;
-    const uint32_t t = blockIdx.x * kTileQ + r;
-    const bool valid = t < g.seq;
     const uint32_t past = past_of(g);
-    const uint32_t key_count = past + t + 1;
-    const uint32_t last_t = min(g.seq, (blockIdx.x + 1) * kTileQ) - 1;
-    const uint32_t block_keys = past + last_t + 1;
+    const uint32_t q0 = qt * kPfQ + wave * 16;  // the wave's first query
+    const uint32_t t = q0 + c;                  // this lane's query
+    const uint32_t tq = min(t, g.seq - 1);      // lanes past the end compute on the last query, unstored
+    const uint32_t block_keys = past + min(g.seq, (qt + 1) * kPfQ);
+    const uint32_t wave_keys = q0 < g.seq ? past + min(g.seq - 1, q0 + 15) + 1 : 0;
+    const uint32_t my_keys = past + t + 1;
 
-    const uint64_t qrow = ((b * g.heads + h) * g.seq + (valid ? t : 0)) * D + half * H;
-    float qv[H], acc[H];
+    float4 qv[D16];
+    const float4* qrow = reinterpret_cast<const float4*>(g.q + ((b * g.heads + h) * g.seq + tq) * D);
 #pragma unroll
-    for (int i = 0; i < H; i += 4) {
-        float4 v4 = *reinterpret_cast<const float4*>(g.q + qrow + i);
-        qv[i] = v4.x; qv[i + 1] = v4.y; qv[i + 2] = v4.z; qv[i + 3] = v4.w;
-        acc[i] = acc[i + 1] = acc[i + 2] = acc[i + 3] = 0.f;
-    }
+    for (int j = 0; j < D16; ++j) qv[j] = qrow[4 * j + kk];
+    v4f_t o[D16];
+#pragma unroll
+    for (int j = 0; j < D16; ++j) o[j] = v4f_t{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, lsum = 0.f;
+
     const uint64_t time_stride = static_cast<uint64_t>(g.kv_heads) * D;
     const float* kbase = g.cache + b * g.batch_stride + g.layer_offset + kvh * D;
     const float* vbase = kbase + g.parity_stride;
-    float m = -INFINITY, l = 0.f;
-
-    for (uint32_t kt = 0; kt < block_keys; kt += kTileK) {
-        __syncthreads();
-        for (int e = threadIdx.x; e < kTileK * D / 4; e += 128) {
-            const uint32_t row = e / (D / 4), col = e % (D / 4);
-            const uint32_t j = kt + row;
-            float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
-            if (j < block_keys) {
-                kk = reinterpret_cast<const float4*>(kbase + j * time_stride)[col];
-                vv = reinterpret_cast<const float4*>(vbase + j * time_stride)[col];
-            }
-            ks[e] = kk;
-            vs[e] = vv;
+    float4 kn[F4], vn[F4];
+    // rows past the block's keys re-read its last key (their scores are masked)
+    auto load = [&](uint32_t kt) {
+#pragma unroll
+        for (int u = 0; u < F4; ++u) {
+            const uint32_t e = tid + 256 * u, row = e / (D / 4), col = e % (D / 4);
+            const uint64_t j = min(kt + row, block_keys - 1);
+            kn[u] = reinterpret_cast<const float4*>(kbase + j * time_stride)[col];
+            vn[u] = reinterpret_cast<const float4*>(vbase + j * time_stride)[col];
+        }
+    };
+    load(0);
+    for (uint32_t kt = 0; kt < block_keys; kt += kPfK) {
+        __syncthreads();  // every wave is done reading the previous tile
+#pragma unroll
+        for (int u = 0; u < F4; ++u) {
+            const uint32_t e = tid + 256 * u, row = e / (D / 4), col = e % (D / 4);
+            *reinterpret_cast<float4*>(ks + row * LS + 4 * col) = kn[u];
+            *reinterpret_cast<float4*>(vs + row * LS + 4 * col) = vn[u];
         }
         __syncthreads();
-        float s[kTileK];
-        float tile_max = -INFINITY;
+        if (kt + kPfK < block_keys) load(kt + kPfK);
+        if (kt >= wave_keys) continue;  // wave-uniform: no key of the tile is visible to the wave
+        // S^T: keys 16 sub + 4 kk + i of the tile, query c
+        v4f_t st[2];
 #pragma unroll
-        for (int jj = 0; jj < kTileK; ++jj) {
-            const float4* kr = ks + jj * (D / 4) + half * (H / 4);
-            float part = 0.f;
+        for (int sub = 0; sub < 2; ++sub) {
+            st[sub] = v4f_t{0.f, 0.f, 0.f, 0.f};
+            const float* krow = ks + (sub * 16 + c) * LS + 4 * kk;
 #pragma unroll
-            for (int i = 0; i < H / 4; ++i) {
-                const float4 k4 = kr[i];
-                part = fmaf(qv[4 * i], k4.x, part);
-                part = fmaf(qv[4 * i + 1], k4.y, part);
-                part = fmaf(qv[4 * i + 2], k4.z, part);
-                part = fmaf(qv[4 * i + 3], k4.w, part);
+            for (int j = 0; j < D16; ++j) {
+                const float4 k4 = *reinterpret_cast<const float4*>(krow + 16 * j);
+                st[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qv[j].x, st[sub], 0, 0, 0);
+                st[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qv[j].y, st[sub], 0, 0, 0);
+                st[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qv[j].z, st[sub], 0, 0, 0);
+                st[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qv[j].w, st[sub], 0, 0, 0);
             }
-            part += __shfl_xor(part, 1, kWave);
-            const bool vis = kt + jj < key_count;
-            s[jj] = vis ? part * g.scale : -INFINITY;
-            tile_max = fmaxf(tile_max, s[jj]);
         }
-        if (tile_max == -INFINITY) continue;  // every key of this tile is masked for this query
-        const float m_new = fmaxf(m, tile_max);
+        float p[2][4];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t key = kt + 16 * sub + 4 * kk + i;
+                p[sub][i] = key < my_keys ? st[sub][i] * g.scale : -INFINITY;
+                tmax = fmaxf(tmax, p[sub][i]);
+            }
+        tmax = fmaxf(tmax, lane_xor16(tmax));
+        tmax = fmaxf(tmax, lane_xor32(tmax));
+        // key 0 is visible to every query, so m is finite from the first tile on
+        const float m_new = fmaxf(m, tmax);
         const float corr = expf(m - m_new);
-        l *= corr;
+        float psum = 0.f;
 #pragma unroll
-        for (int i = 0; i < H; ++i) acc[i] *= corr;
+        for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int jj = 0; jj < kTileK; ++jj) {
-            const float p = expf(s[jj] - m_new);
-            l += p;
-            const float4* vr = vs + jj * (D / 4) + half * (H / 4);
-#pragma unroll
-            for (int i = 0; i < H / 4; ++i) {
-                const float4 v4 = vr[i];
-                acc[4 * i] = fmaf(p, v4.x, acc[4 * i]);
-                acc[4 * i + 1] = fmaf(p, v4.y, acc[4 * i + 1]);
-                acc[4 * i + 2] = fmaf(p, v4.z, acc[4 * i + 2]);
-                acc[4 * i + 3] = fmaf(p, v4.w, acc[4 * i + 3]);
+            for (int i = 0; i < 4; ++i) {
+                p[sub][i] = expf(p[sub][i] - m_new);
+                psum += p[sub][i];
             }
-        }
+        psum += lane_xor16(psum);
+        psum += lane_xor32(psum);
+        lsum = lsum * corr + psum;
         m = m_new;
-    }
-    if (!valid) return;
-    const float inv = 1.0f / l;
-    float* orow = g.out + ((b * g.heads + h) * g.seq + t) * D + half * H;
+        // O^T += V^T P^T: dims 16 j + c (A), keys 16 sub + 4 kk + i (k), query c (B)
 #pragma unroll
-    for (int i = 0; i < H; i += 4)
-        *reinterpret_cast<float4*>(orow + i) =
-            make_float4(acc[i] * inv, acc[i + 1] * inv, acc[i + 2] * inv, acc[i + 3] * inv);
+        for (int j = 0; j < D16; ++j) {
+            o[j] *= corr;
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vs[(16 * sub + 4 * kk + i) * LS + 16 * j + c],
+                                                                 p[sub][i], o[j], 0, 0, 0);
+        }
+    }
+    if (t >= g.seq) return;
+    const float inv = 1.0f / lsum;
+    float* orow = g.out + ((b * g.heads + h) * g.seq + t) * D + 4 * kk;
+#pragma unroll
+    for (int j = 0; j < D16; ++j)
+        *reinterpret_cast<float4*>(orow + 16 * j) = make_float4(o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv);
 }
 
 }  // namespace
@@ -931,9 +975,10 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
     if (e != hipSuccess) return e;
     const bool aligned = aligned16(a.q) && aligned16(a.cache) && aligned16(a.out);
     if (a.seq >= 16 && aligned && (a.head_dim == 64 || a.head_dim == 128)) {
-        dim3 grid(static_cast<unsigned>((a.seq + kTileQ - 1) / kTileQ), g.heads, static_cast<unsigned>(a.batch));
-        if (a.head_dim == 64) attn_tiled<64><<<grid, 128, 0, s>>>(g);
-        else attn_tiled<128><<<grid, 128, 0, s>>>(g);
+        const uint32_t qtiles = static_cast<uint32_t>((a.seq + kPfQ - 1) / kPfQ);
+        dim3 grid(qtiles, g.heads, static_cast<unsigned>(a.batch));
+        if (a.head_dim == 64) attn_prefill<64><<<grid, 256, 0, s>>>(g, qtiles);
+        else attn_prefill<128><<<grid, 256, 0, s>>>(g, qtiles);
         return hipGetLastError();
     }
     if (a.head_dim > 256) return hipErrorInvalidValue;

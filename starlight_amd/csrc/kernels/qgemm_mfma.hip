@@ -95,7 +95,7 @@ __device__ __forceinline__ _Float16 nib(uint32_t word, int shift) {
 }
 
 template <int BITS>
-__global__ __launch_bounds__(256) void qgemm_mfma(GemmArgs p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(GemmArgs p) {
     prefetch_kernarg<arg_bytes<GemmArgs>()>();
     __shared__ __align__(16) _Float16 as[2][2][kTile][kRowPad];  // [stage][hi, lo][row][k]
     __shared__ __align__(16) _Float16 bs[2][kTile][kRowPad];     // [stage][column][k]
@@ -178,16 +178,19 @@ __global__ __launch_bounds__(256) void qgemm_mfma(GemmArgs p) {
     for (int j = 0; j < 4; ++j) scol[j] = min(n0 + 64 * wn + 16 * j + lane % 16, p.n - 1);
     float sv[4];
 
-    // Stages go global -> registers -> LDS through a ring of four register
-    // slots: the loads of stage st + 4 are issued at step st, three steps of
-    // MFMA work before their LDS store (one step is about 500 cycles, short
-    // of a memory round trip). steps (k / 32) is a multiple of 4.
-    StageRegs r0 = load_stage(0), r1 = load_stage(1), r2 = load_stage(2), r3 = load_stage(3);
+    // Stages go global -> registers -> LDS through two register slots: the
+    // loads of stage st + 2 are issued at step st and stored to LDS at the
+    // end of step st + 1. Two slots keep the kernel within 256 registers, so
+    // two blocks share each CU (their LDS, 60 KB each, fits twice) and one
+    // block's MFMA work covers the other's loads, conversions and barriers:
+    // [14336 x 4096] at M = 512 took 288 us with four slots and one block per
+    // CU, 200 us so. steps (k / 32) is a multiple of 4.
+    StageRegs r0 = load_stage(0), r1 = load_stage(1);
     store_stage(0, r0);
     __syncthreads();
     auto step = [&](uint32_t st, StageRegs mine, StageRegs next) -> StageRegs {
         const int buf = st & 1;
-        if (st + 4 < steps) mine = load_stage(st + 4);  // this slot's stage is in LDS already
+        if (st + 2 < steps) mine = load_stage(st + 2);  // this slot's stage is in LDS already
         if (st % group_steps == 0) {
             const uint32_t g = st / group_steps;
 #pragma unroll
@@ -223,11 +226,9 @@ __global__ __launch_bounds__(256) void qgemm_mfma(GemmArgs p) {
         __syncthreads();
         return mine;
     };
-    for (uint32_t st = 0; st < steps; st += 4) {
+    for (uint32_t st = 0; st < steps; st += 2) {
         r0 = step(st, r0, r1);
-        r1 = step(st + 1, r1, r2);
-        r2 = step(st + 2, r2, r3);
-        r3 = step(st + 3, r3, r0);
+        r1 = step(st + 1, r1, r0);
     }
 
     // lane holds rows 4 (lane / 16) + e of each row tile, column lane % 16

@@ -464,8 +464,23 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
             }
         }
         if (used == 1) return 0;
-        const hipError_t e = launch_qgemv_fused(f, d->stream);
-        if (e == hipErrorNotSupported) return 0;
+        hipError_t e = launch_qgemv_fused(f, d->stream);
+        if (e == hipErrorNotSupported) {
+            // Many rows (prefill): the norm on its own, then the projections
+            // as one q-GEMM launch over the normed rows (one activation
+            // split for all of them). A residual Add stays a command of its
+            // own, so only plain units qualify.
+            const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
+            const float* a = norm ? fptr(d, norm->out) : f.a;
+            if (f.epilogue != kFusedPlain || !qgemm_mfma_takes(a, f.w, cnt, rows, ws)) return 0;
+            used = (j - i) + cnt;
+            if (norm) {
+                e = launch_rms_norm(f.a, f.gamma, f.normed, rows, k, f.eps, d->stream);
+                if (e == hipSuccess) e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream);
+            } else {
+                e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream);
+            }
+        }
         *err = e;
         d->stats.fused_commands += used;
         return used;

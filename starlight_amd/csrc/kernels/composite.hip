@@ -44,10 +44,19 @@ hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef&
         if (e == hipSuccess) return launch_linear(g, down, out, rows, hidden, inter, rest, s);
         if (e != hipErrorNotSupported) return e;
     }
+    const QuantWeight* gate_up[2] = {&gate.quant, &up.quant};
+    float* gu_out[2] = {g, u};
     for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
         const uint64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
-        hipError_t e = launch_linear(x + r0 * hidden, gate, g, rc, inter, hidden, rest, s);
-        if (e == hipSuccess) e = launch_linear(x + r0 * hidden, up, u, rc, inter, hidden, rest, s);
+        const float* xr = x + r0 * hidden;
+        hipError_t e;
+        if (gate.quantized() && up.quantized() && rc > 16 && qgemm_mfma_takes(xr, gate_up, 2, rc, rest)) {
+            // many rows: gate and up in one launch over one activation split
+            e = launch_qgemm_multi(xr, gate_up, gu_out, 2, rc, rest, s);
+        } else {
+            e = launch_linear(xr, gate, g, rc, inter, hidden, rest, s);
+            if (e == hipSuccess) e = launch_linear(xr, up, u, rc, inter, hidden, rest, s);
+        }
         if (e == hipSuccess) e = launch_silu_mul(g, u, g, rc * inter, s);
         if (e == hipSuccess) e = launch_linear(g, down, out + r0 * hidden, rc, hidden, inter, rest, s);
         if (e != hipSuccess) return e;

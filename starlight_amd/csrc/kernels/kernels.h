@@ -183,6 +183,12 @@ hipError_t launch_scale_repack(const float* scales, float* tile_scales, uint64_t
 // shape or the workspace does not fit (nothing launched).
 hipError_t launch_qgemm_mfma(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
                              hipStream_t s);
+// The same for up to three weights of equal k, group and format that read
+// the same activations (one activation split, one launch): out[i] =
+// a * dequant(w[i])^T. qgemm_mfma_takes says whether a launch would run.
+bool qgemm_mfma_takes(const float* a, const QuantWeight* const* w, uint32_t nseg, uint64_t m, const Workspace& ws);
+hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float* const* out, uint32_t nseg,
+                              uint64_t m, const Workspace& ws, hipStream_t s);
 hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
                           hipStream_t s);
 // The MFMA decode path (m <= 16, Mfma layout); returns hipErrorNotSupported

@@ -34,7 +34,7 @@ namespace {
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kTile = 128;     // output rows and columns per block
+constexpr int kTile = 128;     // output columns per block (rows: BM, 128 or 64)
 constexpr int kStepK = 32;     // k per MFMA step and per LDS stage
 constexpr int kRowPad = 40;    // halves per LDS row: 80 bytes, conflict-free 16-byte lane reads
 constexpr int kExpBias = 15;   // scaled rows stay below 2^15
@@ -79,14 +79,22 @@ struct StageRegs {
     uint4 h0, l0, h1, l1, b;
 };
 
+// One weight of a launch: its column blocks are block0 .. the next
+// segment's block0 (up to three weights reading the same activations, such
+// as q/k/v, run as one launch).
+struct GemmSeg {
+    const uint8_t* tiles;   // Mfma layout
+    const float* scales;    // [n, k / group], row-major
+    float* out;             // [m, n]
+    uint32_t n, block0;
+};
+
 struct GemmArgs {
     const _Float16* ahi;
     const _Float16* alo;
     const int* row_exp;
-    const uint8_t* tiles;   // Mfma layout
-    const float* scales;    // [n, k / group], row-major
-    float* out;             // [m, n]
-    uint32_t m, n, k, group, groups, sb_total, n_tiles;
+    GemmSeg seg[kFusedMaxSegs];
+    uint32_t nseg, m, k, group, groups, sb_total;
 };
 
 // A signed nibble (two's complement) of byte b, bit offset 0 or 4, as fp16.
@@ -94,25 +102,38 @@ __device__ __forceinline__ _Float16 nib(uint32_t word, int shift) {
     return static_cast<_Float16>(static_cast<int>(word << (28 - shift)) >> 28);
 }
 
-template <int BITS>
+template <int BITS, int BM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(GemmArgs p) {
+    static_assert(BM == 128 || BM == 64, "block rows");
+    constexpr int MT = BM / 32;  // 16-row tiles per wave (a wave owns BM / 2 rows)
     prefetch_kernarg<arg_bytes<GemmArgs>()>();
-    __shared__ __align__(16) _Float16 as[2][2][kTile][kRowPad];  // [stage][hi, lo][row][k]
+    __shared__ __align__(16) _Float16 as[2][2][BM][kRowPad];      // [stage][hi, lo][row][k]
     __shared__ __align__(16) _Float16 bs[2][kTile][kRowPad];     // [stage][column][k]
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const int wm = wave / 2, wn = wave % 2;
-    const uint32_t m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+    // this block's weight, chosen with selects (block-uniform, in scalar
+    // registers; a runtime index into the arguments would be a memory load)
+    const uint32_t bx = blockIdx.x;
+    const uint32_t si = (p.nseg > 1 && bx >= p.seg[1].block0 ? 1u : 0u) + (p.nseg > 2 && bx >= p.seg[2].block0 ? 1u : 0u);
+#define SL_GSEG(f) (si == 0 ? p.seg[0].f : si == 1 ? p.seg[1].f : p.seg[2].f)
+    const uint8_t* const tiles = SL_GSEG(tiles);
+    const float* const scales = SL_GSEG(scales);
+    float* const out = SL_GSEG(out);
+    const uint32_t n = SL_GSEG(n), n_tiles = (n + 15) / 16;
+    const uint32_t m0 = blockIdx.y * BM, n0 = (bx - SL_GSEG(block0)) * kTile;
+#undef SL_GSEG
     const uint32_t steps = p.k / kStepK, group_steps = p.group / kStepK;
 
-    // This thread's share of a stage: two 16-byte chunks of each of hi and
-    // lo (row c / 4, halves 8 (c % 4) ..), and one 32-lane slice of a
+    // This thread's share of a stage: one 16-byte chunk of each of hi and lo
+    // per 64 rows of the block (row c / 4, halves 8 (c % 4) ..), and one
+    // 32-lane slice of a
     // weight tile (tile tid / 32, lane within the slice tid % 32).
     // (plain variables, not arrays: an array the lambdas capture would be
     // placed in LDS by the compiler)
     const uint32_t c0 = tid, c1 = tid + 256;
     const uint64_t aoff0 = static_cast<uint64_t>(min(m0 + c0 / 4, p.m - 1)) * p.k + 8 * (c0 % 4);
     const uint64_t aoff1 = static_cast<uint64_t>(min(m0 + c1 / 4, p.m - 1)) * p.k + 8 * (c1 % 4);
-    const uint32_t bt = min(n0 / 16 + tid / 32, p.n_tiles - 1), bi = tid % 32;
+    const uint32_t bt = min(n0 / 16 + tid / 32, n_tiles - 1), bi = tid % 32;
     // (slots travel by value: a slot passed by reference would be placed in
     // LDS by the compiler)
     auto load_stage = [&](uint32_t st) -> StageRegs {
@@ -120,16 +141,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
         const uint32_t k0 = st * kStepK;
         r.h0 = *reinterpret_cast<const uint4*>(p.ahi + aoff0 + k0);
         r.l0 = *reinterpret_cast<const uint4*>(p.alo + aoff0 + k0);
-        r.h1 = *reinterpret_cast<const uint4*>(p.ahi + aoff1 + k0);
-        r.l1 = *reinterpret_cast<const uint4*>(p.alo + aoff1 + k0);
+        if constexpr (BM == 128) {
+            r.h1 = *reinterpret_cast<const uint4*>(p.ahi + aoff1 + k0);
+            r.l1 = *reinterpret_cast<const uint4*>(p.alo + aoff1 + k0);
+        }
         const uint32_t sb = k0 / 128, t = (k0 % 128) / kStepK, s = t / 2;
         const uint32_t L = (2 * (t % 2) + bi / 16) * 16 + bi % 16;
         const uint64_t tile = static_cast<uint64_t>(bt) * p.sb_total + sb;
         if constexpr (BITS == 4) {
-            const uint2 w = *reinterpret_cast<const uint2*>(p.tiles + tile * 1024 + L * 16 + s * 8);
+            const uint2 w = *reinterpret_cast<const uint2*>(tiles + tile * 1024 + L * 16 + s * 8);
             r.b = make_uint4(w.x, w.y, 0u, 0u);
         } else {
-            r.b = *reinterpret_cast<const uint4*>(p.tiles + tile * 2048 + s * 1024 + L * 16);
+            r.b = *reinterpret_cast<const uint4*>(tiles + tile * 2048 + s * 1024 + L * 16);
         }
         return r;
     };
@@ -137,8 +160,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
         const uint4 rb = r.b;
         *reinterpret_cast<uint4*>(&as[buf][0][c0 / 4][8 * (c0 % 4)]) = r.h0;
         *reinterpret_cast<uint4*>(&as[buf][1][c0 / 4][8 * (c0 % 4)]) = r.l0;
-        *reinterpret_cast<uint4*>(&as[buf][0][c1 / 4][8 * (c1 % 4)]) = r.h1;
-        *reinterpret_cast<uint4*>(&as[buf][1][c1 / 4][8 * (c1 % 4)]) = r.l1;
+        if constexpr (BM == 128) {
+            *reinterpret_cast<uint4*>(&as[buf][0][c1 / 4][8 * (c1 % 4)]) = r.h1;
+            *reinterpret_cast<uint4*>(&as[buf][1][c1 / 4][8 * (c1 % 4)]) = r.l1;
+        }
         // 16 codes of column (tid / 32) * 16 + bi % 16, k 16 (bi / 16) .. + 15
         v8h q0, q1;
         if constexpr (BITS == 4) {
@@ -164,9 +189,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
         *reinterpret_cast<v8h*>(dst + 8) = q1;
     };
 
-    v4f acc[4][4], tmp[4][4];
+    v4f acc[MT][4], tmp[MT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -175,7 +200,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     // the scale column of this lane in each of the wave's 4 column tiles
     uint32_t scol[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) scol[j] = min(n0 + 64 * wn + 16 * j + lane % 16, p.n - 1);
+    for (int j = 0; j < 4; ++j) scol[j] = min(n0 + 64 * wn + 16 * j + lane % 16, n - 1);
     float sv[4];
 
     // Stages go global -> registers -> LDS through two register slots: the
@@ -194,18 +219,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
         if (st % group_steps == 0) {
             const uint32_t g = st / group_steps;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sv[j] = p.scales[static_cast<uint64_t>(scol[j]) * p.groups + g];
+            for (int j = 0; j < 4; ++j) sv[j] = scales[static_cast<uint64_t>(scol[j]) * p.groups + g];
         }
-        // operands: A rows 64 wm + 16 i + lane % 16, B columns 64 wn + 16 j + lane % 16,
+        // operands: A rows (BM / 2) wm + 16 i + lane % 16, B columns 64 wn + 16 j + lane % 16,
         // k 8 (lane / 16) .. + 7 of the step
         const int kq = 8 * (lane / 16);
         v8h bq[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) bq[j] = *reinterpret_cast<const v8h*>(&bs[buf][64 * wn + 16 * j + lane % 16][kq]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const v8h ah = *reinterpret_cast<const v8h*>(&as[buf][0][64 * wm + 16 * i + lane % 16][kq]);
-            const v8h al = *reinterpret_cast<const v8h*>(&as[buf][1][64 * wm + 16 * i + lane % 16][kq]);
+        for (int i = 0; i < MT; ++i) {
+            const v8h ah = *reinterpret_cast<const v8h*>(&as[buf][0][(BM / 2) * wm + 16 * i + lane % 16][kq]);
+            const v8h al = *reinterpret_cast<const v8h*>(&as[buf][1][(BM / 2) * wm + 16 * i + lane % 16][kq]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[j], tmp[i][j], 0, 0, 0);
@@ -214,7 +239,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
         }
         if (st % group_steps == group_steps - 1) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MT; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -233,55 +258,98 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
 
     // lane holds rows 4 (lane / 16) + e of each row tile, column lane % 16
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint32_t row = m0 + 64 * wm + 16 * i + 4 * (lane / 16) + e;
+            const uint32_t row = m0 + (BM / 2) * wm + 16 * i + 4 * (lane / 16) + e;
             if (row >= p.m) continue;
             const int sh = p.row_exp[row] - kExpBias;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t col = n0 + 64 * wn + 16 * j + lane % 16;
-                if (col < p.n) p.out[static_cast<uint64_t>(row) * p.n + col] = ldexpf(acc[i][j][e], sh);
+                if (col < n) out[static_cast<uint64_t>(row) * n + col] = ldexpf(acc[i][j][e], sh);
             }
         }
 }
 
 }  // namespace
 
-hipError_t launch_qgemm_mfma(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
-                             hipStream_t s) {
-    if (w.layout != QuantLayout::Mfma || w.k % 128 != 0 || w.group % kStepK != 0 || w.k % w.group != 0 ||
-        !aligned16(a) || m == 0 || m > 0xffffffffull || w.n > 0xffffffffull || w.k > 0xffffffffull)
-        return hipErrorNotSupported;
-    // workspace: hi and lo (fp16, m x k each), then the row exponents
-    const uint64_t half_floats = (m * w.k + 1) / 2;  // one array of m * k halves, in floats
-    const uint64_t hi_at = 0, lo_at = (half_floats + 63) / 64 * 64, exp_at = lo_at + (half_floats + 63) / 64 * 64;
-    if (exp_at + m > ws.floats) return hipErrorNotSupported;
-    _Float16* hi = reinterpret_cast<_Float16*>(ws.data + hi_at);
-    _Float16* lo = reinterpret_cast<_Float16*>(ws.data + lo_at);
-    int* row_exp = reinterpret_cast<int*>(ws.data + exp_at);
-    split_rows<<<static_cast<unsigned>(m), 256, 0, s>>>(a, hi, lo, row_exp, static_cast<uint32_t>(w.k));
+namespace {
+
+// hi and lo (fp16, m x k each), then the row exponents, in the workspace
+struct SplitLayout {
+    uint64_t lo_at, exp_at, floats;
+};
+SplitLayout split_layout(uint64_t m, uint64_t k) {
+    const uint64_t half_floats = (m * k + 1) / 2;  // one array of m * k halves, in floats
+    const uint64_t lo_at = (half_floats + 63) / 64 * 64, exp_at = lo_at + (half_floats + 63) / 64 * 64;
+    return {lo_at, exp_at, exp_at + m};
+}
+
+}  // namespace
+
+bool qgemm_mfma_takes(const float* a, const QuantWeight* const* w, uint32_t nseg, uint64_t m, const Workspace& ws) {
+    if (nseg == 0 || nseg > kFusedMaxSegs || !aligned16(a) || m == 0 || m > 0xffffffffull) return false;
+    const QuantWeight& w0 = *w[0];
+    uint64_t blocks = 0;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        const QuantWeight& x = *w[i];
+        if (x.layout != QuantLayout::Mfma || x.k != w0.k || x.group != w0.group || x.format != w0.format ||
+            x.k % 128 != 0 || x.group % kStepK != 0 || x.k % x.group != 0 || x.n > 0xffffffffull ||
+            x.k > 0xffffffffull || x.tiles == nullptr)
+            return false;
+        blocks += (x.n + kTile - 1) / kTile;
+    }
+    return blocks <= 0xffffffffull && split_layout(m, w0.k).floats <= ws.floats;
+}
+
+hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float* const* out, uint32_t nseg,
+                              uint64_t m, const Workspace& ws, hipStream_t s) {
+    if (!qgemm_mfma_takes(a, w, nseg, m, ws)) return hipErrorNotSupported;
+    const QuantWeight& w0 = *w[0];
+    const SplitLayout lay = split_layout(m, w0.k);
+    _Float16* hi = reinterpret_cast<_Float16*>(ws.data);
+    _Float16* lo = reinterpret_cast<_Float16*>(ws.data + lay.lo_at);
+    int* row_exp = reinterpret_cast<int*>(ws.data + lay.exp_at);
+    split_rows<<<static_cast<unsigned>(m), 256, 0, s>>>(a, hi, lo, row_exp, static_cast<uint32_t>(w0.k));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    GemmArgs p;
+    GemmArgs p{};
     p.ahi = hi;
     p.alo = lo;
     p.row_exp = row_exp;
-    p.tiles = w.tiles;
-    p.scales = w.scales;
-    p.out = out;
+    uint32_t blocks = 0;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        p.seg[i] = GemmSeg{w[i]->tiles, w[i]->scales, out[i], static_cast<uint32_t>(w[i]->n), blocks};
+        blocks += static_cast<uint32_t>((w[i]->n + kTile - 1) / kTile);
+    }
+    p.nseg = nseg;
     p.m = static_cast<uint32_t>(m);
-    p.n = static_cast<uint32_t>(w.n);
-    p.k = static_cast<uint32_t>(w.k);
-    p.group = w.group;
-    p.groups = static_cast<uint32_t>(w.k / w.group);
-    p.sb_total = static_cast<uint32_t>(w.k / 128);
-    p.n_tiles = static_cast<uint32_t>((w.n + 15) / 16);
-    const dim3 grid(static_cast<unsigned>((w.n + kTile - 1) / kTile), static_cast<unsigned>((m + kTile - 1) / kTile));
-    if (w.format == SL_QFORMAT_INT4) qgemm_mfma<4><<<grid, 256, 0, s>>>(p);
-    else qgemm_mfma<8><<<grid, 256, 0, s>>>(p);
+    p.k = static_cast<uint32_t>(w0.k);
+    p.group = w0.group;
+    p.groups = static_cast<uint32_t>(w0.k / w0.group);
+    p.sb_total = static_cast<uint32_t>(w0.k / 128);
+    // 128-row blocks, or 64-row ones (three per CU, each with less operand
+    // reuse) when 128-row blocks would not give every CU one. Measured on
+    // MI355X: M = 1024 [4096 x 4096] (256 blocks of 128 rows) runs faster in
+    // 64-row blocks; M = 512 [14336 x 4096] (448) runs slower (200 -> 250 us).
+    const bool rows64 = static_cast<uint64_t>(blocks) * ((m + 127) / 128) <= compute_units();
+    const dim3 grid(blocks, static_cast<unsigned>(rows64 ? (m + 63) / 64 : (m + 127) / 128));
+    if (w0.format == SL_QFORMAT_INT4) {
+        if (rows64) qgemm_mfma<4, 64><<<grid, 256, 0, s>>>(p);
+        else qgemm_mfma<4, 128><<<grid, 256, 0, s>>>(p);
+    } else {
+        if (rows64) qgemm_mfma<8, 64><<<grid, 256, 0, s>>>(p);
+        else qgemm_mfma<8, 128><<<grid, 256, 0, s>>>(p);
+    }
     return hipGetLastError();
+}
+
+hipError_t launch_qgemm_mfma(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
+                             hipStream_t s) {
+    const QuantWeight* ws1[1] = {&w};
+    float* outs[1] = {out};
+    return launch_qgemm_multi(a, ws1, outs, 1, m, ws, s);
 }
 
 }  // namespace slhip

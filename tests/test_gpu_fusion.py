@@ -442,3 +442,58 @@ def test_gemv_residual_add_fusions(hip, variant):
         assert_normwise(got[NORMED.offset:NORMED.offset + k], resid_want)
     else:
         assert fused == 2  # MatMulNT (or SwiGlu) + Add
+
+
+@pytest.mark.parametrize("fmt_name", ["INT4", "INT8"])
+def test_prefill_norm_and_projections_run_as_one_gemm(hip, fmt_name):
+    """RmsNorm and three quantized MatMulNT reading its output, at 64 rows
+    (prefill): the norm runs on its own, then q/k/v as one q-GEMM launch over
+    one activation split. Every output — the norm's and each projection's —
+    matches the oracle (norm per element at 1e-6, projections normwise per
+    row at 1e-4), and the unit counts as fused; a SwiGlu at 64 rows (gate
+    and up in one launch) matches too."""
+    from starlight_amd import quant
+    from starlight_amd.ir import QuantFormat
+
+    fmt = QuantFormat[fmt_name]
+    r = np.random.default_rng(120 + len(fmt_name))
+    rows, k, nq, nkv, inter = 64, 512, 512, 128, 384
+    x = r.standard_normal((rows, k)).astype(np.float32)
+    gamma = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+
+    def qw(n, cols):
+        w = (r.standard_normal((n, cols)) * 0.05).astype(np.float32)
+        words, scales = quant.quantize(w, 128, fmt)
+        wb, sb = hip.upload_new_u32(words), hip.upload_new_f32(scales)
+        hip.bind_quantized(wb, sb, fmt, 128, n, cols)
+        return (BufferRef(wb, 0, words.size), Value.quantized([n, cols], fmt, 128),
+                quant.dequantize(words, scales, n, cols, 128, fmt))
+
+    wq, wk, wv = qw(nq, k), qw(nkv, k), qw(nkv, k)
+    X = BufferRef(hip.upload_new_f32(x.ravel()), 0, rows * k)
+    G = BufferRef(hip.upload_new_f32(gamma), 0, k)
+    N = BufferRef(hip.allocate_f32(rows * k, 256), 0, rows * k)
+    outs = {name: BufferRef(hip.allocate_f32(rows * n, 256), 0, rows * n) for name, n in
+            (("q", nq), ("k", nkv), ("v", nkv))}
+    xv = Value.f32([1, rows, k])
+    before = hip.stats()
+    hip.dispatch(Op.rms_norm(1e-5), [X, G], [xv, Value.f32([k], ValueRole.PARAM)], [N], [xv])
+    for name, w, n in (("q", wq, nq), ("k", wk, nkv), ("v", wv, nkv)):
+        hip.dispatch(Op.matmul_nt(), [N, w[0]], [xv, w[1]], [outs[name]], [Value.f32([1, rows, n])])
+    hip.synchronize()
+    assert hip.stats()["fused_commands"] - before["fused_commands"] == 4
+    normed = oracle.rms_norm(x.ravel(), gamma, rows, k, 1e-5)
+    assert_elementwise(hip.read_f32(N.buffer, rows * k), normed)
+    for name, w, n in (("q", wq, nq), ("k", wk, nkv), ("v", wv, nkv)):
+        got = hip.read_f32(outs[name].buffer, rows * n).reshape(rows, n)
+        want = oracle.matmul_nt(normed, w[2], 1, rows, k, n).reshape(rows, n)
+        for i in range(rows):
+            assert_normwise(got[i], want[i])
+
+    g, u, d = qw(inter, k), qw(inter, k), qw(k, inter)
+    Y = BufferRef(hip.allocate_f32(rows * k, 256), 0, rows * k)
+    hip.dispatch(Op.swiglu(), [X, g[0], u[0], d[0]], [xv, g[1], u[1], d[1]], [Y], [xv])
+    got = hip.read_f32(Y.buffer, rows * k).reshape(rows, k)
+    want = oracle.swiglu(x.ravel(), g[2], u[2], d[2], rows, k, inter).reshape(rows, k)
+    for i in range(rows):
+        assert_normwise(got[i], want[i])

@@ -74,9 +74,11 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, _
 }
 
 // One stage's share of a thread: two 16-byte chunks of each of hi and lo,
-// and the weight bytes (INT4: the first 8).
+// the weight bytes (INT4: the first 8), and the scale of column tid % 128
+// for the stage's quantization group.
 struct StageRegs {
     uint4 h0, l0, h1, l1, b;
+    float sc;
 };
 
 // One weight of a launch: its column blocks are block0 .. the next
@@ -109,6 +111,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     prefetch_kernarg<arg_bytes<GemmArgs>()>();
     __shared__ __align__(16) _Float16 as[2][2][BM][kRowPad];      // [stage][hi, lo][row][k]
     __shared__ __align__(16) _Float16 bs[2][kTile][kRowPad];     // [stage][column][k]
+    __shared__ float ss[2][kTile];                                // [stage][column]: the group's scales
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const int wm = wave / 2, wn = wave % 2;
     // this block's weight, chosen with selects (block-uniform, in scalar
@@ -134,6 +137,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     const uint64_t aoff0 = static_cast<uint64_t>(min(m0 + c0 / 4, p.m - 1)) * p.k + 8 * (c0 % 4);
     const uint64_t aoff1 = static_cast<uint64_t>(min(m0 + c1 / 4, p.m - 1)) * p.k + 8 * (c1 % 4);
     const uint32_t bt = min(n0 / 16 + tid / 32, n_tiles - 1), bi = tid % 32;
+    const uint32_t scol_ld = min(n0 + tid % kTile, n - 1);  // the scale this thread stages
     // (slots travel by value: a slot passed by reference would be placed in
     // LDS by the compiler)
     auto load_stage = [&](uint32_t st) -> StageRegs {
@@ -145,6 +149,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
             r.h1 = *reinterpret_cast<const uint4*>(p.ahi + aoff1 + k0);
             r.l1 = *reinterpret_cast<const uint4*>(p.alo + aoff1 + k0);
         }
+        r.sc = scales[static_cast<uint64_t>(scol_ld) * p.groups + k0 / p.group];
         const uint32_t sb = k0 / 128, t = (k0 % 128) / kStepK, s = t / 2;
         const uint32_t L = (2 * (t % 2) + bi / 16) * 16 + bi % 16;
         const uint64_t tile = static_cast<uint64_t>(bt) * p.sb_total + sb;
@@ -158,6 +163,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     };
     auto store_stage = [&](int buf, StageRegs r) {
         const uint4 rb = r.b;
+        if (tid < kTile) ss[buf][tid] = r.sc;
         *reinterpret_cast<uint4*>(&as[buf][0][c0 / 4][8 * (c0 % 4)]) = r.h0;
         *reinterpret_cast<uint4*>(&as[buf][1][c0 / 4][8 * (c0 % 4)]) = r.l0;
         if constexpr (BM == 128) {
@@ -197,11 +203,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
             acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
             tmp[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
         }
-    // the scale column of this lane in each of the wave's 4 column tiles
-    uint32_t scol[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) scol[j] = min(n0 + 64 * wn + 16 * j + lane % 16, n - 1);
-    float sv[4];
 
     // Stages go global -> registers -> LDS through two register slots: the
     // loads of stage st + 2 are issued at step st and stored to LDS at the
@@ -215,12 +216,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     __syncthreads();
     auto step = [&](uint32_t st, StageRegs mine, StageRegs next) -> StageRegs {
         const int buf = st & 1;
-        if (st + 2 < steps) mine = load_stage(st + 2);  // this slot's stage is in LDS already
-        if (st % group_steps == 0) {
-            const uint32_t g = st / group_steps;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sv[j] = scales[static_cast<uint64_t>(scol[j]) * p.groups + g];
-        }
+        // this slot's stage is in LDS already; past the end the last stage
+        // is loaded again, so every step issues the same loads and the
+        // compiler's waits stay exact (a conditional load makes it wait for
+        // every outstanding one where the paths join)
+        mine = load_stage(min(st + 2, steps - 1));
         // operands: A rows (BM / 2) wm + 16 i + lane % 16, B columns 64 wn + 16 j + lane % 16,
         // k 8 (lane / 16) .. + 7 of the step
         const int kq = 8 * (lane / 16);
@@ -238,6 +238,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
             }
         }
         if (st % group_steps == group_steps - 1) {
+            // the group's scales, staged with this step's operands
+            float sv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sv[j] = ss[buf][64 * wn + 16 * j + lane % 16];
 #pragma unroll
             for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -247,7 +251,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
                     tmp[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
                 }
         }
-        if (st + 1 < steps) store_stage(buf ^ 1, next);
+        store_stage(buf ^ 1, next);  // after the last step: into a buffer nothing reads
         __syncthreads();
         return mine;
     };

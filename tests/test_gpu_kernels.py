@@ -227,6 +227,9 @@ ATT_SHAPES = [
     (1, 1, 0, 16, 1, 1, 50, 128, 64),       # 16 query rows per KV head, head_dim 128
     (1, 1, 0, 4, 2, 1, 77, 192, 100),       # head_dim 192
     (2, 1, 0, 8, 2, 3, 40, 64, 64),         # three-token chunk through the decode kernel
+    (2, 1, 0, 8, 8, 16, 3, 128, 32),        # prefill kernel: batch 2, MHA, 16 queries after a prefix
+    (1, 1, 0, 16, 2, 65, 0, 64, 80),        # prefill kernel: 8 query heads per KV head, a 1-query tail tile
+    (1, 1, 0, 32, 8, 1024, 0, 128, 1024),   # prefill kernel at the 8B shape, 1024 tokens
 ]
 
 

@@ -431,7 +431,25 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
                     // Rope of a new key row before it is used and appended
                     constexpr uint32_t D = 4 * D4;
                     const float* st = sc + (j - past) * D;
-                    if (g.rope_variant == SL_ROPE_NEOX) {
+                    if (g.rope_variant == SL_ROPE_NEOX && DV == 1) {
+                        // head_dim 64: the pair of dim d < 32 is d + 32, four
+                        // float4 further, in lane li ^ 8 of the same 16-lane
+                        // group (DPP row rotate by 8); each lane keeps its
+                        // half of rotate()'s result
+                        float4& me = kv[kb][0];
+                        const float4 pa = make_float4(dpp_f<kDppRowRor8>(me.x), dpp_f<kDppRowRor8>(me.y),
+                                                      dpp_f<kDppRowRor8>(me.z), dpp_f<kDppRowRor8>(me.w));
+                        const bool first = li < 8;
+                        const uint32_t pr = 4 * (li & 7);  // pair index of the lane's first dim
+                        const float mine[4] = {me.x, me.y, me.z, me.w}, other[4] = {pa.x, pa.y, pa.z, pa.w};
+                        float res[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float sine = st[pr + e], cosine = st[D / 2 + pr + e];
+                            res[e] = first ? mine[e] * cosine - other[e] * sine : other[e] * sine + mine[e] * cosine;
+                        }
+                        me = make_float4(res[0], res[1], res[2], res[3]);
+                    } else if (g.rope_variant == SL_ROPE_NEOX) {
 #pragma unroll
                         for (int u = 0; u < DV / 2; ++u) {  // pairs (d, d + D/2) sit in one lane
                             const uint32_t d = 4 * li + 64 * u;
@@ -877,7 +895,7 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
     if (!(rows <= kDecodeMaxRows && a.head_dim % 64 == 0 && dv >= 1 && dv <= 4 && rt * dv <= 32 && aligned &&
           a.batch * a.kv_heads * parts * rows * (kDecodePartStride + a.head_dim) <= ws.floats))
         return hipErrorNotSupported;
-    if (fused && (a.positions == nullptr || (a.rope_variant == SL_ROPE_NEOX && dv % 2 != 0) ||
+    if (fused && (a.positions == nullptr || (a.rope_variant == SL_ROPE_NEOX && dv % 2 != 0 && dv != 1) ||
                   a.rope_variant > SL_ROPE_GPTJ))
         return hipErrorNotSupported;
     g.chunks = static_cast<uint32_t>(parts);

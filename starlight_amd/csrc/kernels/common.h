@@ -26,6 +26,7 @@ constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
 constexpr int kDppHalfMirror = 0x141;
 constexpr int kDppMirror = 0x140;
+constexpr int kDppRowRor8 = 0x128;  // row_ror:8, lane i of a 16-lane row takes lane (i + 8) % 16
 
 __device__ __forceinline__ float row_sum(float v) {
     v += dpp_f<kDppXor1>(v);

@@ -29,6 +29,8 @@ CASES = [
     (2, 16, 4, 1, 300, 128, 512, RopeVariant.GPTJ),
     (1, 8, 2, 2, 40, 64, 64, RopeVariant.GPTJ),         # two-token chunk, head_dim 64
     (1, 4, 4, 1, 0, 128, 16, RopeVariant.NEOX),         # first token
+    (1, 32, 8, 1, 300, 64, 512, RopeVariant.NEOX),      # 1B-shaped decode step: head_dim 64, NeoX pairs across lanes
+    (2, 8, 2, 3, 20, 64, 64, RopeVariant.NEOX),         # head_dim 64 NeoX, three-token chunk, batch 2
 ]
 
 
@@ -135,15 +137,15 @@ def run_group(hip, case, consume_intermediate, keep_all=False):
 def test_attention_group_fuses_and_matches(hip, case):
     fused = run_group(hip, case, consume_intermediate=False)
     B, H, Hkv, S, past, D, max_seq, variant = case
-    if variant == RopeVariant.NEOX and (D // 64) % 2:
-        assert fused == 0  # NEOX pairs of head_dim 64 span lanes: not fused
+    if not fusable(case):
+        assert fused == 0  # NEOX pairs of head_dim 192 span lanes and float4 slots: not fused
     else:
         assert fused >= 7
 
 
 def fusable(case):
     B, H, Hkv, S, past, D, max_seq, variant = case
-    return not (variant == RopeVariant.NEOX and (D // 64) % 2)
+    return not (variant == RopeVariant.NEOX and D // 64 == 3)
 
 
 @pytest.mark.parametrize("case", CASES[:2])

@@ -876,8 +876,20 @@ Geo make_geo(const AttentionArgs& a, const Workspace& ws) {
     return g;
 }
 
+// Partials per (row, KV head): one per 128 positions of max_seq, at most
+// kMergeMaxParts, and no more than keep the grid near kDecodeGridBlocks
+// blocks. Each block's share is latency-bound (one or two 16-key tiles per
+// wave), so a batch of many sequences is better served by fewer, longer
+// partials than by rounds of short blocks (8B, batch 8: 2,022 tok/s at 512
+// blocks, 2,006 at 1024, 1,946 with 32 partials as at batch 1). Shapes only:
+// the grid never depends on past_len.
+constexpr uint64_t kDecodeGridBlocks = 512;
 uint64_t decode_parts(const AttentionArgs& a) {
     uint64_t parts = (a.max_seq + 127) / 128;
+    const uint64_t rows = a.batch * a.kv_heads;
+    const uint64_t by_grid = rows ? (kDecodeGridBlocks + rows - 1) / rows : 1;
+    if (parts > by_grid) parts = by_grid;
+    if (parts < 1) parts = 1;
     return parts > kMergeMaxParts ? kMergeMaxParts : parts;
 }
 

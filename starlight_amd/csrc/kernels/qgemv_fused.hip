@@ -265,13 +265,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         uint64_t o;
         if (out_at(tid, si, o)) res_src = SEG_PICK(s_res, si) + o;
     }
-#ifndef SL_PF0
-#define SL_PF0 PF
-#endif
-    constexpr int PF0 = SL_PF0 < PF ? SL_PF0 : PF;
     Item<BITS> win[PF];
 #pragma unroll
-    for (int i = 0; i < PF0; ++i) fetch(win[i], i);
+    for (int i = 0; i < PF; ++i) fetch(win[i], i);
     const float res0 = *global_ptr(res_src);
 #pragma unroll
     for (int u = 0; u < F4; ++u)
@@ -378,8 +374,6 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     }
     __syncthreads();
 
-#pragma unroll
-    for (int i = PF0; i < PF; ++i) fetch(win[i], i);
     // ---- main loop over the stream ----
     const uint32_t kb4 = lane / 16;
     // A-operand row of this lane: with LR row 4 * m + limb (limb 3 repeats
@@ -579,11 +573,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     // Waves per block: 16 for long k (the down projection, k = 14336), which
     // doubles the weight loads in flight per CU and halves each thread's
     // share of the activation prologue; 8 otherwise.
-#ifndef SL_GEMV_WAVES
     const int waves = p.k >= 8192 || p.m * p.k > max_elems(8) ? 16 : 8;
-#else
-    const int waves = SL_GEMV_WAVES;
-#endif
     const uint32_t threads = static_cast<uint32_t>(waves) * kWave;
     const uint32_t wpt = f.epilogue == kFusedPair ? waves / 2 : waves;
     const uint32_t sb_per_group = p.group >= 128 ? p.group / 128 : 1;

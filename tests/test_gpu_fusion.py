@@ -499,3 +499,41 @@ def test_prefill_norm_and_projections_run_as_one_gemm(hip, fmt_name):
     want = oracle.swiglu(x.ravel(), g[2], u[2], d[2], rows, k, inter).reshape(rows, k)
     for i in range(rows):
         assert_normwise(got[i], want[i])
+
+
+@pytest.mark.parametrize("fmt_name,residual", [("INT4", True), ("INT4", False), ("INT8", True)])
+def test_long_k_gemv_with_many_rows(hip, fmt_name, residual):
+    """A quantized MatMulNT with 8 rows of k = 14336 (the down projection at
+    batch 8) has more activations than the fused GEMV's LDS holds, so it
+    runs on the split-k GEMV and its reduction, and a residual Add after it
+    runs as its own command. The product matches the oracle per row
+    (normwise 1e-4); the Add's output is exactly residual + the product."""
+    from starlight_amd import quant
+    from starlight_amd.ir import QuantFormat
+
+    fmt = QuantFormat[fmt_name]
+    r = np.random.default_rng(140 + residual + len(fmt_name))
+    m, k, n = 8, 14336, 512
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    words, scales = quant.quantize(w, 128, fmt)
+    wb, sb = hip.upload_new_u32(words), hip.upload_new_f32(scales)
+    hip.bind_quantized(wb, sb, fmt, 128, n, k)
+    deq = quant.dequantize(words, scales, n, k, 128, fmt)
+    resid = r.standard_normal(m * n).astype(np.float32)
+    X = BufferRef(hip.upload_new_f32(x.ravel()), 0, m * k)
+    Y = BufferRef(hip.allocate_f32(m * n, 256), 0, m * n)
+    R = BufferRef(hip.upload_new_f32(resid), 0, m * n)
+    Z = BufferRef(hip.allocate_f32(m * n, 256), 0, m * n)
+    yv = Value.f32([1, m, n])
+    hip.dispatch(Op.matmul_nt(), [X, BufferRef(wb, 0, words.size)], [Value.f32([1, m, k]),
+                 Value.quantized([n, k], fmt, 128)], [Y], [yv])
+    if residual:
+        hip.dispatch(Op.add(), [R, Y], [yv, yv], [Z], [yv])
+    hip.synchronize()
+    got = hip.read_f32(Y.buffer, m * n).reshape(m, n)
+    want = oracle.matmul_nt(x.ravel(), deq, 1, m, k, n).reshape(m, n)
+    for i in range(m):
+        assert_normwise(got[i], want[i])
+    if residual:
+        np.testing.assert_array_equal(hip.read_f32(Z.buffer, m * n), resid + got.ravel())

@@ -421,6 +421,8 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
     const size_t n_reads = 3;
     QgemvFused f{};
     f.a = fptr(d, a_ref);
+    f.partial = d->workspace;  // the unit uses no other workspace
+    f.partial_floats = d->workspace_floats;
     if (norm) {
         f.gamma = fptr(d, norm->in[1]);
         f.normed = fptr(d, norm->out);
@@ -521,6 +523,8 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
         g.nseg = 1;
         g.m = rows;
         g.epilogue = kFusedPlain;
+        g.partial = d->workspace + d->workspace_floats / 2;  // past h
+        g.partial_floats = d->workspace_floats / 2;
         // The down kernel reads only h (the workspace), the weights and, per
         // element, the residual: nothing another block could overwrite.
         if (j + 1 < n) {

@@ -218,6 +218,11 @@ struct QgemvFused {
     uint32_t nseg;
     uint64_t m;
     uint32_t epilogue;
+    // scratch for the k-slice partial sums of a single weight whose m x k
+    // activations exceed the kernel's LDS (the down projection at batch 8),
+    // or null: such a shape is then not taken
+    float* partial = nullptr;
+    uint64_t partial_floats = 0;
 };
 hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s);
 

@@ -101,6 +101,7 @@ struct Args {
     uint32_t epilogue;
 };
 
+
 // One weight superblock of a wave's stream: codes (16 bytes per lane, INT8
 // two loads) and the scales of its groups for the lane's row.
 template <int BITS>
@@ -113,8 +114,15 @@ struct Item {
 // counted at run time). LR (m <= 4): the three limbs of every activation row
 // share one MFMA as its A rows 4 * m + limb, so a 64-k step is one LDS read
 // and one MFMA; otherwise (m <= 16) each limb matrix is an MFMA of its own.
-template <int BITS, int NT, int SPG, bool LR, int F4, int W>
+// SLICED: k is cut into gridDim.y slices of p.k columns; slice y = blockIdx.y
+// reads columns [y p.k, (y + 1) p.k) of activation rows gridDim.y p.k / 4
+// float4 apart, superblocks y p.sb_total .. of tiles holding gridDim.y
+// p.sb_total, and writes its partial sums m n floats after slice y - 1's
+// (the launcher adds the slices up). Every slice geometry follows from the
+// grid, so the arguments are the same as for one slice.
+template <int BITS, int NT, int SPG, bool LR, int F4, int W, bool SLICED>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(Args p) {
+    prefetch_kernarg<arg_bytes<Args>()>();
     constexpr int kThreads = W * kWave, kWaves = W;
     static_assert(F4 <= kMaxF4, "activations per thread beyond the block's budget");
     constexpr int GPS = SPG == 1 ? 2 : 1;
@@ -127,10 +135,13 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     __shared__ float cfac[max_elems(W) / 256];  // per 256-element chunk: 2^(E-22)
     __shared__ float wres[2][kWaves][16][16];
 
-    prefetch_kernarg<arg_bytes<Args>()>();
     const int tid = threadIdx.x, lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, kept in scalar registers
     const uint32_t M = p.m, K = p.k, K4 = K / 4;
+    const uint32_t ks = SLICED ? blockIdx.y : 0u;  // k slice
+    const float* const a_slice = SLICED ? p.a + static_cast<uint64_t>(ks) * K : p.a;
+    const uint32_t a_stride4 = SLICED ? gridDim.y * K4 : K4;
+    const uint32_t sb_stride = SLICED ? gridDim.y * p.sb_total : p.sb_total;
     const uint32_t RS = K + kLimbPad;  // limb row stride
     float* tres = reinterpret_cast<float*>(limbs + 3 * M * RS);
 
@@ -169,7 +180,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     uint32_t s_n[kFusedMaxSegs];
 #pragma unroll
     for (uint32_t i = 0; i < kFusedMaxSegs; ++i) {
-        s_out[i] = uniform_ptr(p.seg[i].out);
+        s_out[i] = uniform_ptr(SLICED ? p.seg[i].out + static_cast<uint64_t>(ks) * M * p.seg[i].n : p.seg[i].out);
         s_out2[i] = uniform_ptr(p.seg[i].out2);
         s_res[i] = uniform_ptr(p.seg[i].resid);
         s_n[i] = __builtin_amdgcn_readfirstlane(p.seg[i].n);
@@ -199,7 +210,8 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         const uint32_t j = i / len, q = i % len;
         uint32_t tile;
         const uint32_t si = seg_of(blockIdx.x + j * gridDim.x, tile);
-        const uint64_t ts = static_cast<uint64_t>(tile) * p.sb_total + sb0 + (q < nlive ? q : (nlive ? nlive - 1 : 0));
+        const uint64_t ts = static_cast<uint64_t>(tile) * (SLICED ? sb_stride : p.sb_total) +
+                            (SLICED ? ks * p.sb_total : 0u) + sb0 + (q < nlive ? q : (nlive ? nlive - 1 : 0));
         const uint64_t w = reinterpret_cast<uint64_t>(SEG_PICK(s_tiles, si) + ts * SB_BYTES);
         const uint64_t sc = reinterpret_cast<uint64_t>(SEG_PICK(s_tsc, si) + ts * 16 * gps);
         tw_lo = static_cast<uint32_t>(w);
@@ -240,7 +252,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (kThreads * u >= total4) continue;  // block-uniform: runs past the input load nothing
         const uint32_t f = min(static_cast<uint32_t>(tid + kThreads * u), total4 - 1);
-        v[u] = reinterpret_cast<const float4*>(p.a)[f];
+        // rows of a k slice are a_stride4 float4 apart
+        const uint32_t fa = SLICED ? f + (f / K4) * (a_stride4 - K4) : f;
+        v[u] = reinterpret_cast<const float4*>(a_slice)[fa];
         if (p.gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(p.gamma)[f % K4];
     }
     // Output element e of the block's [tiles][16][m] results: its segment
@@ -533,6 +547,20 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
 }
 #undef SEG_PICK
 
+// out[i] = the sum of the k slices' partials of element i, in slice order;
+// with resid, out2[i] = resid[i] + out[i] (the residual Add's order).
+__global__ __launch_bounds__(256) void qgemv_slices_sum(const float* __restrict__ partial, uint32_t slices,
+                                                        uint64_t count, float* out, const float* resid,
+                                                        float* out2) {
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
+         i += static_cast<uint64_t>(gridDim.x) * 256) {
+        float v = partial[i];
+        for (uint32_t sl = 1; sl < slices; ++sl) v += partial[sl * count + i];
+        out[i] = v;
+        if (out2 != nullptr) out2[i] = resid[i] + v;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
@@ -540,10 +568,24 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const QuantWeight& w0 = *f.w[0];
     const uint64_t k = w0.k;
     if (w0.layout != QuantLayout::Mfma || k % 256 != 0 || w0.group % 64 != 0 || k % w0.group != 0 ||
-        !(w0.group == 64 || w0.group == 128 || w0.group % 256 == 0) || f.m * k > max_elems(16) || !aligned16(f.a) || (f.gamma != nullptr && !aligned16(f.gamma)) ||
-        (f.normed != nullptr && !aligned16(f.normed)))
+        !(w0.group == 64 || w0.group == 128 || w0.group % 256 == 0) || !aligned16(f.a) ||
+        (f.gamma != nullptr && !aligned16(f.gamma)) || (f.normed != nullptr && !aligned16(f.normed)))
         return hipErrorNotSupported;
     if (f.epilogue == kFusedPair && f.nseg != 2) return hipErrorNotSupported;
+    // Activations beyond the LDS (m x k above max_elems(16): the down
+    // projection, k = 14336, at batch 8): the grid's y dimension cuts k into
+    // slices that fit, each block converting only its slice; the slices'
+    // partial sums go to f.partial and a second launch adds them up (and
+    // the residual). Single weights without a norm prologue only.
+    uint32_t slices = 1;
+    if (f.m * k > max_elems(16)) {
+        if (f.gamma != nullptr || f.epilogue == kFusedPair || f.nseg != 1 || f.partial == nullptr)
+            return hipErrorNotSupported;
+        const uint64_t unit = w0.group > 256 ? w0.group : 256;
+        while (slices <= 16 && (k % (slices * unit) != 0 || f.m * (k / slices) > max_elems(16))) ++slices;
+        if (slices > 16 || slices * f.m * w0.n > f.partial_floats) return hipErrorNotSupported;
+    }
+    const uint64_t kc = k / slices;
     Args p;
     p.a = f.a;
     p.gamma = f.gamma;
@@ -551,12 +593,12 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     p.eps = f.eps;
     p.nseg = f.nseg;
     p.m = static_cast<uint32_t>(f.m);
-    p.k = static_cast<uint32_t>(k);
+    p.k = static_cast<uint32_t>(kc);
     p.group = w0.group;
     p.sb_total = p.k / 128;
     p.groups_total = p.k / p.group;
     p.unit = p.group < 256 ? p.group : 256;
-    p.epilogue = f.epilogue;
+    p.epilogue = slices > 1 ? kFusedPlain : f.epilogue;
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < f.nseg; ++i) {
         const QuantWeight& w = *f.w[i];
@@ -564,7 +606,8 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
             w.format != w0.format || w.n > 0xffffffffull)
             return hipErrorNotSupported;
         if (f.epilogue == kFusedPair && w.n != w0.n) return hipErrorNotSupported;
-        p.seg[i] = Seg{w.tiles, w.tile_scales, f.out[i], f.resid[i], f.out2[i], static_cast<uint32_t>(w.n), tiles};
+        p.seg[i] = Seg{w.tiles, w.tile_scales, slices > 1 ? f.partial : f.out[i], f.resid[i], f.out2[i],
+                       static_cast<uint32_t>(w.n), tiles};
         if (f.epilogue != kFusedPair) tiles += static_cast<uint32_t>((w.n + 15) / 16);
     }
     if (f.epilogue == kFusedPair) tiles = static_cast<uint32_t>((w0.n + 15) / 16);
@@ -591,7 +634,13 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const uint64_t weight_bytes = static_cast<uint64_t>(tiles) * p.sb_total * (int4 ? 1024 : 2048) * (pair ? 2 : 1);
     uint32_t blocks, per_block;
     const uint32_t per_cap = 4096 / (16 * p.m);
-    if (weight_bytes <= (24ull << 20)) {
+    if (slices > 1) {
+        // about one block per CU over all slices: each block converts its
+        // slice's activations once for several tiles
+        blocks = (compute_units() + slices - 1) / slices;
+        if (blocks > tiles) blocks = tiles;
+        per_block = (tiles + blocks - 1) / blocks;
+    } else if (weight_bytes <= (24ull << 20)) {
         blocks = tiles < compute_units() ? tiles : compute_units();
         per_block = (tiles + blocks - 1) / blocks;
     } else {
@@ -613,17 +662,32 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     // each launch, so its length shows in the launch time (about 1 us for
     // the RMSNorm prologue at 8 float4 per thread against 2).
     const uint32_t f4 = (p.m * p.k / 4 + threads - 1) / threads;
+    const dim3 grid(blocks, slices);
 #define SL_QGEMV_FUSED_F(B, T, G, L)                                                                  \
-    (waves == 16 ? (f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 16><<<blocks, threads, lds, s>>>(p)         \
-                    : f4 <= 4 ? qgemv_fused<B, T, G, L, 4, 16><<<blocks, threads, lds, s>>>(p)         \
-                              : qgemv_fused<B, T, G, L, 8, 16><<<blocks, threads, lds, s>>>(p))        \
-     : f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 8><<<blocks, threads, lds, s>>>(p)                       \
-     : f4 <= 4   ? qgemv_fused<B, T, G, L, 4, 8><<<blocks, threads, lds, s>>>(p)                       \
-                 : qgemv_fused<B, T, G, L, 8, 8><<<blocks, threads, lds, s>>>(p))
+    (waves == 16 ? (f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 16, false><<<grid, threads, lds, s>>>(p)         \
+                    : f4 <= 4 ? qgemv_fused<B, T, G, L, 4, 16, false><<<grid, threads, lds, s>>>(p)         \
+                              : qgemv_fused<B, T, G, L, 8, 16, false><<<grid, threads, lds, s>>>(p))        \
+     : f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 8, false><<<grid, threads, lds, s>>>(p)                       \
+     : f4 <= 4   ? qgemv_fused<B, T, G, L, 4, 8, false><<<grid, threads, lds, s>>>(p)                       \
+                 : qgemv_fused<B, T, G, L, 8, 8, false><<<grid, threads, lds, s>>>(p))
 #define SL_QGEMV_FUSED(B, T, G) (lr ? SL_QGEMV_FUSED_F(B, T, G, true) : SL_QGEMV_FUSED_F(B, T, G, false))
 #define SL_QGEMV_FUSED_G(B, T) \
     (spg == 1 ? SL_QGEMV_FUSED(B, T, 1) : spg == 2 ? SL_QGEMV_FUSED(B, T, 2) : SL_QGEMV_FUSED(B, T, 0))
-    if (int4) {
+    if (slices > 1) {
+        // k slices: many rows (not LR), 16 waves, 8 float4 per thread
+        if (waves != 16 || f4 > 8 || lr) return hipErrorNotSupported;
+#define SL_QGEMV_SLICED(B, G) qgemv_fused<B, 1, G, false, 8, 16, true><<<grid, threads, lds, s>>>(p)
+        if (int4) {
+            if (spg == 1) SL_QGEMV_SLICED(4, 1);
+            else if (spg == 2) SL_QGEMV_SLICED(4, 2);
+            else SL_QGEMV_SLICED(4, 0);
+        } else {
+            if (spg == 1) SL_QGEMV_SLICED(8, 1);
+            else if (spg == 2) SL_QGEMV_SLICED(8, 2);
+            else SL_QGEMV_SLICED(8, 0);
+        }
+#undef SL_QGEMV_SLICED
+    } else if (int4) {
         if (pair) SL_QGEMV_FUSED_G(4, 2);
         else SL_QGEMV_FUSED_G(4, 1);
     } else {
@@ -633,6 +697,15 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
 #undef SL_QGEMV_FUSED_G
 #undef SL_QGEMV_FUSED
 #undef SL_QGEMV_FUSED_F
+    if (slices > 1) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const uint64_t count = f.m * w0.n;
+        const bool residual = f.epilogue == kFusedResidual;
+        qgemv_slices_sum<<<grid_for(count, 256, 1024), 256, 0, s>>>(f.partial, slices, count, f.out[0],
+                                                                   residual ? f.resid[0] : nullptr,
+                                                                   residual ? f.out2[0] : nullptr);
+    }
     return hipGetLastError();
 }
 

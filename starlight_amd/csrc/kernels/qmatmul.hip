@@ -349,6 +349,8 @@ hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint
         f.nseg = 1;
         f.m = m;
         f.epilogue = kFusedPlain;
+        f.partial = ws.data;
+        f.partial_floats = ws.floats;
         hipError_t e = launch_qgemv_fused(f, s);
         if (e != hipErrorNotSupported) return e;
         e = launch_qgemv_mfma(a, w, out, m, ws, s);

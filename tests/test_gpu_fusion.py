@@ -504,10 +504,11 @@ def test_prefill_norm_and_projections_run_as_one_gemm(hip, fmt_name):
 @pytest.mark.parametrize("fmt_name,residual", [("INT4", True), ("INT4", False), ("INT8", True)])
 def test_long_k_gemv_with_many_rows(hip, fmt_name, residual):
     """A quantized MatMulNT with 8 rows of k = 14336 (the down projection at
-    batch 8) has more activations than the fused GEMV's LDS holds, so it
-    runs on the split-k GEMV and its reduction, and a residual Add after it
-    runs as its own command. The product matches the oracle per row
-    (normwise 1e-4); the Add's output is exactly residual + the product."""
+    batch 8) has more activations than the fused GEMV's LDS holds: its grid
+    cuts k into slices whose partial sums a second launch adds up, together
+    with the residual Add when one follows (fused into the unit). The
+    product matches the oracle per row (normwise 1e-4); the Add's output is
+    exactly residual + the product."""
     from starlight_amd import quant
     from starlight_amd.ir import QuantFormat
 
@@ -526,11 +527,14 @@ def test_long_k_gemv_with_many_rows(hip, fmt_name, residual):
     R = BufferRef(hip.upload_new_f32(resid), 0, m * n)
     Z = BufferRef(hip.allocate_f32(m * n, 256), 0, m * n)
     yv = Value.f32([1, m, n])
+    before = hip.stats()
     hip.dispatch(Op.matmul_nt(), [X, BufferRef(wb, 0, words.size)], [Value.f32([1, m, k]),
                  Value.quantized([n, k], fmt, 128)], [Y], [yv])
     if residual:
         hip.dispatch(Op.add(), [R, Y], [yv, yv], [Z], [yv])
     hip.synchronize()
+    if residual:
+        assert hip.stats()["fused_commands"] - before["fused_commands"] == 2
     got = hip.read_f32(Y.buffer, m * n).reshape(m, n)
     want = oracle.matmul_nt(x.ravel(), deq, 1, m, k, n).reshape(m, n)
     for i in range(m):

@@ -470,17 +470,19 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
         if (e == hipErrorNotSupported) {
             // Many rows (prefill): the norm on its own, then the projections
             // as one q-GEMM launch over the normed rows (one activation
-            // split for all of them). A residual Add stays a command of its
-            // own, so only plain units qualify.
+            // split for all of them), a residual Add in its epilogue.
             const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
             const float* a = norm ? fptr(d, norm->out) : f.a;
-            if (f.epilogue != kFusedPlain || !qgemm_mfma_takes(a, f.w, cnt, rows, ws)) return 0;
-            used = (j - i) + cnt;
+            if (!qgemm_mfma_takes(a, f.w, cnt, rows, ws)) return 0;
+            const bool residual = f.epilogue == kFusedResidual;
             if (norm) {
                 e = launch_rms_norm(f.a, f.gamma, f.normed, rows, k, f.eps, d->stream);
-                if (e == hipSuccess) e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream);
+                if (e == hipSuccess)
+                    e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream, nullptr,
+                                           residual ? f.resid : nullptr, residual ? f.out2 : nullptr);
             } else {
-                e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream);
+                e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream, nullptr,
+                                       residual ? f.resid : nullptr, residual ? f.out2 : nullptr);
             }
         }
         *err = e;
@@ -507,7 +509,30 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
         f.m = rows;
         f.epilogue = kFusedPair;
         hipError_t e = launch_qgemv_fused(f, d->stream);
-        if (e == hipErrorNotSupported) return 0;
+        if (e == hipErrorNotSupported) {
+            if (rows <= 16) return 0;
+            // Many rows (prefill): the norm on its own, then the SwiGlu
+            // composite (gate and up as one q-GEMM, silu(g) * u formed by
+            // the down projection's activation split) with the residual Add
+            // in the down projection's epilogue when one follows.
+            size_t used = (j - i) + 1;
+            const Logged* add = j + 1 < n ? &d->log[j + 1] : nullptr;
+            const int other = add ? residual_port(*add, c1.out, rows * hidden, reads, n_reads,
+                                                  norm ? &norm->out : nullptr)
+                                  : -1;
+            e = norm ? launch_rms_norm(f.a, f.gamma, f.normed, rows, hidden, f.eps, d->stream) : hipSuccess;
+            if (e == hipSuccess)
+                e = launch_swiglu(norm ? f.normed : f.a, weight_ref(d, c1.in[1], c1.plan.quant[1]),
+                                  weight_ref(d, c1.in[2], c1.plan.quant[2]), weight_ref(d, c1.in[3], c1.plan.quant[3]),
+                                  fptr(d, c1.out), rows, hidden, inter,
+                                  Workspace{d->workspace, d->workspace_floats, d->counters, kCounterWords},
+                                  d->stream, other >= 0 ? fptr(d, add->in[other]) : nullptr,
+                                  other >= 0 ? fptr(d, add->out) : nullptr);
+            if (other >= 0) ++used;
+            *err = e;
+            d->stats.fused_commands += used;
+            return used;
+        }
         if (e != hipSuccess) {
             *err = e;
             return 1;

@@ -1,9 +1,12 @@
 // Composite operators built from the primitive launchers:
-//  * SwiGlu (reference/swiglu.rs:40-84): gate and up projections, the fused
-//    silu(g)*u epilogue, then the down projection. The reference avoids an
-//    [rows, inter] temporary by accumulating rank-1 updates; on the GPU the
-//    intermediate goes to the device workspace (row chunks when it does not
-//    fit), which turns the three products into plain streaming GEMV/GEMMs.
+//  * SwiGlu (reference/swiglu.rs:40-84): gate and up projections, silu(g)*u,
+//    then the down projection. The reference avoids an [rows, inter]
+//    temporary by accumulating rank-1 updates; on the GPU the intermediates
+//    go to the device workspace (row chunks when they do not fit), which
+//    turns the three products into plain streaming GEMV/GEMMs: for a few
+//    rows the gate/up GEMV's epilogue forms h = silu(g)*u; for many rows
+//    gate and up are one q-GEMM launch and the down projection's activation
+//    split forms silu(g)*u as it reads them.
 //  * RmsNormMatMul (reference/fused.rs:41-90): the normalised rows go to the
 //    workspace, then one matmul.
 #include "common.h"
@@ -19,7 +22,7 @@ hipError_t launch_linear(const float* a, const WeightRef& w, float* out, uint64_
 
 hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up, const WeightRef& down,
                          float* out, uint64_t rows, uint64_t hidden, uint64_t inter, const Workspace& ws,
-                         hipStream_t s) {
+                         hipStream_t s, const float* resid, float* out2) {
     if (rows == 0) return hipSuccess;
     // Keep half of the workspace for the projections' own scratch.
     const uint64_t budget = ws.floats / 2;
@@ -41,7 +44,11 @@ hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef&
         f.m = rows;
         f.epilogue = kFusedPair;
         hipError_t e = launch_qgemv_fused(f, s);
-        if (e == hipSuccess) return launch_linear(g, down, out, rows, hidden, inter, rest, s);
+        if (e == hipSuccess) {
+            e = launch_linear(g, down, out, rows, hidden, inter, rest, s);
+            if (e == hipSuccess && out2 != nullptr) e = launch_add(resid, out, out2, rows * hidden, s);
+            return e;
+        }
         if (e != hipErrorNotSupported) return e;
     }
     const QuantWeight* gate_up[2] = {&gate.quant, &up.quant};
@@ -57,8 +64,22 @@ hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef&
             e = launch_linear(xr, gate, g, rc, inter, hidden, rest, s);
             if (e == hipSuccess) e = launch_linear(xr, up, u, rc, inter, hidden, rest, s);
         }
-        if (e == hipSuccess) e = launch_silu_mul(g, u, g, rc * inter, s);
-        if (e == hipSuccess) e = launch_linear(g, down, out + r0 * hidden, rc, hidden, inter, rest, s);
+        if (e != hipSuccess) return e;
+        float* const out_r = out + r0 * hidden;
+        const float* const resid_r = resid != nullptr ? resid + r0 * hidden : nullptr;
+        float* const out2_r = out2 != nullptr ? out2 + r0 * hidden : nullptr;
+        const QuantWeight* dw[1] = {&down.quant};
+        if (down.quantized() && rc > 16 && qgemm_mfma_takes(g, dw, 1, rc, rest)) {
+            // many rows: silu(g) * u formed by the down projection's
+            // activation split (no h pass), the residual in its epilogue
+            float* outs[1] = {out_r};
+            float* out2s[1] = {out2_r};
+            e = launch_qgemm_multi(g, dw, outs, 1, rc, rest, s, u, &resid_r, out2s);
+        } else {
+            e = launch_silu_mul(g, u, g, rc * inter, s);
+            if (e == hipSuccess) e = launch_linear(g, down, out_r, rc, hidden, inter, rest, s);
+            if (e == hipSuccess && out2_r != nullptr) e = launch_add(resid_r, out_r, out2_r, rc * hidden, s);
+        }
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

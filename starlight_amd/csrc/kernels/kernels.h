@@ -185,10 +185,14 @@ hipError_t launch_qgemm_mfma(const float* a, const QuantWeight& w, float* out, u
                              hipStream_t s);
 // The same for up to three weights of equal k, group and format that read
 // the same activations (one activation split, one launch): out[i] =
-// a * dequant(w[i])^T. qgemm_mfma_takes says whether a launch would run.
+// a * dequant(w[i])^T. With u, the activations are silu(a) * u (SwiGlu's
+// down projection, elementwise); with out2[i] set, also out2[i] = resid[i]
+// + out[i] (a residual Add). qgemm_mfma_takes says whether a launch would
+// run.
 bool qgemm_mfma_takes(const float* a, const QuantWeight* const* w, uint32_t nseg, uint64_t m, const Workspace& ws);
 hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float* const* out, uint32_t nseg,
-                              uint64_t m, const Workspace& ws, hipStream_t s);
+                              uint64_t m, const Workspace& ws, hipStream_t s, const float* u = nullptr,
+                              const float* const* resid = nullptr, float* const* out2 = nullptr);
 hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
                           hipStream_t s);
 // The MFMA decode path (m <= 16, Mfma layout); returns hipErrorNotSupported
@@ -235,9 +239,11 @@ struct WeightRef {
 hipError_t launch_linear(const float* a, const WeightRef& w, float* out, uint64_t rows, uint64_t n,
                          uint64_t k, const Workspace& ws, hipStream_t s);
 // SwiGlu (reference/swiglu.rs): out = (silu(x Wg^T) * (x Wu^T)) Wd^T.
+// With out2, also out2 = resid + out (a residual Add after the SwiGlu).
 hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up,
                          const WeightRef& down, float* out, uint64_t rows, uint64_t hidden,
-                         uint64_t inter, const Workspace& ws, hipStream_t s);
+                         uint64_t inter, const Workspace& ws, hipStream_t s, const float* resid = nullptr,
+                         float* out2 = nullptr);
 // gate/up epilogue: h = silu(g) * u, elementwise over n values.
 hipError_t launch_silu_mul(const float* g, const float* u, float* h, uint64_t n, hipStream_t s);
 // RmsNormMatMul (reference/fused.rs): out = rms_norm(x, weight) W^T.

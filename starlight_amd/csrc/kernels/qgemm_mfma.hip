@@ -39,18 +39,35 @@ constexpr int kStepK = 32;     // k per MFMA step and per LDS stage
 constexpr int kRowPad = 48;    // halves per LDS row: 96 bytes, 16-byte aligned (80 and 112 measured slower)
 constexpr int kExpBias = 15;   // scaled rows stay below 2^15
 
+// The activation element: a, or with a second input u (SwiGlu's down
+// projection) silu(a) * u, the elementwise kernels' formula
+// (elementwise.rs:10-12): (a * (1 / (1 + exp(-a)))) * u.
+__device__ __forceinline__ float4 act4(const float4* row, const float4* urow, uint32_t i) {
+    float4 v = row[i];
+    if (urow != nullptr) {
+        const float4 u = urow[i];
+        v.x = (v.x * (1.0f / (1.0f + expf(-v.x)))) * u.x;
+        v.y = (v.y * (1.0f / (1.0f + expf(-v.y)))) * u.y;
+        v.z = (v.z * (1.0f / (1.0f + expf(-v.z)))) * u.z;
+        v.w = (v.w * (1.0f / (1.0f + expf(-v.w)))) * u.w;
+    }
+    return v;
+}
+
 // Row r: E with max |a| < 2^E (0 for an all-zero row), then hi/lo of
-// a * 2^(15 - E). k % 4 == 0 and a row 16-byte aligned.
-__global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, _Float16* __restrict__ hi,
-                                                  _Float16* __restrict__ lo, int* __restrict__ row_exp,
-                                                  uint32_t k) {
+// a * 2^(15 - E); with u, of silu(a) * u. k % 4 == 0 and rows 16-byte
+// aligned.
+__global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, const float* __restrict__ u,
+                                                  _Float16* __restrict__ hi, _Float16* __restrict__ lo,
+                                                  int* __restrict__ row_exp, uint32_t k) {
     __shared__ float scratch[4];
     const uint64_t r = blockIdx.x;
     const float4* row = reinterpret_cast<const float4*>(a + r * k);
+    const float4* urow = u != nullptr ? reinterpret_cast<const float4*>(u + r * k) : nullptr;
     const uint32_t k4 = k / 4;
     float mx = 0.f;
     for (uint32_t i = threadIdx.x; i < k4; i += 256) {
-        const float4 v = row[i];
+        const float4 v = act4(row, urow, i);
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
     mx = block_max(mx, scratch);
@@ -59,7 +76,7 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, _
     if (threadIdx.x == 0) row_exp[r] = e;
     const int shift = kExpBias - e;
     for (uint32_t i = threadIdx.x; i < k4; i += 256) {
-        const float4 v = row[i];
+        const float4 v = act4(row, urow, i);
         const float x[4] = {ldexpf(v.x, shift), ldexpf(v.y, shift), ldexpf(v.z, shift), ldexpf(v.w, shift)};
         _Float16 h[4], l[4];
 #pragma unroll
@@ -88,6 +105,8 @@ struct GemmSeg {
     const uint8_t* tiles;   // Mfma layout
     const float* scales;    // [n, k / group], row-major
     float* out;             // [m, n]
+    const float* resid;     // with out2: out2 = resid + out (a residual Add), else null
+    float* out2;
     uint32_t n, block0;
 };
 
@@ -122,6 +141,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     const uint8_t* const tiles = SL_GSEG(tiles);
     const float* const scales = SL_GSEG(scales);
     float* const out = SL_GSEG(out);
+    const float* const resid = SL_GSEG(resid);
+    float* const out2 = SL_GSEG(out2);
     const uint32_t n = SL_GSEG(n), n_tiles = (n + 15) / 16;
     const uint32_t m0 = blockIdx.y * BM, n0 = (bx - SL_GSEG(block0)) * kTile;
 #undef SL_GSEG
@@ -271,7 +292,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t col = n0 + 64 * wn + 16 * j + lane % 16;
-                if (col < n) out[static_cast<uint64_t>(row) * n + col] = ldexpf(acc[i][j][e], sh);
+                if (col >= n) continue;
+                const uint64_t o = static_cast<uint64_t>(row) * n + col;
+                const float val = ldexpf(acc[i][j][e], sh);
+                out[o] = val;
+                if (out2 != nullptr) out2[o] = resid[o] + val;
             }
         }
 }
@@ -308,14 +333,15 @@ bool qgemm_mfma_takes(const float* a, const QuantWeight* const* w, uint32_t nseg
 }
 
 hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float* const* out, uint32_t nseg,
-                              uint64_t m, const Workspace& ws, hipStream_t s) {
+                              uint64_t m, const Workspace& ws, hipStream_t s, const float* u,
+                              const float* const* resid, float* const* out2) {
     if (!qgemm_mfma_takes(a, w, nseg, m, ws)) return hipErrorNotSupported;
     const QuantWeight& w0 = *w[0];
     const SplitLayout lay = split_layout(m, w0.k);
     _Float16* hi = reinterpret_cast<_Float16*>(ws.data);
     _Float16* lo = reinterpret_cast<_Float16*>(ws.data + lay.lo_at);
     int* row_exp = reinterpret_cast<int*>(ws.data + lay.exp_at);
-    split_rows<<<static_cast<unsigned>(m), 256, 0, s>>>(a, hi, lo, row_exp, static_cast<uint32_t>(w0.k));
+    split_rows<<<static_cast<unsigned>(m), 256, 0, s>>>(a, u, hi, lo, row_exp, static_cast<uint32_t>(w0.k));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     GemmArgs p{};
@@ -324,7 +350,9 @@ hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float
     p.row_exp = row_exp;
     uint32_t blocks = 0;
     for (uint32_t i = 0; i < nseg; ++i) {
-        p.seg[i] = GemmSeg{w[i]->tiles, w[i]->scales, out[i], static_cast<uint32_t>(w[i]->n), blocks};
+        const bool res = resid != nullptr && out2 != nullptr && out2[i] != nullptr;
+        p.seg[i] = GemmSeg{w[i]->tiles, w[i]->scales, out[i], res ? resid[i] : nullptr, res ? out2[i] : nullptr,
+                           static_cast<uint32_t>(w[i]->n), blocks};
         blocks += static_cast<uint32_t>((w[i]->n + kTile - 1) / kTile);
     }
     p.nseg = nseg;

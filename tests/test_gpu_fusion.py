@@ -541,3 +541,62 @@ def test_long_k_gemv_with_many_rows(hip, fmt_name, residual):
         assert_normwise(got[i], want[i])
     if residual:
         np.testing.assert_array_equal(hip.read_f32(Z.buffer, m * n), resid + got.ravel())
+
+
+@pytest.mark.parametrize("variant", ["matmul", "swiglu", "norm_swiglu"])
+def test_prefill_residual_add_in_the_gemm_epilogue(hip, variant):
+    """At 64 rows (prefill) a quantized MatMulNT, or a SwiGlu (after an
+    RmsNorm), followed by the residual Add runs with the Add in the q-GEMM's
+    epilogue (the SwiGlu's silu(g) * u formed by the down projection's
+    activation split). Products match the oracle per row (normwise 1e-4);
+    the Add's output is exactly residual + the product written."""
+    from starlight_amd import quant
+    from starlight_amd.ir import QuantFormat
+
+    r = np.random.default_rng(160 + len(variant))
+    rows, k, n, inter = 64, 512, 512, 1024
+    x = r.standard_normal((rows, k)).astype(np.float32)
+    resid = r.standard_normal(rows * n).astype(np.float32)
+    gamma = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+
+    def qw(nr, cols):
+        w = (r.standard_normal((nr, cols)) * 0.05).astype(np.float32)
+        words, scales = quant.quantize(w, 128, QuantFormat.INT4)
+        wb, sb = hip.upload_new_u32(words), hip.upload_new_f32(scales)
+        hip.bind_quantized(wb, sb, QuantFormat.INT4, 128, nr, cols)
+        return (BufferRef(wb, 0, words.size), Value.quantized([nr, cols], QuantFormat.INT4, 128),
+                quant.dequantize(words, scales, nr, cols, 128, QuantFormat.INT4))
+
+    X = BufferRef(hip.upload_new_f32(x.ravel()), 0, rows * k)
+    N = BufferRef(hip.allocate_f32(rows * k, 256), 0, rows * k)
+    Y = BufferRef(hip.allocate_f32(rows * n, 256), 0, rows * n)
+    R = BufferRef(hip.upload_new_f32(resid), 0, rows * n)
+    Z = BufferRef(hip.allocate_f32(rows * n, 256), 0, rows * n)
+    xv, yv = Value.f32([1, rows, k]), Value.f32([1, rows, n])
+    before = hip.stats()
+    if variant == "matmul":
+        w = qw(n, k)
+        hip.dispatch(Op.matmul_nt(), [X, w[0]], [xv, w[1]], [Y], [yv])
+        want = oracle.matmul_nt(x.ravel(), w[2], 1, rows, k, n)
+        expect_fused = 2
+    else:
+        # weights first: an upload runs what the log holds so far
+        g, u, dn = qw(inter, k), qw(inter, k), qw(n, inter)
+        G = BufferRef(hip.upload_new_f32(gamma), 0, k)
+        src = x.ravel()
+        inp = X
+        if variant == "norm_swiglu":
+            hip.dispatch(Op.rms_norm(1e-5), [X, G],
+                         [xv, Value.f32([k], ValueRole.PARAM)], [N], [xv])
+            src = oracle.rms_norm(x.ravel(), gamma, rows, k, 1e-5)
+            inp = N
+        hip.dispatch(Op.swiglu(), [inp, g[0], u[0], dn[0]], [xv, g[1], u[1], dn[1]], [Y], [yv])
+        want = oracle.swiglu(src, g[2], u[2], dn[2], rows, k, inter)
+        expect_fused = 3 if variant == "norm_swiglu" else 2
+    hip.dispatch(Op.add(), [R, Y], [yv, yv], [Z], [yv])
+    hip.synchronize()
+    assert hip.stats()["fused_commands"] - before["fused_commands"] == expect_fused
+    got = hip.read_f32(Y.buffer, rows * n).reshape(rows, n)
+    for i in range(rows):
+        assert_normwise(got[i], want.reshape(rows, n)[i])
+    np.testing.assert_array_equal(hip.read_f32(Z.buffer, rows * n), resid + got.ravel())

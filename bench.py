@@ -412,7 +412,7 @@ def micro_lines(dev):
     us = submission_us(dev, lambda: [dev.dispatch(Op.rope(RopeVariant.NEOX, 500000.0),
                                                   [BufferRef(xs[i % 4], 0, nx), BufferRef(pos, 0, seq)], [xv, pv],
                                                   [BufferRef(ys[i % 4], 0, nx)], [xv]) for i in range(20)]) / 20
-    lines.append(hbm_line("rope_kernel (RoPE [1,32,4096,128] NeoX)", 2 * nx * 4 + seq * 4, us))
+    lines.append(hbm_line("rope_vec4 (RoPE [1,32,4096,128] NeoX)", 2 * nx * 4 + seq * 4, us))
     dev.synchronize()
 
     lines.append(rmsnorm_roofline(dev))

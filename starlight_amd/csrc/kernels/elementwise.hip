@@ -57,9 +57,13 @@ __global__ __launch_bounds__(256) void ew_scalar(const float* __restrict__ a, co
     }
 }
 
-// 256 CUs x 8 resident blocks of 256 threads keeps every CU busy; larger
-// tensors loop inside the kernel.
+// The scalar form: 256 CUs x 8 resident blocks of 256 threads keeps every CU
+// busy; larger tensors loop inside the kernel. The vector form gives each
+// thread one float4 up to 2^28 of them (a 4096 x 14336 Add: 118 us, 5.95
+// TB/s on MI355X, against 125 us with the grid capped at 2048 blocks and
+// each thread looping); the loop covers anything larger.
 constexpr unsigned kGridCap = 256 * 8;
+constexpr unsigned kVecGridCap = 1u << 20;
 
 template <Ew OP>
 hipError_t launch_ew(const float* a, const float* b, float* out, uint64_t n, float factor, hipStream_t s) {
@@ -68,7 +72,7 @@ hipError_t launch_ew(const float* a, const float* b, float* out, uint64_t n, flo
     uint64_t done = 0;
     if (vec && n >= 4) {
         const uint64_t n4 = n / 4;
-        ew_vec4<OP><<<grid_for(n4, 256, kGridCap), 256, 0, s>>>(
+        ew_vec4<OP><<<grid_for(n4, 256, kVecGridCap), 256, 0, s>>>(
             reinterpret_cast<const float4*>(a), reinterpret_cast<const float4*>(b),
             reinterpret_cast<float4*>(out), n4, factor);
         done = n4 * 4;

@@ -137,7 +137,7 @@ def test_softmax_causal_parity(hip, rows, seq, past):
 @pytest.mark.parametrize("batch,heads,seq,hd,theta,rank3", [
     (1, 1, 1, 2, 10_000.0, False), (2, 3, 5, 4, 10_000.0, False), (2, 2, 4, 8, 500_000.0, False),
     (1, 2, 3, 10, 1_000_000.0, False), (1, 32, 512, 128, 500_000.0, False), (2, 1, 17, 64, 10_000.0, True),
-    (1, 8, 3, 128, 500_000.0, False)])
+    (1, 8, 3, 128, 500_000.0, False), (1, 1, 2, 128, 500_000.0, False), (1, 40, 2, 256, 10_000.0, False)])
 def test_rope_parity(hip, variant, batch, heads, seq, hd, theta, rank3):
     r = rng(batch * 100 + seq)
     x = r.uniform(-2, 2, batch * heads * seq * hd).astype(np.float32)

@@ -450,41 +450,52 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
             f.out[cnt] = fptr(d, c.out);
             ++cnt;
         }
-        if (cnt == 0 || (cnt == 1 && !norm && j + 1 >= n)) return 0;
+        if (cnt == 0) return 0;
         size_t used = (j - i) + cnt;
         f.nseg = cnt;
         f.m = rows;
         f.epilogue = kFusedPlain;
-        if (cnt == 1 && j + 1 < n) {
-            const Logged& a = d->log[j + 1];
-            const int other = residual_port(a, outs[0], rows * w[0].n, reads, n_reads, norm ? &norm->out : nullptr);
+        const Logged* add = cnt == 1 && j + 1 < n ? &d->log[j + 1] : nullptr;
+        const uint64_t count = rows * w[0].n;
+        auto set_residual = [&](int other) {
+            f.epilogue = other >= 0 ? kFusedResidual : kFusedPlain;
             if (other >= 0) {
-                f.epilogue = kFusedResidual;
-                f.resid[0] = fptr(d, a.in[other]);
-                f.out2[0] = fptr(d, a.out);
-                ++used;
+                f.resid[0] = fptr(d, add->in[other]);
+                f.out2[0] = fptr(d, add->out);
             }
+        };
+        // Few rows: one fused GEMV launch, whose blocks read the activations
+        // (and block 0 writes the norm output) while others write results.
+        const int other = add ? residual_port(*add, outs[0], count, reads, n_reads, norm ? &norm->out : nullptr) : -1;
+        hipError_t e = hipErrorNotSupported;
+        if (used + (other >= 0 ? 1 : 0) > 1) {
+            set_residual(other);
+            e = launch_qgemv_fused(f, d->stream);
         }
-        if (used == 1) return 0;
-        hipError_t e = launch_qgemv_fused(f, d->stream);
-        if (e == hipErrorNotSupported) {
-            // Many rows (prefill): the norm on its own, then the projections
-            // as one q-GEMM launch over the normed rows (one activation
-            // split for all of them), a residual Add in its epilogue.
-            const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
-            const float* a = norm ? fptr(d, norm->out) : f.a;
-            if (!qgemm_mfma_takes(a, f.w, cnt, rows, ws)) return 0;
-            const bool residual = f.epilogue == kFusedResidual;
-            if (norm) {
-                e = launch_rms_norm(f.a, f.gamma, f.normed, rows, k, f.eps, d->stream);
-                if (e == hipSuccess)
-                    e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream, nullptr,
-                                           residual ? f.resid : nullptr, residual ? f.out2 : nullptr);
-            } else {
-                e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream, nullptr,
-                                       residual ? f.resid : nullptr, residual ? f.out2 : nullptr);
-            }
+        if (e != hipErrorNotSupported) {
+            if (other >= 0) ++used;
+            *err = e;
+            d->stats.fused_commands += used;
+            return used;
         }
+        // Many rows (prefill): the norm on its own, then the projections as
+        // one q-GEMM launch over the normed rows (one activation split for
+        // all of them), a residual Add in its epilogue. The split copies the
+        // activations into the workspace before the GEMM starts, so the
+        // Add's output may reuse their space.
+        if (rows <= 16) return 0;  // few rows the fused GEMV did not take: one launch each
+        const int other_many = add ? residual_port(*add, outs[0], count, nullptr, 0) : -1;
+        if (used + (other_many >= 0 ? 1 : 0) == 1) return 0;
+        const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
+        const float* a = norm ? fptr(d, norm->out) : f.a;
+        if (!qgemm_mfma_takes(a, f.w, cnt, rows, ws)) return 0;
+        set_residual(other_many);
+        const bool residual = other_many >= 0;
+        e = norm ? launch_rms_norm(f.a, f.gamma, f.normed, rows, k, f.eps, d->stream) : hipSuccess;
+        if (e == hipSuccess)
+            e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream, nullptr, residual ? f.resid : nullptr,
+                                   residual ? f.out2 : nullptr);
+        if (residual) ++used;
         *err = e;
         d->stats.fused_commands += used;
         return used;
@@ -515,11 +526,17 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
             // composite (gate and up as one q-GEMM, silu(g) * u formed by
             // the down projection's activation split) with the residual Add
             // in the down projection's epilogue when one follows.
+            // Each row chunk's activations are split into the workspace
+            // before its products run, so the Add's output may reuse their
+            // space, unless it is shifted against them and a later chunk
+            // still reads rows an earlier chunk's Add wrote.
             size_t used = (j - i) + 1;
             const Logged* add = j + 1 < n ? &d->log[j + 1] : nullptr;
-            const int other = add ? residual_port(*add, c1.out, rows * hidden, reads, n_reads,
-                                                  norm ? &norm->out : nullptr)
-                                  : -1;
+            const sl_buffer_ref x_ref = norm ? norm->out : c1.in[0];
+            int other = add ? residual_port(*add, c1.out, rows * hidden, nullptr, 0) : -1;
+            if (other >= 0 && overlaps(add->out, x_ref) && !same_ref(add->out, x_ref) &&
+                swiglu_chunk_rows(d->workspace_floats, inter) < rows)
+                other = -1;
             e = norm ? launch_rms_norm(f.a, f.gamma, f.normed, rows, hidden, f.eps, d->stream) : hipSuccess;
             if (e == hipSuccess)
                 e = launch_swiglu(norm ? f.normed : f.a, weight_ref(d, c1.in[1], c1.plan.quant[1]),

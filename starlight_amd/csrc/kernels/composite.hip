@@ -20,13 +20,20 @@ hipError_t launch_linear(const float* a, const WeightRef& w, float* out, uint64_
     return launch_matmul(a, w.dense, out, 1, 1, 1, rows, k, n, true, s);
 }
 
+// Rows per chunk of launch_swiglu with a workspace of ws_floats: its g and
+// u intermediates take half of the workspace, the projections' own scratch
+// the other half.
+uint64_t swiglu_chunk_rows(uint64_t ws_floats, uint64_t inter) {
+    const uint64_t budget = ws_floats / 2;
+    return budget > 64 && inter != 0 ? (budget - 64) / (2 * inter) : 0;
+}
+
 hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up, const WeightRef& down,
                          float* out, uint64_t rows, uint64_t hidden, uint64_t inter, const Workspace& ws,
                          hipStream_t s, const float* resid, float* out2) {
     if (rows == 0) return hipSuccess;
-    // Keep half of the workspace for the projections' own scratch.
     const uint64_t budget = ws.floats / 2;
-    uint64_t chunk = budget > 64 ? (budget - 64) / (2 * inter) : 0;
+    uint64_t chunk = swiglu_chunk_rows(ws.floats, inter);
     if (chunk == 0) return hipErrorOutOfMemory;
     if (chunk > rows) chunk = rows;
     const uint64_t u_off = (chunk * inter + 63) / 64 * 64;

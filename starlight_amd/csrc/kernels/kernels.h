@@ -238,6 +238,8 @@ struct WeightRef {
 };
 hipError_t launch_linear(const float* a, const WeightRef& w, float* out, uint64_t rows, uint64_t n,
                          uint64_t k, const Workspace& ws, hipStream_t s);
+// Rows per chunk of launch_swiglu for a workspace of ws_floats floats.
+uint64_t swiglu_chunk_rows(uint64_t ws_floats, uint64_t inter);
 // SwiGlu (reference/swiglu.rs): out = (silu(x Wg^T) * (x Wu^T)) Wd^T.
 // With out2, also out2 = resid + out (a residual Add after the SwiGlu).
 hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up,

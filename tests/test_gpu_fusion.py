@@ -543,13 +543,17 @@ def test_long_k_gemv_with_many_rows(hip, fmt_name, residual):
         np.testing.assert_array_equal(hip.read_f32(Z.buffer, m * n), resid + got.ravel())
 
 
+@pytest.mark.parametrize("alias", [False, True])
 @pytest.mark.parametrize("variant", ["matmul", "swiglu", "norm_swiglu"])
-def test_prefill_residual_add_in_the_gemm_epilogue(hip, variant):
+def test_prefill_residual_add_in_the_gemm_epilogue(hip, variant, alias):
     """At 64 rows (prefill) a quantized MatMulNT, or a SwiGlu (after an
     RmsNorm), followed by the residual Add runs with the Add in the q-GEMM's
     epilogue (the SwiGlu's silu(g) * u formed by the down projection's
     activation split). Products match the oracle per row (normwise 1e-4);
-    the Add's output is exactly residual + the product written."""
+    the Add's output is exactly residual + the product written. With alias,
+    the Add writes over the product's input (the MatMulNT's or SwiGlu's
+    activations), as a memory plan reusing their space after their last read
+    does."""
     from starlight_amd import quant
     from starlight_amd.ir import QuantFormat
 
@@ -572,6 +576,8 @@ def test_prefill_residual_add_in_the_gemm_epilogue(hip, variant):
     Y = BufferRef(hip.allocate_f32(rows * n, 256), 0, rows * n)
     R = BufferRef(hip.upload_new_f32(resid), 0, rows * n)
     Z = BufferRef(hip.allocate_f32(rows * n, 256), 0, rows * n)
+    if alias:
+        Z = N if variant == "norm_swiglu" else X
     xv, yv = Value.f32([1, rows, k]), Value.f32([1, rows, n])
     before = hip.stats()
     if variant == "matmul":

@@ -115,7 +115,7 @@ def test_softmax_parity(hip, rows, cols):
 
 
 @pytest.mark.parametrize("rows,seq,past", [(2, 2, 0), (12, 4, 1), (4, 1, 7), (6, 3, 2), (64, 32, 100),
-                                           (8, 2, 9000)])
+                                           (8, 2, 9000), (16, 8, 4088)])
 def test_softmax_causal_parity(hip, rows, seq, past):
     cols = past + seq
     x = rng(rows * 3 + past).standard_normal(rows * cols).astype(np.float32) * 3

@@ -20,9 +20,10 @@
 //  * split_rows: one block per row: E, then hi/lo in fp16 ([m][k] each)
 //    and E per row into the workspace;
 //  * qgemm_mfma: 128 x 128 output tiles, 4 waves of 64 x 64 (4 x 4 MFMA
-//    tiles of 16 x 16), k in steps of 32 through double-buffered LDS. The
-//    weight step is read from the tile layout (per 16-row tile and 128-k
-//    superblock; the 32-k step is half of one 64-k half: 32 lanes x 8 bytes
+//    tiles of 16 x 16), k in stages of 32 through double-buffered LDS; or
+//    64 x 128 tiles (waves of 32 x 64) in stages of 32 or 64. The weight
+//    stage is read from the tile layout (per 16-row tile and 128-k
+//    superblock; a 32-k stage is half of one 64-k half: 32 lanes x 8 bytes
 //    for INT4, x 16 bytes for INT8) and converted to fp16 codes in LDS.
 #include "common.h"
 #include "kernels.h"
@@ -35,8 +36,12 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 128;     // output columns per block (rows: BM, 128 or 64)
-constexpr int kStepK = 32;     // k per MFMA step and per LDS stage
-constexpr int kRowPad = 48;    // halves per LDS row: 96 bytes, 16-byte aligned (80 and 112 measured slower)
+constexpr int kStepK = 32;     // k per MFMA step (an LDS stage holds KS = 32 or 64)
+// halves per LDS row: 96 bytes for 32-k stages (80 and 112 measured
+// slower); 144 bytes for 64-k stages, which puts the 16 rows one operand
+// read spans on 16 disjoint groups of 4 banks
+template <int KS>
+constexpr int row_pad() { return KS == 32 ? 48 : 72; }
 constexpr int kExpBias = 15;   // scaled rows stay below 2^15
 
 // The activation element: a, or with a second input u (SwiGlu's down
@@ -94,7 +99,7 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, c
 // the weight bytes (INT4: the first 8), and the scale of column tid % 128
 // for the stage's quantization group.
 struct StageRegs {
-    uint4 h0, l0, h1, l1, b;
+    uint4 h0, l0, h1, l1, b, b2;  // b2: 64-k stages of INT8 weights
     float sc;
 };
 
@@ -123,14 +128,18 @@ __device__ __forceinline__ _Float16 nib(uint32_t word, int shift) {
     return static_cast<_Float16>(static_cast<int>(word << (28 - shift)) >> 28);
 }
 
-template <int BITS, int BM>
+template <int BITS, int BM, int KS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(GemmArgs p) {
     static_assert(BM == 128 || BM == 64, "block rows");
+    static_assert(KS == 32 || KS == 64, "stage depth");
+    constexpr int CPR = KS / 8;  // 16-byte chunks per row and stage
+    static_assert(BM * CPR <= 512, "at most two activation chunks per plane per thread");
     constexpr int MT = BM / 32;  // 16-row tiles per wave (a wave owns BM / 2 rows)
+    constexpr int RP = row_pad<KS>();
     prefetch_kernarg<arg_bytes<GemmArgs>()>();
-    __shared__ __align__(16) _Float16 as[2][2][BM][kRowPad];      // [stage][hi, lo][row][k]
-    __shared__ __align__(16) _Float16 bs[2][kTile][kRowPad];     // [stage][column][k]
-    __shared__ float ss[2][kTile];                                // [stage][column]: the group's scales
+    __shared__ __align__(16) _Float16 as[2][2][BM][RP];      // [stage][hi, lo][row][k]
+    __shared__ __align__(16) _Float16 bs[2][kTile][RP];     // [stage][column][k]
+    __shared__ float ss[2][kTile];                           // [stage][column]: the group's scales
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const int wm = wave / 2, wn = wave % 2;
     // this block's weight, chosen with selects (block-uniform, in scalar
@@ -146,74 +155,106 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     const uint32_t n = SL_GSEG(n), n_tiles = (n + 15) / 16;
     const uint32_t m0 = blockIdx.y * BM, n0 = (bx - SL_GSEG(block0)) * kTile;
 #undef SL_GSEG
-    const uint32_t steps = p.k / kStepK, group_steps = p.group / kStepK;
+    const uint32_t steps = p.k / KS, group_steps = p.group / KS;
 
     // This thread's share of a stage: one 16-byte chunk of each of hi and lo
-    // per 64 rows of the block (row c / 4, halves 8 (c % 4) ..), and one
-    // 32-lane slice of a
-    // weight tile (tile tid / 32, lane within the slice tid % 32).
+    // per 256 / CPR rows of the block (row c / CPR, halves 8 (c % CPR) ..),
+    // and of the weights (tile layout: per 16-row tile and 64-k half of a
+    // superblock, lane L holds 16 codes of column L % 16, k 16 (L / 16) ..):
+    // 32-k stages, lanes 32 t .. 32 t + 31 of tile tid / 32 (bi = tid % 32);
+    // 64-k stages, lane tid % 64 of tiles tid / 64 and tid / 64 + 4.
     // (plain variables, not arrays: an array the lambdas capture would be
     // placed in LDS by the compiler)
     const uint32_t c0 = tid, c1 = tid + 256;
-    const uint64_t aoff0 = static_cast<uint64_t>(min(m0 + c0 / 4, p.m - 1)) * p.k + 8 * (c0 % 4);
-    const uint64_t aoff1 = static_cast<uint64_t>(min(m0 + c1 / 4, p.m - 1)) * p.k + 8 * (c1 % 4);
-    const uint32_t bt = min(n0 / 16 + tid / 32, n_tiles - 1), bi = tid % 32;
+    const uint64_t aoff0 = static_cast<uint64_t>(min(m0 + c0 / CPR, p.m - 1)) * p.k + 8 * (c0 % CPR);
+    const uint64_t aoff1 = static_cast<uint64_t>(min(m0 + c1 / CPR, p.m - 1)) * p.k + 8 * (c1 % CPR);
+    const uint32_t bi = KS == 32 ? tid % 32 : tid % 64;
+    const uint32_t bt = min(n0 / 16 + (KS == 32 ? tid / 32 : tid / 64), n_tiles - 1);
+    const uint32_t bt2 = min(n0 / 16 + tid / 64 + 4, n_tiles - 1);  // 64-k stages
     const uint32_t scol_ld = min(n0 + tid % kTile, n - 1);  // the scale this thread stages
     // (slots travel by value: a slot passed by reference would be placed in
     // LDS by the compiler)
     auto load_stage = [&](uint32_t st) -> StageRegs {
         StageRegs r;
-        const uint32_t k0 = st * kStepK;
+        const uint32_t k0 = st * KS;
         r.h0 = *reinterpret_cast<const uint4*>(p.ahi + aoff0 + k0);
         r.l0 = *reinterpret_cast<const uint4*>(p.alo + aoff0 + k0);
-        if constexpr (BM == 128) {
+        if constexpr (BM * CPR == 512) {
             r.h1 = *reinterpret_cast<const uint4*>(p.ahi + aoff1 + k0);
             r.l1 = *reinterpret_cast<const uint4*>(p.alo + aoff1 + k0);
         }
         r.sc = scales[static_cast<uint64_t>(scol_ld) * p.groups + k0 / p.group];
-        const uint32_t sb = k0 / 128, t = (k0 % 128) / kStepK, s = t / 2;
-        const uint32_t L = (2 * (t % 2) + bi / 16) * 16 + bi % 16;
-        const uint64_t tile = static_cast<uint64_t>(bt) * p.sb_total + sb;
-        if constexpr (BITS == 4) {
-            const uint2 w = *reinterpret_cast<const uint2*>(tiles + tile * 1024 + L * 16 + s * 8);
-            r.b = make_uint4(w.x, w.y, 0u, 0u);
+        const uint32_t sb = k0 / 128;
+        if constexpr (KS == 32) {
+            const uint32_t t = (k0 % 128) / kStepK, s = t / 2;
+            const uint32_t L = (2 * (t % 2) + bi / 16) * 16 + bi % 16;
+            const uint64_t tile = static_cast<uint64_t>(bt) * p.sb_total + sb;
+            if constexpr (BITS == 4) {
+                const uint2 w = *reinterpret_cast<const uint2*>(tiles + tile * 1024 + L * 16 + s * 8);
+                r.b = make_uint4(w.x, w.y, 0u, 0u);
+            } else {
+                r.b = *reinterpret_cast<const uint4*>(tiles + tile * 2048 + s * 1024 + L * 16);
+            }
         } else {
-            r.b = *reinterpret_cast<const uint4*>(tiles + tile * 2048 + s * 1024 + L * 16);
+            const uint32_t s = (k0 % 128) / 64, L = bi;
+            const uint64_t t0 = static_cast<uint64_t>(bt) * p.sb_total + sb;
+            const uint64_t t1 = static_cast<uint64_t>(bt2) * p.sb_total + sb;
+            if constexpr (BITS == 4) {
+                const uint2 w0 = *reinterpret_cast<const uint2*>(tiles + t0 * 1024 + L * 16 + s * 8);
+                const uint2 w1 = *reinterpret_cast<const uint2*>(tiles + t1 * 1024 + L * 16 + s * 8);
+                r.b = make_uint4(w0.x, w0.y, w1.x, w1.y);
+            } else {
+                r.b = *reinterpret_cast<const uint4*>(tiles + t0 * 2048 + s * 1024 + L * 16);
+                r.b2 = *reinterpret_cast<const uint4*>(tiles + t1 * 2048 + s * 1024 + L * 16);
+            }
         }
         return r;
     };
-    auto store_stage = [&](int buf, StageRegs r) {
-        const uint4 rb = r.b;
-        if (tid < kTile) ss[buf][tid] = r.sc;
-        *reinterpret_cast<uint4*>(&as[buf][0][c0 / 4][8 * (c0 % 4)]) = r.h0;
-        *reinterpret_cast<uint4*>(&as[buf][1][c0 / 4][8 * (c0 % 4)]) = r.l0;
-        if constexpr (BM == 128) {
-            *reinterpret_cast<uint4*>(&as[buf][0][c1 / 4][8 * (c1 % 4)]) = r.h1;
-            *reinterpret_cast<uint4*>(&as[buf][1][c1 / 4][8 * (c1 % 4)]) = r.l1;
-        }
-        // 16 codes of column (tid / 32) * 16 + bi % 16, k 16 (bi / 16) .. + 15
+    // 16 codes (INT4: words x, y; INT8: x, y, z, w) as fp16 at dst
+    auto put_codes = [&](_Float16* dst, uint32_t x, uint32_t y, uint32_t z, uint32_t w) {
         v8h q0, q1;
         if constexpr (BITS == 4) {
             // byte b of word 0: k = b (low nibble), 4 + b (high); word 1: 8 + b, 12 + b
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                q0[b] = nib(rb.x, 8 * b);
-                q0[4 + b] = nib(rb.x, 8 * b + 4);
-                q1[b] = nib(rb.y, 8 * b);
-                q1[4 + b] = nib(rb.y, 8 * b + 4);
+                q0[b] = nib(x, 8 * b);
+                q0[4 + b] = nib(x, 8 * b + 4);
+                q1[b] = nib(y, 8 * b);
+                q1[4 + b] = nib(y, 8 * b + 4);
             }
         } else {
-            const uint32_t w[4] = {rb.x, rb.y, rb.z, rb.w};
+            const uint32_t wd[4] = {x, y, z, w};
 #pragma unroll
             for (int b = 0; b < 16; ++b) {
-                const _Float16 v = static_cast<_Float16>(static_cast<int>(w[b / 4] << (24 - 8 * (b % 4))) >> 24);
+                const _Float16 v = static_cast<_Float16>(static_cast<int>(wd[b / 4] << (24 - 8 * (b % 4))) >> 24);
                 if (b < 8) q0[b] = v;
                 else q1[b - 8] = v;
             }
         }
-        _Float16* dst = &bs[buf][(tid / 32) * 16 + bi % 16][16 * (bi / 16)];
         *reinterpret_cast<v8h*>(dst) = q0;
         *reinterpret_cast<v8h*>(dst + 8) = q1;
+    };
+    auto store_stage = [&](int buf, StageRegs r) {
+        const uint4 rb = r.b;
+        if (tid < kTile) ss[buf][tid] = r.sc;
+        *reinterpret_cast<uint4*>(&as[buf][0][c0 / CPR][8 * (c0 % CPR)]) = r.h0;
+        *reinterpret_cast<uint4*>(&as[buf][1][c0 / CPR][8 * (c0 % CPR)]) = r.l0;
+        if constexpr (BM * CPR == 512) {
+            *reinterpret_cast<uint4*>(&as[buf][0][c1 / CPR][8 * (c1 % CPR)]) = r.h1;
+            *reinterpret_cast<uint4*>(&as[buf][1][c1 / CPR][8 * (c1 % CPR)]) = r.l1;
+        }
+        if constexpr (KS == 32) {
+            // 16 codes of column (tid / 32) * 16 + bi % 16, k 16 (bi / 16) .. + 15
+            put_codes(&bs[buf][(tid / 32) * 16 + bi % 16][16 * (bi / 16)], rb.x, rb.y, rb.z, rb.w);
+        } else if constexpr (BITS == 4) {
+            // lane bi of tiles tid / 64 and tid / 64 + 4: column 16 t + bi % 16, k 16 (bi / 16) ..
+            put_codes(&bs[buf][(tid / 64) * 16 + bi % 16][16 * (bi / 16)], rb.x, rb.y, 0u, 0u);
+            put_codes(&bs[buf][(tid / 64 + 4) * 16 + bi % 16][16 * (bi / 16)], rb.z, rb.w, 0u, 0u);
+        } else {
+            const uint4 rb2 = r.b2;
+            put_codes(&bs[buf][(tid / 64) * 16 + bi % 16][16 * (bi / 16)], rb.x, rb.y, rb.z, rb.w);
+            put_codes(&bs[buf][(tid / 64 + 4) * 16 + bi % 16][16 * (bi / 16)], rb2.x, rb2.y, rb2.z, rb2.w);
+        }
     };
 
     v4f acc[MT][4], tmp[MT][4];
@@ -231,7 +272,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     // two blocks share each CU (their LDS, 73 KB each, fits twice) and one
     // block's MFMA work covers the other's loads, conversions and barriers:
     // [14336 x 4096] at M = 512 took 288 us with four slots and one block per
-    // CU, 200 us so. steps (k / 32) is a multiple of 4.
+    // CU, 200 us so. steps is even (k % 128 == 0).
     StageRegs r0 = load_stage(0), r1 = load_stage(1);
     store_stage(0, r0);
     __syncthreads();
@@ -242,20 +283,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
         // compiler's waits stay exact (a conditional load makes it wait for
         // every outstanding one where the paths join)
         mine = load_stage(min(st + 2, steps - 1));
-        // operands: A rows (BM / 2) wm + 16 i + lane % 16, B columns 64 wn + 16 j + lane % 16,
-        // k 8 (lane / 16) .. + 7 of the step
-        const int kq = 8 * (lane / 16);
-        v8h bq[4];
+        // operands of MFMA step h: A rows (BM / 2) wm + 16 i + lane % 16, B columns
+        // 64 wn + 16 j + lane % 16, k 32 h + 8 (lane / 16) .. + 7 of the stage
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bq[j] = *reinterpret_cast<const v8h*>(&bs[buf][64 * wn + 16 * j + lane % 16][kq]);
+        for (int h = 0; h < KS / kStepK; ++h) {
+            const int kq = kStepK * h + 8 * (lane / 16);
+            v8h bq[4];
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
-            const v8h ah = *reinterpret_cast<const v8h*>(&as[buf][0][(BM / 2) * wm + 16 * i + lane % 16][kq]);
-            const v8h al = *reinterpret_cast<const v8h*>(&as[buf][1][(BM / 2) * wm + 16 * i + lane % 16][kq]);
+            for (int j = 0; j < 4; ++j)
+                bq[j] = *reinterpret_cast<const v8h*>(&bs[buf][64 * wn + 16 * j + lane % 16][kq]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[j], tmp[i][j], 0, 0, 0);
-                tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[j], tmp[i][j], 0, 0, 0);
+            for (int i = 0; i < MT; ++i) {
+                const v8h ah = *reinterpret_cast<const v8h*>(&as[buf][0][(BM / 2) * wm + 16 * i + lane % 16][kq]);
+                const v8h al = *reinterpret_cast<const v8h*>(&as[buf][1][(BM / 2) * wm + 16 * i + lane % 16][kq]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[j], tmp[i][j], 0, 0, 0);
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[j], tmp[i][j], 0, 0, 0);
+                }
             }
         }
         if (st % group_steps == group_steps - 1) {
@@ -366,13 +411,16 @@ hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float
     // MI355X: M = 1024 [4096 x 4096] (256 blocks of 128 rows) runs faster in
     // 64-row blocks; M = 512 [14336 x 4096] (448) runs slower (200 -> 250 us).
     const bool rows64 = static_cast<uint64_t>(blocks) * ((m + 127) / 128) <= compute_units();
+    const bool deep = rows64 && w0.group % 64 == 0;  // 64-k stages
     const dim3 grid(blocks, static_cast<unsigned>(rows64 ? (m + 63) / 64 : (m + 127) / 128));
     if (w0.format == SL_QFORMAT_INT4) {
-        if (rows64) qgemm_mfma<4, 64><<<grid, 256, 0, s>>>(p);
-        else qgemm_mfma<4, 128><<<grid, 256, 0, s>>>(p);
+        if (deep) qgemm_mfma<4, 64, 64><<<grid, 256, 0, s>>>(p);
+        else if (rows64) qgemm_mfma<4, 64, 32><<<grid, 256, 0, s>>>(p);
+        else qgemm_mfma<4, 128, 32><<<grid, 256, 0, s>>>(p);
     } else {
-        if (rows64) qgemm_mfma<8, 64><<<grid, 256, 0, s>>>(p);
-        else qgemm_mfma<8, 128><<<grid, 256, 0, s>>>(p);
+        if (deep) qgemm_mfma<8, 64, 64><<<grid, 256, 0, s>>>(p);
+        else if (rows64) qgemm_mfma<8, 64, 32><<<grid, 256, 0, s>>>(p);
+        else qgemm_mfma<8, 128, 32><<<grid, 256, 0, s>>>(p);
     }
     return hipGetLastError();
 }

@@ -1247,6 +1247,7 @@ sl_status sl_hip_paged_attention(sl_hip_device* d, const sl_op* op, const sl_buf
     for (uint64_t b = 0; b < B; ++b)
         if (readers[tb.mirror[b * kv->pages_per_seq + lb.mirror[b] / kv->page_size]] != b)
             return d->fail(Error::execution("a row appends into a page another row reads"));
+    if (B == 0) return SL_OK;  // an empty batch: nothing to read or append
     if (slhip::flush(d) != SL_OK) return d->last.status;
     slhip::PagedAttentionArgs a{};
     a.q = slhip::fptr(d, *q);

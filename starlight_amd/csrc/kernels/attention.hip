@@ -729,11 +729,15 @@ __global__ __launch_bounds__(256) void attn_prefill(Geo g, uint32_t qtiles) {
     __shared__ __align__(16) float vs[kPfK * LS];
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const int c = lane % 16, kk = lane / 16;
-    const uint32_t qt = qtiles - 1 - blockIdx.x;
     const uint32_t h = blockIdx.y;
     const uint64_t b = blockIdx.z;
     const uint32_t kvh = h / g.group;
     const uint32_t past = past_of(g);
+    // query tiles qtiles - 1 - x, then x (the causal key ranges of the two
+    // add up to about the same for every block)
+    for (uint32_t pass = 0; pass < 2; ++pass) {
+    const uint32_t qt = pass == 0 ? qtiles - 1 - blockIdx.x : blockIdx.x;
+    if (pass == 1 && qt >= qtiles - 1 - blockIdx.x) break;  // block-uniform
     const uint32_t q0 = qt * kPfQ + wave * 16;  // the wave's first query
     const uint32_t t = q0 + c;                  // this lane's query
     const uint32_t tq = min(t, g.seq - 1);      // lanes past the end compute on the last query, unstored
@@ -830,12 +834,15 @@ __global__ __launch_bounds__(256) void attn_prefill(Geo g, uint32_t qtiles) {
                                                                  p[sub][i], o[j], 0, 0, 0);
         }
     }
-    if (t >= g.seq) return;
-    const float inv = 1.0f / lsum;
-    float* orow = g.out + ((b * g.heads + h) * g.seq + t) * D + 4 * kk;
+    if (t < g.seq) {
+        const float inv = 1.0f / lsum;
+        float* orow = g.out + ((b * g.heads + h) * g.seq + t) * D + 4 * kk;
 #pragma unroll
-    for (int j = 0; j < D16; ++j)
-        *reinterpret_cast<float4*>(orow + 16 * j) = make_float4(o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv);
+        for (int j = 0; j < D16; ++j)
+            *reinterpret_cast<float4*>(orow + 16 * j) =
+                make_float4(o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv);
+    }
+    }
 }
 
 }  // namespace
@@ -1006,7 +1013,7 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
     const bool aligned = aligned16(a.q) && aligned16(a.cache) && aligned16(a.out);
     if (a.seq >= 16 && aligned && (a.head_dim == 64 || a.head_dim == 128)) {
         const uint32_t qtiles = static_cast<uint32_t>((a.seq + kPfQ - 1) / kPfQ);
-        dim3 grid(qtiles, g.heads, static_cast<unsigned>(a.batch));
+        dim3 grid((qtiles + 1) / 2, g.heads, static_cast<unsigned>(a.batch));
         if (a.head_dim == 64) attn_prefill<64><<<grid, 256, 0, s>>>(g, qtiles);
         else attn_prefill<128><<<grid, 256, 0, s>>>(g, qtiles);
         return hipGetLastError();

@@ -152,3 +152,18 @@ def test_bad_block_tables_are_rejected(hip, case, message):
         hip.paged_attention(Op.causal_attention(0, H, HKV, D, SCALE), q, kv, kv2, BufferRef(out, 0, 2 * H * D), 2,
                             cache.c_struct())
     assert e.value == DeviceError.execution(message)
+
+
+def test_empty_batch_is_a_no_op(hip):
+    """A batch of no rows validates its arguments and launches nothing:
+    the page pool is unchanged."""
+    pool = PagePool(num_pages=4, page_size=16, pages_per_seq=2, max_batch=2)
+    cache = PagedKvCache(hip, LAYERS, HKV, D, pool)
+    host = np.random.default_rng(51).uniform(-1, 1, cache.pool_elements).astype(np.float32)
+    hip.upload_f32(cache.pool_buffer, host)
+    cache.sync()
+    empty = BufferRef(hip.allocate_f32(16, 256), 0, 0)
+    out = BufferRef(hip.allocate_f32(16, 256), 0, 0)
+    hip.paged_attention(Op.causal_attention(0, H, HKV, D, SCALE), empty, empty, empty, out, 0, cache.c_struct())
+    hip.synchronize()
+    np.testing.assert_array_equal(hip.read_f32(cache.pool_buffer, cache.pool_elements), host)

@@ -699,8 +699,10 @@ __global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
 
 // ---- prefill: the f32 matrix cores ----
 //
-// A block of 4 waves owns 64 queries of one head (wave w: queries 16 w ..
-// 16 w + 15 of the block's range) and streams the keys 32 at a time. Each
+// A block owns 64 queries of one head (query wave w: queries 16 w .. 16 w +
+// 15 of the block's range) and streams the keys 32 at a time; with KH = 2
+// two waves serve each query wave, one per 16-key half of every tile, and
+// their softmax states are combined through LDS at the end. Each
 // tile of K and V rows goes to LDS (row stride D + 4 floats, so a wave's
 // 16-byte K reads and 4-byte V reads hit 64 distinct banks) while the next
 // tile's rows wait in registers. Per tile a wave forms S^T = K Q^T (keys x
@@ -714,20 +716,31 @@ __global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
 // The reduction over d is taken in a permuted order, the same for both
 // operands: of each 16 dims, step s takes d = 4 (l / 16) + s, so a lane's
 // operands of four steps are one float4 of K in LDS and of Q in registers.
-// Blocks run the longest key ranges first (query tiles in reverse order).
+// A block runs two query tiles one after the other, the last and the first,
+// the second-to-last and the second, ..., so every block's causal key ranges
+// add up to about the same work.
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 constexpr int kPfQ = 64;  // queries per block
 constexpr int kPfK = 32;  // keys per tile
 
-template <int D>
-__global__ __launch_bounds__(256) void attn_prefill(Geo g, uint32_t qtiles) {
+template <int D, int KH>
+__global__ __launch_bounds__(256 * KH) void attn_prefill(Geo g, uint32_t qtiles) {
     prefetch_kernarg<arg_bytes<Geo, uint32_t>()>();
+    constexpr int NT = 256 * KH;             // threads
     constexpr int LS = D + 4;                // LDS row stride (floats)
     constexpr int D16 = D / 16;              // float4 of Q per lane, and 16-dim output tiles
-    constexpr int F4 = kPfK * D / 4 / 256;   // float4 of K (and of V) per thread per tile
+    constexpr int F4 = kPfK * D / 4 / NT;    // float4 of K (and of V) per thread per tile
+    constexpr int NS = 2 / KH;               // 16-key halves of a tile per wave
+    static_assert(F4 >= 1 && KH >= 1 && KH <= 2, "tile split");
     __shared__ __align__(16) float ks[kPfK * LS];
     __shared__ __align__(16) float vs[kPfK * LS];
+    // KH == 2: the second key half's softmax state (m, l, o) per lane of
+    // each query wave, field-major
+    constexpr int XF = 2 + D / 4;
+    __shared__ float xs[KH == 2 ? XF * 256 : 1];
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int qw = wave % 4;                 // query wave: queries 16 qw .. of the tile
+    const int half = KH == 2 ? wave / 4 : 0; // KH == 2: keys 16 half .. 16 half + 15 of each tile
     const int c = lane % 16, kk = lane / 16;
     const uint32_t h = blockIdx.y;
     const uint64_t b = blockIdx.z;
@@ -738,7 +751,7 @@ __global__ __launch_bounds__(256) void attn_prefill(Geo g, uint32_t qtiles) {
     for (uint32_t pass = 0; pass < 2; ++pass) {
     const uint32_t qt = pass == 0 ? qtiles - 1 - blockIdx.x : blockIdx.x;
     if (pass == 1 && qt >= qtiles - 1 - blockIdx.x) break;  // block-uniform
-    const uint32_t q0 = qt * kPfQ + wave * 16;  // the wave's first query
+    const uint32_t q0 = qt * kPfQ + qw * 16;    // the wave's first query
     const uint32_t t = q0 + c;                  // this lane's query
     const uint32_t tq = min(t, g.seq - 1);      // lanes past the end compute on the last query, unstored
     const uint32_t block_keys = past + min(g.seq, (qt + 1) * kPfQ);
@@ -762,7 +775,7 @@ __global__ __launch_bounds__(256) void attn_prefill(Geo g, uint32_t qtiles) {
     auto load = [&](uint32_t kt) {
 #pragma unroll
         for (int u = 0; u < F4; ++u) {
-            const uint32_t e = tid + 256 * u, row = e / (D / 4), col = e % (D / 4);
+            const uint32_t e = tid + NT * u, row = e / (D / 4), col = e % (D / 4);
             const uint64_t j = min(kt + row, block_keys - 1);
             kn[u] = reinterpret_cast<const float4*>(kbase + j * time_stride)[col];
             vn[u] = reinterpret_cast<const float4*>(vbase + j * time_stride)[col];
@@ -773,50 +786,56 @@ __global__ __launch_bounds__(256) void attn_prefill(Geo g, uint32_t qtiles) {
         __syncthreads();  // every wave is done reading the previous tile
 #pragma unroll
         for (int u = 0; u < F4; ++u) {
-            const uint32_t e = tid + 256 * u, row = e / (D / 4), col = e % (D / 4);
+            const uint32_t e = tid + NT * u, row = e / (D / 4), col = e % (D / 4);
             *reinterpret_cast<float4*>(ks + row * LS + 4 * col) = kn[u];
             *reinterpret_cast<float4*>(vs + row * LS + 4 * col) = vn[u];
         }
         __syncthreads();
         if (kt + kPfK < block_keys) load(kt + kPfK);
-        if (kt >= wave_keys) continue;  // wave-uniform: no key of the tile is visible to the wave
+        // wave-uniform: no key of the wave's part of the tile is visible to it
+        if (kt + 16 * half >= wave_keys) continue;
         // S^T: keys 16 sub + 4 kk + i of the tile, query c
-        v4f_t st[2];
+        v4f_t st[NS];
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            st[sub] = v4f_t{0.f, 0.f, 0.f, 0.f};
+        for (int si = 0; si < NS; ++si) {
+            const int sub = KH == 2 ? half : si;
+            st[si] = v4f_t{0.f, 0.f, 0.f, 0.f};
             const float* krow = ks + (sub * 16 + c) * LS + 4 * kk;
 #pragma unroll
             for (int j = 0; j < D16; ++j) {
                 const float4 k4 = *reinterpret_cast<const float4*>(krow + 16 * j);
-                st[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qv[j].x, st[sub], 0, 0, 0);
-                st[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qv[j].y, st[sub], 0, 0, 0);
-                st[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qv[j].z, st[sub], 0, 0, 0);
-                st[sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qv[j].w, st[sub], 0, 0, 0);
+                st[si] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qv[j].x, st[si], 0, 0, 0);
+                st[si] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qv[j].y, st[si], 0, 0, 0);
+                st[si] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qv[j].z, st[si], 0, 0, 0);
+                st[si] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qv[j].w, st[si], 0, 0, 0);
             }
         }
-        float p[2][4];
+        float p[NS][4];
         float tmax = -INFINITY;
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
+        for (int si = 0; si < NS; ++si)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                const int sub = KH == 2 ? half : si;
                 const uint32_t key = kt + 16 * sub + 4 * kk + i;
-                p[sub][i] = key < my_keys ? st[sub][i] * g.scale : -INFINITY;
-                tmax = fmaxf(tmax, p[sub][i]);
+                p[si][i] = key < my_keys ? st[si][i] * g.scale : -INFINITY;
+                tmax = fmaxf(tmax, p[si][i]);
             }
         tmax = fmaxf(tmax, lane_xor16(tmax));
         tmax = fmaxf(tmax, lane_xor32(tmax));
-        // key 0 is visible to every query, so m is finite from the first tile on
+        // With one key half per wave a query can see none of a tile's keys
+        // (m_new == -inf): the guards keep corr and every weight 0, not NaN.
+        // (With both halves key 0 is visible to every query, so m is finite
+        // from the first tile on.)
         const float m_new = fmaxf(m, tmax);
-        const float corr = expf(m - m_new);
+        const float corr = m == -INFINITY ? 0.f : expf(m - m_new);
         float psum = 0.f;
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
+        for (int si = 0; si < NS; ++si)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                p[sub][i] = expf(p[sub][i] - m_new);
-                psum += p[sub][i];
+                p[si][i] = p[si][i] == -INFINITY ? 0.f : expf(p[si][i] - m_new);
+                psum += p[si][i];
             }
         psum += lane_xor16(psum);
         psum += lane_xor32(psum);
@@ -827,12 +846,36 @@ __global__ __launch_bounds__(256) void attn_prefill(Geo g, uint32_t qtiles) {
         for (int j = 0; j < D16; ++j) {
             o[j] *= corr;
 #pragma unroll
-            for (int sub = 0; sub < 2; ++sub)
+            for (int si = 0; si < NS; ++si)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 4; ++i) {
+                    const int sub = KH == 2 ? half : si;
                     o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vs[(16 * sub + 4 * kk + i) * LS + 16 * j + c],
-                                                                 p[sub][i], o[j], 0, 0, 0);
+                                                                 p[si][i], o[j], 0, 0, 0);
+                }
         }
+    }
+    if constexpr (KH == 2) {
+        // the second half's state through LDS; the first half's waves merge
+        const int x = qw * kWave + lane;
+        if (half == 1) {
+            xs[x] = m;
+            xs[256 + x] = lsum;
+#pragma unroll
+            for (int j = 0; j < D16; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xs[(2 + 4 * j + e) * 256 + x] = o[j][e];
+        }
+        __syncthreads();
+        if (half == 1) continue;
+        const float m1 = xs[x], l1 = xs[256 + x];
+        const float mm = fmaxf(m, m1);
+        const float c0 = m == -INFINITY ? 0.f : expf(m - mm), c1 = m1 == -INFINITY ? 0.f : expf(m1 - mm);
+        lsum = lsum * c0 + l1 * c1;
+#pragma unroll
+        for (int j = 0; j < D16; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[j][e] = o[j][e] * c0 + xs[(2 + 4 * j + e) * 256 + x] * c1;
     }
     if (t < g.seq) {
         const float inv = 1.0f / lsum;
@@ -1014,8 +1057,8 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
     if (a.seq >= 16 && aligned && (a.head_dim == 64 || a.head_dim == 128)) {
         const uint32_t qtiles = static_cast<uint32_t>((a.seq + kPfQ - 1) / kPfQ);
         dim3 grid((qtiles + 1) / 2, g.heads, static_cast<unsigned>(a.batch));
-        if (a.head_dim == 64) attn_prefill<64><<<grid, 256, 0, s>>>(g, qtiles);
-        else attn_prefill<128><<<grid, 256, 0, s>>>(g, qtiles);
+        if (a.head_dim == 64) attn_prefill<64, 2><<<grid, 512, 0, s>>>(g, qtiles);
+        else attn_prefill<128, 2><<<grid, 512, 0, s>>>(g, qtiles);
         return hipGetLastError();
     }
     if (a.head_dim > 256) return hipErrorInvalidValue;

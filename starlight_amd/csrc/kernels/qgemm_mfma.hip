@@ -95,6 +95,19 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, c
     }
 }
 
+// out[i] = the k slices' partial sums of element i, added in slice order;
+// with resid, out2[i] = resid[i] + out[i] (the residual Add's order).
+__global__ __launch_bounds__(256) void gemm_slices_sum(const float* __restrict__ partial, uint32_t slices,
+                                                       uint64_t count, float* out, const float* resid, float* out2) {
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
+         i += static_cast<uint64_t>(gridDim.x) * 256) {
+        float v = partial[i];
+        for (uint32_t z = 1; z < slices; ++z) v += partial[z * count + i];
+        out[i] = v;
+        if (out2 != nullptr) out2[i] = resid[i] + v;
+    }
+}
+
 // One stage's share of a thread: two 16-byte chunks of each of hi and lo,
 // the weight bytes (INT4: the first 8), and the scale of column tid % 128
 // for the stage's quantization group.
@@ -121,6 +134,9 @@ struct GemmArgs {
     const int* row_exp;
     GemmSeg seg[kFusedMaxSegs];
     uint32_t nseg, m, k, group, groups, sb_total;
+    // k cut into gridDim.z slices of k / gridDim.z (one weight only): slice z
+    // writes its m x n partial sums at partial + z m n, added up afterwards
+    float* partial;
 };
 
 // A signed nibble (two's complement) of byte b, bit offset 0 or 4, as fp16.
@@ -144,7 +160,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     const int wm = wave / 2, wn = wave % 2;
     // this block's weight, chosen with selects (block-uniform, in scalar
     // registers; a runtime index into the arguments would be a memory load)
-    const uint32_t bx = blockIdx.x;
+    // this block's column block bx, row block by and k slice bz
+    const uint32_t bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
     const uint32_t si = (p.nseg > 1 && bx >= p.seg[1].block0 ? 1u : 0u) + (p.nseg > 2 && bx >= p.seg[2].block0 ? 1u : 0u);
 #define SL_GSEG(f) (si == 0 ? p.seg[0].f : si == 1 ? p.seg[1].f : p.seg[2].f)
     const uint8_t* const tiles = SL_GSEG(tiles);
@@ -153,9 +170,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     const float* const resid = SL_GSEG(resid);
     float* const out2 = SL_GSEG(out2);
     const uint32_t n = SL_GSEG(n), n_tiles = (n + 15) / 16;
-    const uint32_t m0 = blockIdx.y * BM, n0 = (bx - SL_GSEG(block0)) * kTile;
+    const uint32_t m0 = by * BM, n0 = (bx - SL_GSEG(block0)) * kTile;
 #undef SL_GSEG
-    const uint32_t steps = p.k / KS, group_steps = p.group / KS;
+    const uint32_t kslice = p.k / gridDim.z, kbeg = bz * kslice;  // this block's k range
+    const uint32_t steps = kslice / KS, group_steps = p.group / KS;
 
     // This thread's share of a stage: one 16-byte chunk of each of hi and lo
     // per 256 / CPR rows of the block (row c / CPR, halves 8 (c % CPR) ..),
@@ -176,7 +194,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     // LDS by the compiler)
     auto load_stage = [&](uint32_t st) -> StageRegs {
         StageRegs r;
-        const uint32_t k0 = st * KS;
+        const uint32_t k0 = kbeg + st * KS;
         r.h0 = *reinterpret_cast<const uint4*>(p.ahi + aoff0 + k0);
         r.l0 = *reinterpret_cast<const uint4*>(p.alo + aoff0 + k0);
         if constexpr (BM * CPR == 512) {
@@ -340,6 +358,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
                 if (col >= n) continue;
                 const uint64_t o = static_cast<uint64_t>(row) * n + col;
                 const float val = ldexpf(acc[i][j][e], sh);
+                if (gridDim.z > 1) {
+                    p.partial[static_cast<uint64_t>(bz) * p.m * n + o] = val;
+                    continue;
+                }
                 out[o] = val;
                 if (out2 != nullptr) out2[o] = resid[o] + val;
             }
@@ -410,9 +432,19 @@ hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float
     // reuse) when 128-row blocks would not give every CU one. Measured on
     // MI355X: M = 1024 [4096 x 4096] (256 blocks of 128 rows) runs faster in
     // 64-row blocks; M = 512 [14336 x 4096] (448) runs slower (200 -> 250 us).
-    const bool rows64 = static_cast<uint64_t>(blocks) * ((m + 127) / 128) <= compute_units();
+    // 128-row blocks, or when they would not give every CU one: k in two
+    // slices of 128-row blocks (one weight, the slice a whole number of
+    // groups and 128-k superblocks, room for the partial sums), else 64-row
+    // blocks. Measured on MI355X at M = 1024: [4096 x 14336] 395-402 us in
+    // k slices (the slice sums included) against 440 us in 64-row blocks.
+    const uint64_t blocks128 = static_cast<uint64_t>(blocks) * ((m + 127) / 128);
+    const uint64_t part_at = (lay.floats + 63) / 64 * 64;
+    const bool sliced = blocks128 <= compute_units() && nseg == 1 && (w0.k / 2) % 128 == 0 &&
+                        (w0.k / 2) % w0.group == 0 && part_at + 2 * m * w0.n <= ws.floats;
+    const bool rows64 = blocks128 <= compute_units() && !sliced;
     const bool deep = rows64 && w0.group % 64 == 0;  // 64-k stages
-    const dim3 grid(blocks, static_cast<unsigned>(rows64 ? (m + 63) / 64 : (m + 127) / 128));
+    p.partial = sliced ? ws.data + part_at : nullptr;
+    const dim3 grid(blocks, static_cast<unsigned>(rows64 ? (m + 63) / 64 : (m + 127) / 128), sliced ? 2u : 1u);
     if (w0.format == SL_QFORMAT_INT4) {
         if (deep) qgemm_mfma<4, 64, 64><<<grid, 256, 0, s>>>(p);
         else if (rows64) qgemm_mfma<4, 64, 32><<<grid, 256, 0, s>>>(p);
@@ -421,6 +453,14 @@ hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float
         if (deep) qgemm_mfma<8, 64, 64><<<grid, 256, 0, s>>>(p);
         else if (rows64) qgemm_mfma<8, 64, 32><<<grid, 256, 0, s>>>(p);
         else qgemm_mfma<8, 128, 32><<<grid, 256, 0, s>>>(p);
+    }
+    if (sliced) {
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const bool res = resid != nullptr && out2 != nullptr && out2[0] != nullptr;
+        const uint64_t count = m * w0.n;
+        gemm_slices_sum<<<grid_for(count, 256, 4096), 256, 0, s>>>(p.partial, 2, count, out[0],
+                                                                  res ? resid[0] : nullptr, res ? out2[0] : nullptr);
     }
     return hipGetLastError();
 }

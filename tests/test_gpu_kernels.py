@@ -388,11 +388,17 @@ def test_rms_norm_then_quantized_projections_fuse(hip, m):
 @pytest.mark.parametrize("fmt,m,n,k,group", [(QuantFormat.INT4, 17, 100, 128, 128), (QuantFormat.INT8, 130, 257, 512, 64),
                                               (QuantFormat.INT4, 300, 512, 1024, 256),
                                               (QuantFormat.INT8, 200, 96, 2048, 128),
-                                              (QuantFormat.INT4, 512, 512, 4096, 128)])
+                                              (QuantFormat.INT4, 512, 512, 4096, 128),
+                                              (QuantFormat.INT4, 40, 64, 384, 32),
+                                              (QuantFormat.INT8, 33, 200, 384, 128),
+                                              (QuantFormat.INT4, 272, 11008, 256, 128)])
 def test_quantized_matmul_many_rows_on_matrix_cores(hip, fmt, m, n, k, group):
     """m > 16: the fp16 matrix-core path on split activations. Rows span nine
     orders of magnitude (each is split against its own maximum) and row 0 is
-    all zeros."""
+    all zeros. The shapes reach each block form: k in two slices of 128-row
+    blocks (small grids whose half k is a whole number of groups and 128-k
+    superblocks), 64-row blocks with 64-k stages (k 128, 384 at group 128) or
+    32-k stages (group 32), and 128-row blocks (more than 256 of them)."""
     r = rng(m + n + k + group)
     w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
     mag = (10.0 ** r.uniform(-6, 3, m)).astype(np.float32)

@@ -17,8 +17,9 @@
 // inside the 1e-4 bound.
 //
 // Kernels
-//  * split_rows: one block per row: E, then hi/lo in fp16 ([m][k] each)
-//    and E per row into the workspace;
+//  * split_rows: one block per row: E, then hi/lo in fp16 ([m][k] each,
+//    every group of 8 along k in the order kPerm8) and E per row into the
+//    workspace;
 //  * qgemm_mfma: 128 x 128 output tiles, 4 waves of 64 x 64 (4 x 4 MFMA
 //    tiles of 16 x 16), k in stages of 32 through double-buffered LDS; or
 //    64 x 128 tiles (waves of 32 x 64) in stages of 32 or 64. The weight
@@ -28,6 +29,8 @@
 #include "common.h"
 #include "kernels.h"
 #include "starlight_hip.h"
+
+#include <type_traits>
 
 namespace slhip {
 namespace {
@@ -59,8 +62,14 @@ __device__ __forceinline__ float4 act4(const float4* row, const float4* urow, ui
     return v;
 }
 
+// Within every aligned group of 8 along k, position j of the split
+// activations and of the converted codes holds element kPerm8[j]: the order
+// in which the code conversion below takes nibble (and byte) pairs out of
+// a word. Both operands share it, so the products pair up as before.
+__device__ constexpr int kPerm8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+
 // Row r: E with max |a| < 2^E (0 for an all-zero row), then hi/lo of
-// a * 2^(15 - E); with u, of silu(a) * u. k % 4 == 0 and rows 16-byte
+// a * 2^(15 - E); with u, of silu(a) * u. k % 8 == 0 and rows 16-byte
 // aligned.
 __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, const float* __restrict__ u,
                                                   _Float16* __restrict__ hi, _Float16* __restrict__ lo,
@@ -80,18 +89,20 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, c
     if (mx != 0.f) frexpf(mx, &e);  // mx < 2^e
     if (threadIdx.x == 0) row_exp[r] = e;
     const int shift = kExpBias - e;
-    for (uint32_t i = threadIdx.x; i < k4; i += 256) {
-        const float4 v = act4(row, urow, i);
-        const float x[4] = {ldexpf(v.x, shift), ldexpf(v.y, shift), ldexpf(v.z, shift), ldexpf(v.w, shift)};
-        _Float16 h[4], l[4];
+    // eight elements per step, stored in the order kPerm8 (the order the
+    // weight conversion produces codes in)
+    for (uint32_t i = threadIdx.x; i < k4 / 2; i += 256) {
+        const float4 v0 = act4(row, urow, 2 * i), v1 = act4(row, urow, 2 * i + 1);
+        const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        v8h h, l;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            h[j] = static_cast<_Float16>(x[j]);
-            l[j] = static_cast<_Float16>(x[j] - static_cast<float>(h[j]));  // the subtraction is exact
+        for (int j = 0; j < 8; ++j) {
+            const float xs = ldexpf(x[kPerm8[j]], shift);
+            h[j] = static_cast<_Float16>(xs);
+            l[j] = static_cast<_Float16>(xs - static_cast<float>(h[j]));  // the subtraction is exact
         }
-        typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-        *reinterpret_cast<v4h*>(hi + r * k + 4 * i) = v4h{h[0], h[1], h[2], h[3]};
-        *reinterpret_cast<v4h*>(lo + r * k + 4 * i) = v4h{l[0], l[1], l[2], l[3]};
+        *reinterpret_cast<v8h*>(hi + r * k + 8 * i) = h;
+        *reinterpret_cast<v8h*>(lo + r * k + 8 * i) = l;
     }
 }
 
@@ -139,12 +150,47 @@ struct GemmArgs {
     float* partial;
 };
 
-// A signed nibble (two's complement) of byte b, bit offset 0 or 4, as fp16.
-__device__ __forceinline__ _Float16 nib(uint32_t word, int shift) {
-    return static_cast<_Float16>(static_cast<int>(word << (28 - shift)) >> 28);
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// Two codes held in the low bits of the two 16-bit halves of w (offset
+// binary, code + bias, at most 8 bits) as fp16: OR-ing them into the
+// mantissa of 1024 (0x6400) makes 1024 + code + bias exactly, and one packed
+// subtraction leaves the code.
+__device__ __forceinline__ uint32_t pair_f16(uint32_t w, uint32_t mask, float bias) {
+    const uint32_t x = (w & mask) | 0x64006400u;
+    v2h h = __builtin_bit_cast(v2h, x);
+    const _Float16 b = static_cast<_Float16>(1024.0f + bias);
+    h -= v2h{b, b};
+    return __builtin_bit_cast(uint32_t, h);
 }
 
-template <int BITS, int BM, int KS>
+// Eight signed codes as fp16 in the order kPerm8. INT4: one word, byte b
+// holding codes b (low nibble) and 4 + b (high); flipping bit 3 of every
+// nibble makes them offset binary (code + 8). INT8: two words (codes 0..3,
+// 4..7), bit 7 flipped (code + 128).
+template <int BITS>
+__device__ __forceinline__ v8h codes8(uint32_t w0, uint32_t w1) {
+    uint32_t d[4];
+    if constexpr (BITS == 4) {
+        const uint32_t x = w0 ^ 0x88888888u;
+        d[0] = pair_f16(x, 0x000F000Fu, 8.f);        // codes 0, 2
+        d[1] = pair_f16(x >> 4, 0x000F000Fu, 8.f);   // 4, 6
+        d[2] = pair_f16(x >> 8, 0x000F000Fu, 8.f);   // 1, 3
+        d[3] = pair_f16(x >> 12, 0x000F000Fu, 8.f);  // 5, 7
+    } else {
+        const uint32_t x = w0 ^ 0x80808080u, y = w1 ^ 0x80808080u;
+        d[0] = pair_f16(x, 0x00FF00FFu, 128.f);       // codes 0, 2
+        d[1] = pair_f16(y, 0x00FF00FFu, 128.f);       // 4, 6
+        d[2] = pair_f16(x >> 8, 0x00FF00FFu, 128.f);  // 1, 3
+        d[3] = pair_f16(y >> 8, 0x00FF00FFu, 128.f);  // 5, 7
+    }
+    return __builtin_bit_cast(v8h, d);
+}
+
+// GS: stages per quantization group known at compile time (4: 32-k stages,
+// group 128; 2: 64-k stages and group 128, or 32-k stages and group 64), or
+// 0 for any group (counted at run time).
+template <int BITS, int BM, int KS, int GS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qgemm_mfma(GemmArgs p) {
     static_assert(BM == 128 || BM == 64, "block rows");
     static_assert(KS == 32 || KS == 64, "stage depth");
@@ -228,29 +274,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
         }
         return r;
     };
-    // 16 codes (INT4: words x, y; INT8: x, y, z, w) as fp16 at dst
+    // 16 codes (INT4: words x, y; INT8: x, y, z, w) as fp16 at dst, each
+    // group of 8 in the order kPerm8
     auto put_codes = [&](_Float16* dst, uint32_t x, uint32_t y, uint32_t z, uint32_t w) {
-        v8h q0, q1;
-        if constexpr (BITS == 4) {
-            // byte b of word 0: k = b (low nibble), 4 + b (high); word 1: 8 + b, 12 + b
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                q0[b] = nib(x, 8 * b);
-                q0[4 + b] = nib(x, 8 * b + 4);
-                q1[b] = nib(y, 8 * b);
-                q1[4 + b] = nib(y, 8 * b + 4);
-            }
-        } else {
-            const uint32_t wd[4] = {x, y, z, w};
-#pragma unroll
-            for (int b = 0; b < 16; ++b) {
-                const _Float16 v = static_cast<_Float16>(static_cast<int>(wd[b / 4] << (24 - 8 * (b % 4))) >> 24);
-                if (b < 8) q0[b] = v;
-                else q1[b - 8] = v;
-            }
-        }
-        *reinterpret_cast<v8h*>(dst) = q0;
-        *reinterpret_cast<v8h*>(dst + 8) = q1;
+        *reinterpret_cast<v8h*>(dst) = BITS == 4 ? codes8<4>(x, 0u) : codes8<8>(x, y);
+        *reinterpret_cast<v8h*>(dst + 8) = BITS == 4 ? codes8<4>(y, 0u) : codes8<8>(z, w);
     };
     auto store_stage = [&](int buf, StageRegs r) {
         const uint4 rb = r.b;
@@ -294,7 +322,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
     StageRegs r0 = load_stage(0), r1 = load_stage(1);
     store_stage(0, r0);
     __syncthreads();
-    auto step = [&](uint32_t st, StageRegs mine, StageRegs next) -> StageRegs {
+    // One stage. FRESH: the first stage of a group (its first product
+    // starts the group's sums from zero); END: 1 the last stage of a group,
+    // -1 decided at run time (GS == 0, where the group sums are cleared).
+    auto step = [&](auto fresh_c, auto end_c, uint32_t st, StageRegs mine, StageRegs next) -> StageRegs {
+        constexpr bool FRESH = decltype(fresh_c)::value;
+        constexpr int END = decltype(end_c)::value;
         const int buf = st & 1;
         // this slot's stage is in LDS already; past the end the last stage
         // is loaded again, so every step issues the same loads and the
@@ -316,12 +349,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
                 const v8h al = *reinterpret_cast<const v8h*>(&as[buf][1][(BM / 2) * wm + 16 * i + lane % 16][kq]);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[j], tmp[i][j], 0, 0, 0);
+                    const v4f c = FRESH && h == 0 ? v4f{0.f, 0.f, 0.f, 0.f} : tmp[i][j];
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[j], c, 0, 0, 0);
                     tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[j], tmp[i][j], 0, 0, 0);
                 }
             }
         }
-        if (st % group_steps == group_steps - 1) {
+        if (END == 1 || (END == -1 && st % group_steps == group_steps - 1)) {
             // the group's scales, staged with this step's operands
             float sv[4];
 #pragma unroll
@@ -332,16 +366,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
                 for (int j = 0; j < 4; ++j) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(tmp[i][j][e], sv[j], acc[i][j][e]);
-                    tmp[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (END == -1) tmp[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
                 }
         }
         store_stage(buf ^ 1, next);  // after the last step: into a buffer nothing reads
         __syncthreads();
         return mine;
     };
-    for (uint32_t st = 0; st < steps; st += 2) {
-        r0 = step(st, r0, r1);
-        r1 = step(st + 1, r1, r0);
+    using T = std::true_type;
+    using F = std::false_type;
+    using E1 = std::integral_constant<int, 1>;
+    using E0 = std::integral_constant<int, 0>;
+    using ER = std::integral_constant<int, -1>;
+    if constexpr (GS == 4) {
+        for (uint32_t st = 0; st < steps; st += 4) {
+            r0 = step(T{}, E0{}, st, r0, r1);
+            r1 = step(F{}, E0{}, st + 1, r1, r0);
+            r0 = step(F{}, E0{}, st + 2, r0, r1);
+            r1 = step(F{}, E1{}, st + 3, r1, r0);
+        }
+    } else if constexpr (GS == 2) {
+        for (uint32_t st = 0; st < steps; st += 2) {
+            r0 = step(T{}, E0{}, st, r0, r1);
+            r1 = step(F{}, E1{}, st + 1, r1, r0);
+        }
+    } else {
+        for (uint32_t st = 0; st < steps; st += 2) {
+            r0 = step(F{}, ER{}, st, r0, r1);
+            r1 = step(F{}, ER{}, st + 1, r1, r0);
+        }
     }
 
     // lane holds rows 4 (lane / 16) + e of each row tile, column lane % 16
@@ -445,15 +498,26 @@ hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float
     const bool deep = rows64 && w0.group % 64 == 0;  // 64-k stages
     p.partial = sliced ? ws.data + part_at : nullptr;
     const dim3 grid(blocks, static_cast<unsigned>(rows64 ? (m + 63) / 64 : (m + 127) / 128), sliced ? 2u : 1u);
+    // stages per group when it is a compile-time form: 128 / KS for group 128
+    // (4 or 2), 2 for group 64 in 32-k stages; 0 otherwise
+    const int ks = deep ? 64 : 32;
+    const int gs = w0.group == 128 ? 128 / ks : w0.group == 64 && ks == 32 ? 2 : 0;
+#define SL_QGEMM(B, R, K)                                                    \
+    do {                                                                     \
+        if (gs == 4) qgemm_mfma<B, R, K, 4><<<grid, 256, 0, s>>>(p);          \
+        else if (gs == 2) qgemm_mfma<B, R, K, 2><<<grid, 256, 0, s>>>(p);     \
+        else qgemm_mfma<B, R, K, 0><<<grid, 256, 0, s>>>(p);                  \
+    } while (0)
     if (w0.format == SL_QFORMAT_INT4) {
-        if (deep) qgemm_mfma<4, 64, 64><<<grid, 256, 0, s>>>(p);
-        else if (rows64) qgemm_mfma<4, 64, 32><<<grid, 256, 0, s>>>(p);
-        else qgemm_mfma<4, 128, 32><<<grid, 256, 0, s>>>(p);
+        if (deep) SL_QGEMM(4, 64, 64);
+        else if (rows64) SL_QGEMM(4, 64, 32);
+        else SL_QGEMM(4, 128, 32);
     } else {
-        if (deep) qgemm_mfma<8, 64, 64><<<grid, 256, 0, s>>>(p);
-        else if (rows64) qgemm_mfma<8, 64, 32><<<grid, 256, 0, s>>>(p);
-        else qgemm_mfma<8, 128, 32><<<grid, 256, 0, s>>>(p);
+        if (deep) SL_QGEMM(8, 64, 64);
+        else if (rows64) SL_QGEMM(8, 64, 32);
+        else SL_QGEMM(8, 128, 32);
     }
+#undef SL_QGEMM
     if (sliced) {
         e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -700,12 +700,13 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
     const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
     const uint64_t mirror_at = (attention_workspace_floats(a) + 63) / 64 * 64;
     // The output projection is chained (it reads the mirror, not MergeHeads'
-    // output) only when the mirror fits; otherwise it runs on its own and
-    // reads MergeHeads' output, which must then be written.
+    // output) only for decode (at most 16 rows, the fused GEMV's) and when
+    // the mirror fits; otherwise it runs on its own and reads MergeHeads'
+    // output, which must then be written.
     const Logged* mm = mh && i + used < n ? &d->log[i + used] : nullptr;
     const bool chain = mm && mm->plan.code == SL_OP_MATMUL_NT && same_ref(mm->in[0], mh->out) &&
                        mfma_weight(d, *mm, 1) && mm->plan.batch * mm->plan.m == B * S && mm->plan.k == H * D &&
-                       mirror_at + B * S * H * D <= ws.floats;
+                       B * S <= 16 && mirror_at + B * S * H * D <= ws.floats;
     const bool merged_needed = mh != nullptr && !dead_after(d, i + used, mh->out, chain ? i + used : SIZE_MAX);
     // outputs of the merge kernel: no overlap with the cache, or with each other
     if (overlaps(att, cache) || (mh && overlaps(mh->out, cache)) ||

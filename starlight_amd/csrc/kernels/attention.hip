@@ -879,13 +879,78 @@ __global__ __launch_bounds__(256 * KH) void attn_prefill(Geo g, uint32_t qtiles)
     }
     if (t < g.seq) {
         const float inv = 1.0f / lsum;
-        float* orow = g.out + ((b * g.heads + h) * g.seq + t) * D + 4 * kk;
+        // [B, H, S, D], and MergeHeads' [B, S, H * D] (fused form)
+        float* orow = g.out != nullptr ? g.out + ((b * g.heads + h) * g.seq + t) * D + 4 * kk : nullptr;
+        float* mrow = g.merged != nullptr ? g.merged + ((b * g.seq + t) * g.heads + h) * D + 4 * kk : nullptr;
 #pragma unroll
-        for (int j = 0; j < D16; ++j)
-            *reinterpret_cast<float4*>(orow + 16 * j) =
-                make_float4(o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv);
+        for (int j = 0; j < D16; ++j) {
+            const float4 v = make_float4(o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv);
+            if (orow != nullptr) *reinterpret_cast<float4*>(orow + 16 * j) = v;
+            if (mrow != nullptr) *reinterpret_cast<float4*>(mrow + 16 * j) = v;
+        }
     }
     }
+}
+
+// ---- prefill, fused form: SplitHeads, Rope and KvAppend in one pass ----
+//
+// One block per token (b, t) of the chunk: the pair angles' sine and cosine
+// for its position (f64, as rope_vec4 and reference/rope.rs compute them,
+// once per token), then q [b, t, H * D] rotated into qr [b, h, t, D] (the
+// attention's input), k [b, t, Hkv * D] rotated into the cache's K row of
+// slot past + t, and v copied into its V row (reference/attention.rs:33-83).
+// Rotation x c - y s, x s + y c in f32, the expressions of rope_vec4: the
+// results equal the unfused ops' bit for bit.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_prep(Geo g, float* __restrict__ qr) {
+    prefetch_kernarg<arg_bytes<Geo, float*>()>();
+    __shared__ float sc[D];  // [D / 2] sine, [D / 2] cosine
+    constexpr uint32_t D4 = D / 4;
+    const uint32_t S = g.seq, H = g.heads, Hkv = g.kv_heads;
+    const uint64_t bt = blockIdx.x, b = bt / S, t = bt % S;
+    const uint32_t past = past_of(g);
+    const double position = static_cast<double>(g.pos[bt]);
+    for (uint32_t pair = threadIdx.x; pair < D / 2; pair += blockDim.x) {
+        const double exponent = 2.0 * static_cast<double>(pair) / static_cast<double>(D);
+        const double angle = position / pow(g.theta, exponent);
+        sc[pair] = static_cast<float>(sin(angle));
+        sc[D / 2 + pair] = static_cast<float>(cos(angle));
+    }
+    __syncthreads();
+    const bool neox = g.rope_variant == SL_ROPE_NEOX;
+    // items per head: NeoX the float4 c < D / 8 with its partner c + D / 8
+    // (pairs d, d + D / 2), GPT-J every float4 (pairs 2i, 2i + 1)
+    const uint32_t per_head = neox ? D / 8 : D4;
+    // rotates item c of the head row src into dst (float4 indices)
+    auto rotate_item = [&](const float4* src, float4* dst, uint32_t c) {
+        if (neox) {
+            const float4 x = src[c], y = src[c + D / 8];
+            const uint32_t p0 = 4 * c;
+            const float s0 = sc[p0], s1 = sc[p0 + 1], s2 = sc[p0 + 2], s3 = sc[p0 + 3];
+            const float c0 = sc[D / 2 + p0], c1 = sc[D / 2 + p0 + 1], c2 = sc[D / 2 + p0 + 2], c3 = sc[D / 2 + p0 + 3];
+            dst[c] = make_float4(x.x * c0 - y.x * s0, x.y * c1 - y.y * s1, x.z * c2 - y.z * s2, x.w * c3 - y.w * s3);
+            dst[c + D / 8] = make_float4(x.x * s0 + y.x * c0, x.y * s1 + y.y * c1, x.z * s2 + y.z * c2,
+                                         x.w * s3 + y.w * c3);
+        } else {
+            const float4 a = src[c];
+            const float s0 = sc[2 * c], c0 = sc[D / 2 + 2 * c], s1 = sc[2 * c + 1], c1 = sc[D / 2 + 2 * c + 1];
+            dst[c] = make_float4(a.x * c0 - a.y * s0, a.x * s0 + a.y * c0, a.z * c1 - a.w * s1, a.z * s1 + a.w * c1);
+        }
+    };
+    const float4* qrow = reinterpret_cast<const float4*>(g.q + bt * H * D);
+    for (uint32_t i = threadIdx.x; i < H * per_head; i += blockDim.x) {
+        const uint32_t h = i / per_head, c = i % per_head;
+        rotate_item(qrow + h * D4, reinterpret_cast<float4*>(qr + ((b * H + h) * S + t) * D), c);
+    }
+    float* krow = g.wcache + b * g.batch_stride + g.layer_offset + static_cast<uint64_t>(past + t) * Hkv * D;
+    const float4* ksrc = reinterpret_cast<const float4*>(g.k_new + bt * Hkv * D);
+    for (uint32_t i = threadIdx.x; i < Hkv * per_head; i += blockDim.x) {
+        const uint32_t h = i / per_head, c = i % per_head;
+        rotate_item(ksrc + h * D4, reinterpret_cast<float4*>(krow + h * D), c);
+    }
+    const float4* vsrc = reinterpret_cast<const float4*>(g.v_new + bt * Hkv * D);
+    float4* vrow = reinterpret_cast<float4*>(krow + g.parity_stride);
+    for (uint32_t i = threadIdx.x; i < Hkv * D4; i += blockDim.x) vrow[i] = vsrc[i];
 }
 
 }  // namespace
@@ -1034,7 +1099,33 @@ uint64_t paged_attention_workspace_floats(const PagedAttentionArgs& p) {
 
 hipError_t launch_attention_fused(const AttentionArgs& a, const Workspace& ws, hipStream_t s) {
     if (a.batch * a.heads * a.seq == 0 || a.head_dim == 0 || a.kv_heads == 0) return hipErrorNotSupported;
-    return launch_decode(a, make_geo(a, ws), ws, s, true);
+    const hipError_t d = launch_decode(a, make_geo(a, ws), ws, s, true);
+    if (d != hipErrorNotSupported) return d;
+    // Prefill: prefill_prep (SplitHeads, Rope, KvAppend), then attn_prefill
+    // writing the attention output and / or MergeHeads' layout. The rotated q
+    // goes to the workspace; the unit's other intermediates must be dead (no
+    // staging) and the output projection not chained.
+    const uint64_t qr_floats = a.batch * a.seq * a.heads * a.head_dim;
+    const bool aligned = aligned16(a.q) && aligned16(a.k_new) && aligned16(a.v_new) && aligned16(a.cache) &&
+                         (a.out == nullptr || aligned16(a.out)) && (a.merged == nullptr || aligned16(a.merged));
+    if (a.seq < 16 || !(a.head_dim == 64 || a.head_dim == 128) || !aligned || a.positions == nullptr ||
+        a.rope_variant > SL_ROPE_GPTJ || a.mirror != nullptr || a.q_split != nullptr || a.k_split != nullptr ||
+        a.v_split != nullptr || a.q_rot != nullptr || a.k_rot != nullptr || (a.out == nullptr && a.merged == nullptr) ||
+        qr_floats > ws.floats || a.batch * a.seq > 0x7fffffffull)
+        return hipErrorNotSupported;
+    float* qr = ws.data;
+    Geo g = make_geo(a, ws);
+    const unsigned tokens = static_cast<unsigned>(a.batch * a.seq);
+    if (a.head_dim == 64) prefill_prep<64><<<tokens, 256, 0, s>>>(g, qr);
+    else prefill_prep<128><<<tokens, 256, 0, s>>>(g, qr);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    g.q = qr;
+    const uint32_t qtiles = static_cast<uint32_t>((a.seq + kPfQ - 1) / kPfQ);
+    const dim3 grid((qtiles + 1) / 2, g.heads, static_cast<unsigned>(a.batch));
+    if (a.head_dim == 64) attn_prefill<64, 2><<<grid, 512, 0, s>>>(g, qtiles);
+    else attn_prefill<128, 2><<<grid, 512, 0, s>>>(g, qtiles);
+    return hipGetLastError();
 }
 
 hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStream_t s) {

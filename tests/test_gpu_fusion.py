@@ -1,7 +1,8 @@
 """Fused submission units on the GPU, against the oracle run op by op.
 
 The device fuses SplitHeads x3 + Rope x2 + CausalAttention + MergeHeads into
-the decode attention kernels. The split and rotated heads are written only
+the decode attention kernels, and for prefill chunks into one pass that
+splits, rotates and appends followed by the prefill attention. The split and rotated heads are written only
 when a later command of the same submission reads them (dead ones, every
 element overwritten before any read, are skipped). These tests lay the values
 out in one scratch buffer, make the intermediates dead with a later Scale over
@@ -31,6 +32,9 @@ CASES = [
     (1, 4, 4, 1, 0, 128, 16, RopeVariant.NEOX),         # first token
     (1, 32, 8, 1, 300, 64, 512, RopeVariant.NEOX),      # 1B-shaped decode step: head_dim 64, NeoX pairs across lanes
     (2, 8, 2, 3, 20, 64, 64, RopeVariant.NEOX),         # head_dim 64 NeoX, three-token chunk, batch 2
+    (1, 32, 8, 64, 0, 128, 128, RopeVariant.NEOX),      # 8B-shaped prefill of 64 tokens
+    (2, 8, 2, 40, 17, 64, 128, RopeVariant.GPTJ),       # prefill chunk after a prefix, batch 2, head_dim 64
+    (1, 4, 4, 20, 5, 128, 64, RopeVariant.NEOX),        # MHA prefill chunk of 20 after 5
 ]
 
 
@@ -143,21 +147,27 @@ def test_attention_group_fuses_and_matches(hip, case):
         assert fused >= 7
 
 
-def fusable(case):
+def fusable(case, live=False):
+    """Decode-sized units (at most 16 query rows per KV head) fuse into the
+    decode kernels, except NeoX at head_dim 192; prefill units (16 or more
+    tokens, head_dim 64 or 128) into the prefill pass, when every
+    intermediate is dead."""
     B, H, Hkv, S, past, D, max_seq, variant = case
-    return not (variant == RopeVariant.NEOX and D // 64 == 3)
+    if (H // Hkv) * S <= 16:
+        return not (variant == RopeVariant.NEOX and D // 64 == 3)
+    return not live and S >= 16 and D in (64, 128)
 
 
 @pytest.mark.parametrize("case", CASES[:2])
 def test_attention_group_with_live_intermediate_fuses_and_writes_it(hip, case):
     fused = run_group(hip, case, consume_intermediate=True)
-    assert fused >= 7 if fusable(case) else fused == 0
+    assert fused >= 7 if fusable(case, live=True) else fused == 0
 
 
 @pytest.mark.parametrize("case", CASES)
 def test_attention_group_keeps_every_live_intermediate(hip, case):
     fused = run_group(hip, case, consume_intermediate=False, keep_all=True)
-    assert fused >= 7 if fusable(case) else fused == 0
+    assert fused >= 7 if fusable(case, live=True) else fused == 0
 
 
 # The scratch layout of the last layer of an 8B-shaped decode step as the

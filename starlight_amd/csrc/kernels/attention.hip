@@ -19,8 +19,10 @@
 //  * attn_split / attn_merge — other decode shapes: one wave per
 //    (b, h, t, key chunk), score by wave reduction, then a merge kernel.
 //  * attn_prefill — prefill (16 or more queries, head_dim 64 or 128): a block
-//    owns 64 queries of one head and streams 32-key K/V tiles through LDS;
-//    both products run on the f32 matrix cores.
+//    owns 64 queries of one head (two query tiles in turn) and streams 32-key
+//    K/V tiles through LDS; both products run on the f32 matrix cores. In the
+//    fused form prefill_prep first splits, rotates and appends (one block per
+//    token) and attn_prefill writes MergeHeads' layout.
 #include "common.h"
 #include "kernels.h"
 #include "starlight_hip.h"

@@ -22,10 +22,12 @@
 //    workspace;
 //  * qgemm_mfma: 128 x 128 output tiles, 4 waves of 64 x 64 (4 x 4 MFMA
 //    tiles of 16 x 16), k in stages of 32 through double-buffered LDS; or
-//    64 x 128 tiles (waves of 32 x 64) in stages of 32 or 64. The weight
-//    stage is read from the tile layout (per 16-row tile and 128-k
+//    64 x 128 tiles (waves of 32 x 64) in stages of 32 or 64; a grid z of
+//    2 cuts k in two slices whose partial sums gemm_slices_sum adds. The
+//    weight stage is read from the tile layout (per 16-row tile and 128-k
 //    superblock; a 32-k stage is half of one 64-k half: 32 lanes x 8 bytes
-//    for INT4, x 16 bytes for INT8) and converted to fp16 codes in LDS.
+//    for INT4, x 16 bytes for INT8) and converted to fp16 codes in LDS
+//    (codes8: through the mantissa of 1024, no converts).
 #include "common.h"
 #include "kernels.h"
 #include "starlight_hip.h"

@@ -246,16 +246,26 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     // ---- activations first (the prologue waits for them only), then the
     // weight window: element float4 f = tid + kThreads * u of [m][k/4] ----
     const uint32_t total4 = M * K4;
+    // k % 256 == 0 keeps a wave's 64 float4 inside one row: run (u, wave)
+    // starts at float4 fb = wave * 64 + u * kThreads, row ru[u] = fb / k4,
+    // column cb[u] = fb % k4, all wave-uniform (a wave past the end takes
+    // the last run), so no lane divides.
+    uint32_t ru[F4], cb[F4];
+#pragma unroll
+    for (int u = 0; u < F4; ++u) {
+        const uint32_t fb = min(static_cast<uint32_t>(wave * kWave + kThreads * u), total4 - kWave);
+        ru[u] = __builtin_amdgcn_readfirstlane(fb / K4);
+        cb[u] = fb - ru[u] * K4;
+    }
     float4 v[F4], gv[F4];
 #pragma unroll
     for (int u = 0; u < F4; ++u) {
         v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (kThreads * u >= total4) continue;  // block-uniform: runs past the input load nothing
-        const uint32_t f = min(static_cast<uint32_t>(tid + kThreads * u), total4 - 1);
+        const uint32_t c4 = cb[u] + lane;
         // rows of a k slice are a_stride4 float4 apart
-        const uint32_t fa = SLICED ? f + (f / K4) * (a_stride4 - K4) : f;
-        v[u] = reinterpret_cast<const float4*>(a_slice)[fa];
-        if (p.gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(p.gamma)[f % K4];
+        v[u] = reinterpret_cast<const float4*>(a_slice)[ru[u] * a_stride4 + c4];
+        if (p.gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(p.gamma)[c4];
     }
     // Output element e of the block's [tiles][16][m] results: its segment
     // and offset, false past the segment's rows.
@@ -287,26 +297,6 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     for (int u = 0; u < F4; ++u)
         if (tid + kThreads * u >= total4) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
 
-    // Row of the wave-uniform run (u, wave): k % 256 == 0 keeps a wave's 64
-    // float4 inside one row. Each wave reduces the rows w, w + 8 over the
-    // (u, wave) partials in a fixed order.
-    auto row_reduce = [&](bool is_max) {
-        __syncthreads();
-        for (uint32_t r = wave; r < M; r += kWaves) {
-            // kMaxF4 x W partials, one per lane for 8 waves, two for 16
-            float x = 0.f;
-#pragma unroll
-            for (int e0 = 0; e0 < kMaxF4 * kWaves; e0 += kWave) {
-                const int e = e0 + lane, u = e / kWaves, w = e % kWaves;
-                const uint32_t fb = static_cast<uint32_t>(w) * kWave + kThreads * u;
-                if (fb < total4 && fb / K4 == r) x = e0 == 0 ? red[u][w] : (is_max ? fmaxf(x, red[u][w]) : x + red[u][w]);
-            }
-            x = is_max ? wave_max(x) : wave_sum(x);
-            if (lane == 0) row_val[r] = x;
-        }
-        __syncthreads();
-    };
-
     if (p.gamma != nullptr) {
 #pragma unroll
         for (int u = 0; u < F4; ++u) {
@@ -318,13 +308,29 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
             ss = wave_sum(ss);
             if (lane == 0) red[u][wave] = ss;
         }
-        row_reduce(false);
+        // Each wave sums the rows w, w + W over the (u, wave) partials of
+        // their runs in a fixed order, and stores the row's 1 / rms.
+        __syncthreads();
         const float kf = static_cast<float>(K);
+        for (uint32_t r = wave; r < M; r += kWaves) {
+            // kMaxF4 x W partials, one per lane for 8 waves, two for 16
+            const uint32_t lo = r * K4, hi = lo + K4;
+            float x = 0.f;
+#pragma unroll
+            for (int e0 = 0; e0 < kMaxF4 * kWaves; e0 += kWave) {
+                const int e = e0 + lane, u = e / kWaves, w = e % kWaves;
+                const uint32_t fb = static_cast<uint32_t>(w) * kWave + kThreads * u;
+                if (fb < total4 && fb >= lo && fb < hi) x = e0 == 0 ? red[u][w] : x + red[u][w];
+            }
+            x = wave_sum(x);
+            if (lane == 0) row_val[r] = 1.0f / sqrtf(x / kf + p.eps);
+        }
+        __syncthreads();
 #pragma unroll
         for (int u = 0; u < F4; ++u) {
             const uint32_t f = tid + kThreads * u;
             if (f < total4) {
-                const float inv = 1.0f / sqrtf(row_val[f / K4] / kf + p.eps);
+                const float inv = row_val[ru[u]];
                 const float4 g = gv[u];
                 v[u].x = (v[u].x * inv) * g.x;
                 v[u].y = (v[u].y * inv) * g.y;
@@ -346,13 +352,12 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     for (int u = 0; u < F4; ++u) {
         const uint32_t fb = static_cast<uint32_t>(wave) * kWave + kThreads * u;
         if (fb >= total4) continue;  // whole wave past the end
-        const uint32_t f = tid + kThreads * u;
-        const uint32_t r = f / K4, c4 = f % K4;
+        const uint32_t r = ru[u], c4 = cb[u] + lane;
         const float mx = wave_max(fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
         int ex = 0;
         if (mx != 0.f) frexpf(mx, &ex);  // max|x| < 2^ex
         const int shift = 22 - ex;
-        if (lane == 0) cfac[r * chunks + c4 / 64] = ldexpf(1.0f, ex - 22 - (BITS == 4 ? 4 : 0));
+        if (lane == 0) cfac[r * chunks + cb[u] / 64] = ldexpf(1.0f, ex - 22 - (BITS == 4 ? 4 : 0));
         // X from one fma: with |x * 2^shift| <= 2^22, y = x * 2^shift +
         // 1.5 * 2^23 rounds to an integer (ties to even, as rintf) and
         // bits(y) = 0x4B400000 + X. X + 0x808080 lies in [0, 2^24) and its

@@ -63,6 +63,25 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(lane_value(r, 0), lane_value(r, 16)), fmaxf(lane_value(r, 32), lane_value(r, 48)));
 }
 
+// The largest v of the wave, for values ordered as unsigned integers (such
+// as the bit patterns of non-negative floats): one DPP max per step within
+// the rows (a float max would first quiet each operand), then the four rows
+// in scalar registers.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, static_cast<uint32_t>(dpp_i<kDppXor1>(static_cast<int>(v))));
+    v = max(v, static_cast<uint32_t>(dpp_i<kDppXor2>(static_cast<int>(v))));
+    v = max(v, static_cast<uint32_t>(dpp_i<kDppHalfMirror>(static_cast<int>(v))));
+    v = max(v, static_cast<uint32_t>(dpp_i<kDppMirror>(static_cast<int>(v))));
+    const uint32_t a = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0));
+    const uint32_t b = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16));
+    const uint32_t c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32));
+    const uint32_t d = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 48));
+    // (each pair's max kept scalar: a three-input max would go to the VALU)
+    const uint32_t ab = __builtin_amdgcn_readfirstlane(max(a, b));
+    const uint32_t cd = __builtin_amdgcn_readfirstlane(max(c, d));
+    return max(ab, cd);
+}
+
 // Block-wide sum/max for blocks of up to 1024 threads; every thread gets the
 // result. `scratch` needs blockDim.x / 64 floats of LDS.
 __device__ __forceinline__ float block_sum(float v, float* scratch) {

@@ -260,12 +260,14 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     float4 v[F4], gv[F4];
 #pragma unroll
     for (int u = 0; u < F4; ++u) {
-        v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (kThreads * u >= total4) continue;  // block-uniform: runs past the input load nothing
-        const uint32_t c4 = cb[u] + lane;
-        // rows of a k slice are a_stride4 float4 apart
-        v[u] = reinterpret_cast<const float4*>(a_slice)[ru[u] * a_stride4 + c4];
-        if (p.gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(p.gamma)[c4];
+        if (kThreads * u < total4) {  // block-uniform: runs past the input load nothing
+            const uint32_t c4 = cb[u] + lane;
+            // rows of a k slice are a_stride4 float4 apart
+            v[u] = reinterpret_cast<const float4*>(a_slice)[ru[u] * a_stride4 + c4];
+            if (p.gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(p.gamma)[c4];
+        } else {
+            v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     }
     // Output element e of the block's [tiles][16][m] results: its segment
     // and offset, false past the segment's rows.
@@ -293,9 +295,10 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
 #pragma unroll
     for (int i = 0; i < PF; ++i) fetch(win[i], i);
     const float res0 = *global_ptr(res_src);
+    // a wave past the input (wave-uniform: whole runs) loaded the last run again
 #pragma unroll
     for (int u = 0; u < F4; ++u)
-        if (tid + kThreads * u >= total4) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (static_cast<uint32_t>(wave) * kWave + kThreads * u >= total4) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
 
     if (p.gamma != nullptr) {
 #pragma unroll
@@ -348,48 +351,54 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     // chunks, each with its chunk's factor 2^(E-22) (2^(E-26) for INT4,
     // whose operands are the signed bytes 16 q).
     const uint32_t chunks = K / 256;
+    int8_t* const limb_lane = limbs + 4 * lane;  // this lane's word of a limb row's run
 #pragma unroll
     for (int u = 0; u < F4; ++u) {
         const uint32_t fb = static_cast<uint32_t>(wave) * kWave + kThreads * u;
         if (fb >= total4) continue;  // whole wave past the end
-        const uint32_t r = ru[u], c4 = cb[u] + lane;
-        const float mx = wave_max(fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
-        int ex = 0;
-        if (mx != 0.f) frexpf(mx, &ex);  // max|x| < 2^ex
+        const uint32_t r = ru[u];
+        // max|x| of the chunk as a bit pattern (non-negative floats order as
+        // unsigned integers) and ex = its biased exponent - 126: frexp's
+        // exponent, max|x| < 2^ex. A zero or subnormal maximum gives -126;
+        // such a chunk's limbs are then at most 2^9 and its factor 2^(ex-22)
+        // underflows to zero, as with frexp's smaller exponent.
+        const uint32_t mb = wave_max_u32(__float_as_uint(
+            fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w)))));
+        const int ex = static_cast<int>(mb >> 23) - 126;
         const int shift = 22 - ex;
         if (lane == 0) cfac[r * chunks + cb[u] / 64] = ldexpf(1.0f, ex - 22 - (BITS == 4 ? 4 : 0));
         // X from one fma: with |x * 2^shift| <= 2^22, y = x * 2^shift +
         // 1.5 * 2^23 rounds to an integer (ties to even, as rintf) and
         // bits(y) = 0x4B400000 + X. X + 0x808080 lies in [0, 2^24) and its
-        // bytes b_i satisfy X = sum (b_i - 128) 256^i, so the bytes of
-        // (X + 0x808080) ^ 0x808080 are the three signed limbs; v_perm
-        // gathers byte i of the four elements into limb word i. A chunk
-        // whose 2^shift is not a normal float (max|x| < 2^-105) scales in
-        // two exact steps.
+        // bytes b_i satisfy X = sum (b_i - 128) 256^i; v_perm gathers byte i
+        // of the four elements into limb word i, and flipping the top bit
+        // of every byte of a limb word makes its bytes the signed limbs. A
+        // chunk whose 2^shift is not a normal float (max|x| < 2^-105)
+        // scales in two exact steps.
         const float xe[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
         uint32_t y[4];
         if (shift <= 127) {  // wave-uniform
             const float s2 = __uint_as_float(static_cast<uint32_t>(shift + 127) << 23);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                y[e] = (__float_as_uint(fmaf(xe[e], s2, 12582912.0f)) - 0x4ABF7F80u) ^ 0x808080u;
+                y[e] = __float_as_uint(fmaf(xe[e], s2, 12582912.0f)) - 0x4ABF7F80u;
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float xs = xe[e] * 0x1p127f;  // exact: |x| < 2^-105
-                y[e] = (__float_as_uint(fmaf(xs, ldexpf(1.0f, shift - 127), 12582912.0f)) - 0x4ABF7F80u) ^ 0x808080u;
+                y[e] = __float_as_uint(fmaf(xs, ldexpf(1.0f, shift - 127), 12582912.0f)) - 0x4ABF7F80u;
             }
         }
         const uint32_t lo01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);  // y0.b0 y1.b0 y0.b1 y1.b1
         const uint32_t lo23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
         const uint32_t hi01 = __builtin_amdgcn_perm(y[1], y[0], 0x07030602u);  // y0.b2 y1.b2 ..
         const uint32_t hi23 = __builtin_amdgcn_perm(y[3], y[2], 0x07030602u);
-        const uint32_t packed[3] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u),
-                                    __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
-                                    __builtin_amdgcn_perm(hi23, hi01, 0x05040100u)};
+        const uint32_t packed[3] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u,
+                                    __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u,
+                                    __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u};
 #pragma unroll
-        for (int limb = 0; limb < 3; ++limb)
-            *reinterpret_cast<uint32_t*>(limbs + (limb * M + r) * RS + 4 * c4) = packed[limb];
+        for (int limb = 0; limb < 3; ++limb)  // row limb * M + r, columns 4 cb[u] + 4 lane
+            *reinterpret_cast<uint32_t*>(limb_lane + ((limb * M + r) * RS + 4 * cb[u])) = packed[limb];
     }
     __syncthreads();
 

@@ -1048,6 +1048,11 @@ sl_status sl_hip_device_create(int ordinal, sl_hip_device** out) {
         delete d;
         return SL_ERR_EXECUTION;
     }
+    // Every kernel file's code object now rather than inside the first
+    // submission that needs it (about 5 ms of a first 8B prefill). A file
+    // that does not load here fails at its first launch with that error.
+    (void)slhip::preload_code();
+    (void)hipGetLastError();
     const uint64_t ws_bytes = slhip::workspace_bytes_setting();
     if (hipMalloc(reinterpret_cast<void**>(&d->workspace), ws_bytes) != hipSuccess) {
         (void)hipStreamDestroy(d->stream);

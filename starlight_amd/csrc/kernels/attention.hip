@@ -1185,4 +1185,12 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
     return hipGetLastError();
 }
 
+// Loads this file's code object now: HIP loads one at the first use of
+// any of its kernels, which otherwise lands inside the first submission
+// that needs it (about 1-2 ms each, more for large objects).
+hipError_t load_code_attention() {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&attn_split<1>));
+}
+
 }  // namespace slhip

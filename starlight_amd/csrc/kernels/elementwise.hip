@@ -131,4 +131,12 @@ hipError_t launch_copy(const float* src, float* dst, uint64_t n, hipStream_t s) 
     return launch_ew<Ew::Copy>(src, nullptr, dst, n, 0.f, s);
 }
 
+// Loads this file's code object now: HIP loads one at the first use of
+// any of its kernels, which otherwise lands inside the first submission
+// that needs it (about 1-2 ms each, more for large objects).
+hipError_t load_code_elementwise() {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&set_words));
+}
+
 }  // namespace slhip

@@ -30,6 +30,32 @@ struct Workspace {
 };
 
 // ---- elementwise (reference/elementwise.rs) ----
+// Each kernel file's code object, loaded ahead of its first launch (HIP
+// loads one at the first use of any of its kernels); preload_code loads
+// them all and returns the first error.
+hipError_t load_code_attention();
+hipError_t load_code_elementwise();
+hipError_t load_code_layout();
+hipError_t load_code_matmul();
+hipError_t load_code_norm_softmax();
+hipError_t load_code_qgemm_mfma();
+hipError_t load_code_qgemv_fused();
+hipError_t load_code_qgemv_mfma();
+hipError_t load_code_qmatmul();
+hipError_t load_code_rope();
+inline hipError_t preload_code() {
+    hipError_t (*const loads[])() = {load_code_attention, load_code_elementwise, load_code_layout,
+                                     load_code_matmul,    load_code_norm_softmax, load_code_qgemm_mfma,
+                                     load_code_qgemv_fused, load_code_qgemv_mfma, load_code_qmatmul,
+                                     load_code_rope};
+    hipError_t first = hipSuccess;
+    for (auto load : loads) {
+        const hipError_t e = load();
+        if (first == hipSuccess) first = e;
+    }
+    return first;
+}
+
 hipError_t launch_add(const float* a, const float* b, float* out, uint64_t n, hipStream_t s);
 hipError_t launch_mul(const float* a, const float* b, float* out, uint64_t n, hipStream_t s);
 hipError_t launch_scale(const float* x, float* out, uint64_t n, float factor, hipStream_t s);

@@ -154,4 +154,12 @@ hipError_t launch_kv_append(const float* k, const float* v, float* cache, uint64
     return hipGetLastError();
 }
 
+// Loads this file's code object now: HIP loads one at the first use of
+// any of its kernels, which otherwise lands inside the first submission
+// that needs it (about 1-2 ms each, more for large objects).
+hipError_t load_code_layout() {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&gather_rows));
+}
+
 }  // namespace slhip

@@ -99,4 +99,12 @@ hipError_t launch_matmul(const float* a, const float* b, float* out, uint64_t ba
     return hipSuccess;
 }
 
+// Loads this file's code object now: HIP loads one at the first use of
+// any of its kernels, which otherwise lands inside the first submission
+// that needs it (about 1-2 ms each, more for large objects).
+hipError_t load_code_matmul() {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&sgemm_tiled<true>));
+}
+
 }  // namespace slhip

@@ -179,4 +179,12 @@ hipError_t launch_softmax(const float* x, float* out, uint64_t rows, uint64_t co
     return hipGetLastError();
 }
 
+// Loads this file's code object now: HIP loads one at the first use of
+// any of its kernels, which otherwise lands inside the first submission
+// that needs it (about 1-2 ms each, more for large objects).
+hipError_t load_code_norm_softmax() {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&rms_norm_any));
+}
+
 }  // namespace slhip

@@ -538,4 +538,12 @@ hipError_t launch_qgemm_mfma(const float* a, const QuantWeight& w, float* out, u
     return launch_qgemm_multi(a, ws1, outs, 1, m, ws, s);
 }
 
+// Loads this file's code object now: HIP loads one at the first use of
+// any of its kernels, which otherwise lands inside the first submission
+// that needs it (about 1-2 ms each, more for large objects).
+hipError_t load_code_qgemm_mfma() {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_rows));
+}
+
 }  // namespace slhip

@@ -69,7 +69,6 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* global_ptr(T* p)
 
 // W waves per block (8 or 16); each thread holds at most kMaxF4 float4 of
 // activations (F4: this launch's count), so a block holds max_elems(W).
-constexpr int kMaxWaves = 16;
 // Bytes between consecutive rows of the limb matrices beyond k: the A
 // operand of a 64-k step reads the same 16-byte columns of several rows,
 // and rows a multiple of the bank width apart would all hit the same banks.
@@ -721,6 +720,14 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
                                                                    residual ? f.out2[0] : nullptr);
     }
     return hipGetLastError();
+}
+
+// Loads this file's code object now: HIP loads one at the first use of
+// any of its kernels, which otherwise lands inside the first submission
+// that needs it (about 1-2 ms each, more for large objects).
+hipError_t load_code_qgemv_fused() {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&qgemv_slices_sum));
 }
 
 }  // namespace slhip

@@ -314,4 +314,12 @@ hipError_t launch_qgemv_mfma(const float* a, const QuantWeight& w, float* out, u
     return hipGetLastError();
 }
 
+// Loads this file's code object now: HIP loads one at the first use of
+// any of its kernels, which otherwise lands inside the first submission
+// that needs it (about 1-2 ms each, more for large objects).
+hipError_t load_code_qgemv_mfma() {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&qgemv_reduce));
+}
+
 }  // namespace slhip

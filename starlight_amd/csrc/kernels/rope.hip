@@ -177,4 +177,12 @@ hipError_t launch_rope(const float* x, const uint32_t* positions, float* out, ui
     return hipGetLastError();
 }
 
+// Loads this file's code object now: HIP loads one at the first use of
+// any of its kernels, which otherwise lands inside the first submission
+// that needs it (about 1-2 ms each, more for large objects).
+hipError_t load_code_rope() {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&rope_kernel<false>));
+}
+
 }  // namespace slhip

@@ -348,6 +348,41 @@ def test_quantized_matmul_parity(hip, fmt, m, n, k, group):
         assert_normwise(got[i], want.reshape(m, n)[i])
 
 
+@pytest.mark.parametrize("fmt", [QuantFormat.INT4, QuantFormat.INT8])
+@pytest.mark.parametrize("m,n,k", [(1, 96, 4096), (4, 64, 2048), (8, 80, 4096), (3, 48, 14336)])
+def test_quantized_gemv_extreme_activations(hip, fmt, m, n, k):
+    """The GEMV's activation limbs take each 256-element chunk's exponent
+    from its largest |x|: rows here are all zero, around 1e-33 (the chunk's
+    scale 2^(22 - E) is not a normal float, so it is applied in two steps),
+    around 1e25, and rows whose chunks span twelve orders of magnitude."""
+    r = rng(m * 7 + n + k)
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    chunk_mag = 10.0 ** (np.arange(k // 256) % 13 - 6.0)
+    kinds = ["zero", "tiny", "huge", "spread"]
+    for i in range(m):
+        kind = kinds[i % 4]
+        if kind == "zero":
+            a[i] = 0.0
+        elif kind == "tiny":
+            a[i] *= np.float32(1e-33)
+        elif kind == "huge":
+            a[i] *= np.float32(1e25)
+        else:
+            a[i] *= np.repeat(chunk_mag, 256).astype(np.float32)
+    wr, wv, deq = quant_weight(hip, w, fmt, 128)
+    _, ar = put(hip, a.ravel())
+    _, orf = out_buf(hip, m * n)
+    hip.dispatch(Op.matmul_nt(), [ar, wr], [Value.f32([1, m, k]), wv], [orf], [Value.f32([1, m, n])])
+    want = oracle.matmul_nt(a.ravel(), deq, 1, m, k, n).reshape(m, n)
+    got = read(hip, orf).reshape(m, n)
+    for i in range(m):
+        if kinds[i % 4] == "zero":
+            np.testing.assert_array_equal(got[i], np.zeros(n, np.float32))
+        else:
+            assert_normwise(got[i], want[i])
+
+
 @pytest.mark.parametrize("m", [1, 4, 8])
 def test_rms_norm_then_quantized_projections_fuse(hip, m):
     """RmsNorm and two MatMulNT reading its output run as one fused GEMV with

@@ -49,7 +49,6 @@ constexpr uint64_t kMirrorMaxElements = 1ull << 22;        // host copy of u32 b
 constexpr uint64_t kSmallUploadWords = 64;                  // uploads carried in kernel arguments, at most
 constexpr uint64_t kWorkspaceBytes = 512ull << 20;          // split-K partials, SwiGlu intermediates
 constexpr uint64_t kRopeTableFloats = 16 * 512;  // tokens x head_dim of one decode submission
-constexpr uint64_t kCounterWords = 1ull << 16;              // cross-block completion counters (kept at zero)
 constexpr uint64_t kIdScratchElements = 1ull << 20;         // host scratch for unmirrored id checks
 
 struct Buffer {
@@ -94,7 +93,6 @@ struct Device : BufferView {
     float* workspace = nullptr;
     uint64_t workspace_floats = 0;
     float* static_scratch = nullptr;  // this GPU's static array (no-allocation entry point)
-    uint32_t* counters = nullptr;
     std::vector<uint32_t> id_scratch;
     Error last;
     // deferred submission
@@ -486,7 +484,7 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
         if (rows <= 16) return 0;  // few rows the fused GEMV did not take: one launch each
         const int other_many = add ? residual_port(*add, outs[0], count, nullptr, 0) : -1;
         if (used + (other_many >= 0 ? 1 : 0) == 1) return 0;
-        const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
+        const Workspace ws{d->workspace, d->workspace_floats};
         const float* a = norm ? fptr(d, norm->out) : f.a;
         if (!qgemm_mfma_takes(a, f.w, cnt, rows, ws)) return 0;
         set_residual(other_many);
@@ -542,7 +540,7 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
                 e = launch_swiglu(norm ? f.normed : f.a, weight_ref(d, c1.in[1], c1.plan.quant[1]),
                                   weight_ref(d, c1.in[2], c1.plan.quant[2]), weight_ref(d, c1.in[3], c1.plan.quant[3]),
                                   fptr(d, c1.out), rows, hidden, inter,
-                                  Workspace{d->workspace, d->workspace_floats, d->counters, kCounterWords},
+                                  Workspace{d->workspace, d->workspace_floats},
                                   d->stream, other >= 0 ? fptr(d, add->in[other]) : nullptr,
                                   other >= 0 ? fptr(d, add->out) : nullptr);
             if (other >= 0) ++used;
@@ -580,7 +578,7 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
         }
         e = mfma_weight(d, c1, 3) ? launch_qgemv_fused(g, d->stream) : hipErrorNotSupported;
         if (e == hipErrorNotSupported) {
-            const Workspace rest = Workspace{d->workspace, d->workspace_floats, d->counters, kCounterWords}.after(
+            const Workspace rest = Workspace{d->workspace, d->workspace_floats}.after(
                 d->workspace_floats / 2);
             e = launch_linear(h, down, g.out[0], rows, hidden, inter, rest, d->stream);
         } else if (g.epilogue == kFusedResidual) {
@@ -697,7 +695,7 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
                     ap.max_seq, ap.scale, dyn_of(d, at)};
     // Workspace: the decode partials, the mirror of the merged heads, then
     // the staged intermediates.
-    const Workspace ws{d->workspace, d->workspace_floats, d->counters, kCounterWords};
+    const Workspace ws{d->workspace, d->workspace_floats};
     const uint64_t mirror_at = (attention_workspace_floats(a) + 63) / 64 * 64;
     // The output projection is chained (it reads the mirror, not MergeHeads'
     // output) only for decode (at most 16 rows, the fused GEMV's) and when
@@ -861,7 +859,7 @@ hipError_t run_log(Device* d) {
         if (used == 0) {
             const Logged& c = d->log[i];
             e = launch(d, c.plan, c.in, &c.out, dyn_of(d, c),
-                       Workspace{d->workspace, d->workspace_floats, d->counters, kCounterWords});
+                       Workspace{d->workspace, d->workspace_floats});
             if (e != hipSuccess) return e;
             used = 1;
         }
@@ -1060,18 +1058,10 @@ sl_status sl_hip_device_create(int ordinal, sl_hip_device** out) {
         return SL_ERR_OUT_OF_MEMORY;
     }
     d->workspace_floats = ws_bytes / 4;
-    if (hipMalloc(reinterpret_cast<void**>(&d->counters), slhip::kCounterWords * 4) != hipSuccess ||
-        hipMemset(d->counters, 0, slhip::kCounterWords * 4) != hipSuccess) {
-        (void)hipFree(d->workspace);
-        (void)hipStreamDestroy(d->stream);
-        delete d;
-        return SL_ERR_OUT_OF_MEMORY;
-    }
     if (hipMalloc(reinterpret_cast<void**>(&d->rope_tab), slhip::kRopeTableFloats * 4) != hipSuccess ||
         hipMalloc(reinterpret_cast<void**>(&d->dyn), slhip::kLogFlushLength * sizeof(uint32_t)) != hipSuccess) {
         (void)hipGetLastError();
         if (d->rope_tab) (void)hipFree(d->rope_tab);
-        (void)hipFree(d->counters);
         (void)hipFree(d->workspace);
         (void)hipStreamDestroy(d->stream);
         delete d;
@@ -1101,7 +1091,6 @@ void sl_hip_device_destroy(sl_hip_device* d) {
         if (b.tiles) (void)hipFree(b.tiles);
     }
     if (d->workspace) (void)hipFree(d->workspace);
-    if (d->counters) (void)hipFree(d->counters);
     if (d->rope_tab) (void)hipFree(d->rope_tab);
     (void)hipStreamDestroy(d->stream);
     delete d;
@@ -1174,8 +1163,7 @@ sl_status sl_hip_dispatch_noalloc(sl_hip_device* d, const sl_op* op, const sl_bu
     // past_len reaches the kernels as the scalar itself (no device word)
     const hipError_t e =
         slhip::launch(d, plan, inputs, &out, nullptr,
-                      slhip::Workspace{d->static_scratch, slhip::kStaticScratchFloats, d->counters,
-                                       slhip::kCounterWords});
+                      slhip::Workspace{d->static_scratch, slhip::kStaticScratchFloats});
     if (e != hipSuccess) return d->hip_fail(e);
     return SL_OK;
 }
@@ -1276,7 +1264,7 @@ sl_status sl_hip_paged_attention(sl_hip_device* d, const sl_op* op, const sl_buf
     if (slhip::paged_attention_workspace_floats(a) > d->workspace_floats)
         return d->fail(Error::unimplemented("paged attention partials exceed the device workspace"));
     const hipError_t e = slhip::launch_paged_attention(
-        a, slhip::Workspace{d->workspace, d->workspace_floats, d->counters, slhip::kCounterWords}, d->stream);
+        a, slhip::Workspace{d->workspace, d->workspace_floats}, d->stream);
     if (e == hipErrorNotSupported) return d->fail(Error::unimplemented("paged attention shape is not supported"));
     if (e != hipSuccess) return d->hip_fail(e);
     return SL_OK;

@@ -9,17 +9,13 @@
 
 namespace slhip {
 
-// Device-owned scratch passed to kernels that need it: `data` for partial
-// results and intermediates, `counters` for cross-block completion counts.
-// Every kernel that uses a counter leaves it at zero when it finishes, so
-// the region stays zero between launches without any memset.
+// Device-owned scratch passed to kernels that need it: partial results and
+// intermediates.
 struct Workspace {
     float* data;
     uint64_t floats;
-    uint32_t* counters;
-    uint64_t n_counters;
 
-    // The part of `data` after the first `used` floats (counters shared).
+    // The part of `data` after the first `used` floats.
     Workspace after(uint64_t used) const {
         Workspace w = *this;
         used = (used + 63) / 64 * 64;  // keep 256-byte alignment

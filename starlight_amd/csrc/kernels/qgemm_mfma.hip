@@ -72,7 +72,10 @@ __device__ constexpr int kPerm8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
 
 // Row r: E with max |a| < 2^E (0 for an all-zero row), then hi/lo of
 // a * 2^(15 - E); with u, of silu(a) * u. k % 8 == 0 and rows 16-byte
-// aligned.
+// aligned. NP > 0: the row's values stay in registers between the two
+// passes (thread t holds the 8-element groups t + 256 j, j < NP, so k <=
+// 2048 NP), and a and u are read once; NP == 0 reads the row twice.
+template <int NP>
 __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, const float* __restrict__ u,
                                                   _Float16* __restrict__ hi, _Float16* __restrict__ lo,
                                                   int* __restrict__ row_exp, uint32_t k) {
@@ -81,10 +84,26 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, c
     const float4* row = reinterpret_cast<const float4*>(a + r * k);
     const float4* urow = u != nullptr ? reinterpret_cast<const float4*>(u + r * k) : nullptr;
     const uint32_t k4 = k / 4;
+    const uint32_t groups = k4 / 2;  // eight elements each
+    float4 keep[NP > 0 ? 2 * NP : 1];
     float mx = 0.f;
-    for (uint32_t i = threadIdx.x; i < k4; i += 256) {
-        const float4 v = act4(row, urow, i);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    if constexpr (NP > 0) {
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            const uint32_t i = threadIdx.x + 256 * j;
+            if (i < groups) {
+                keep[2 * j] = act4(row, urow, 2 * i);
+                keep[2 * j + 1] = act4(row, urow, 2 * i + 1);
+                const float4 v0 = keep[2 * j], v1 = keep[2 * j + 1];
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))));
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+            }
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < k4; i += 256) {
+            const float4 v = act4(row, urow, i);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
     }
     mx = block_max(mx, scratch);
     int e = 0;
@@ -93,8 +112,7 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, c
     const int shift = kExpBias - e;
     // eight elements per step, stored in the order kPerm8 (the order the
     // weight conversion produces codes in)
-    for (uint32_t i = threadIdx.x; i < k4 / 2; i += 256) {
-        const float4 v0 = act4(row, urow, 2 * i), v1 = act4(row, urow, 2 * i + 1);
+    auto put8 = [&](uint32_t i, float4 v0, float4 v1) {
         const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         v8h h, l;
 #pragma unroll
@@ -105,6 +123,15 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, c
         }
         *reinterpret_cast<v8h*>(hi + r * k + 8 * i) = h;
         *reinterpret_cast<v8h*>(lo + r * k + 8 * i) = l;
+    };
+    if constexpr (NP > 0) {
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            const uint32_t i = threadIdx.x + 256 * j;
+            if (i < groups) put8(i, keep[2 * j], keep[2 * j + 1]);
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < groups; i += 256) put8(i, act4(row, urow, 2 * i), act4(row, urow, 2 * i + 1));
     }
 }
 
@@ -463,7 +490,12 @@ hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float
     _Float16* hi = reinterpret_cast<_Float16*>(ws.data);
     _Float16* lo = reinterpret_cast<_Float16*>(ws.data + lay.lo_at);
     int* row_exp = reinterpret_cast<int*>(ws.data + lay.exp_at);
-    split_rows<<<static_cast<unsigned>(m), 256, 0, s>>>(a, u, hi, lo, row_exp, static_cast<uint32_t>(w0.k));
+    // rows of up to 32768 elements stay in registers between the passes
+    const uint32_t kk = static_cast<uint32_t>(w0.k);
+    if (w0.k <= 2048 * 4) split_rows<4><<<static_cast<unsigned>(m), 256, 0, s>>>(a, u, hi, lo, row_exp, kk);
+    else if (w0.k <= 2048 * 8) split_rows<8><<<static_cast<unsigned>(m), 256, 0, s>>>(a, u, hi, lo, row_exp, kk);
+    else if (w0.k <= 2048 * 16) split_rows<16><<<static_cast<unsigned>(m), 256, 0, s>>>(a, u, hi, lo, row_exp, kk);
+    else split_rows<0><<<static_cast<unsigned>(m), 256, 0, s>>>(a, u, hi, lo, row_exp, kk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     GemmArgs p{};
@@ -543,7 +575,7 @@ hipError_t launch_qgemm_mfma(const float* a, const QuantWeight& w, float* out, u
 // that needs it (about 1-2 ms each, more for large objects).
 hipError_t load_code_qgemm_mfma() {
     hipFuncAttributes attr;
-    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_rows));
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&split_rows<0>));
 }
 
 }  // namespace slhip

@@ -401,6 +401,9 @@ int residual_port(const Logged& a, const sl_buffer_ref& o, uint64_t count, const
     return other;
 }
 
+// Whether `r` is dead after log[from..] (defined with the attention fusion below).
+bool dead_after(const Device* d, size_t from, const sl_buffer_ref& r, size_t skip_reads = SIZE_MAX);
+
 // Tries to run log[i..] as one fused unit; returns the number of commands it
 // covered (0: nothing launched, run log[i] alone).
 size_t try_fuse(Device* d, size_t i, hipError_t* err) {
@@ -489,11 +492,13 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
         if (!qgemm_mfma_takes(a, f.w, cnt, rows, ws)) return 0;
         set_residual(other_many);
         const bool residual = other_many >= 0;
+        if (residual) ++used;
+        // the product itself, when nothing after the Add reads it, is not written
+        if (residual && dead_after(d, i + used, outs[0])) f.out[0] = nullptr;
         e = norm ? launch_rms_norm(f.a, f.gamma, f.normed, rows, k, f.eps, d->stream) : hipSuccess;
         if (e == hipSuccess)
             e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream, nullptr, residual ? f.resid : nullptr,
                                    residual ? f.out2 : nullptr);
-        if (residual) ++used;
         *err = e;
         d->stats.fused_commands += used;
         return used;
@@ -542,7 +547,8 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
                                   fptr(d, c1.out), rows, hidden, inter,
                                   Workspace{d->workspace, d->workspace_floats},
                                   d->stream, other >= 0 ? fptr(d, add->in[other]) : nullptr,
-                                  other >= 0 ? fptr(d, add->out) : nullptr);
+                                  other >= 0 ? fptr(d, add->out) : nullptr,
+                                  other >= 0 && dead_after(d, i + used + 1, c1.out));
             if (other >= 0) ++used;
             *err = e;
             d->stats.fused_commands += used;
@@ -600,7 +606,7 @@ const uint32_t* dyn_of(const Device* d, const Logged& c) {
 // writing it (the final contents are those later writes either way).
 // `skip_reads` names a command whose reads do not count (one a fused unit
 // redirects elsewhere).
-bool dead_after(const Device* d, size_t from, const sl_buffer_ref& r, size_t skip_reads = SIZE_MAX) {
+bool dead_after(const Device* d, size_t from, const sl_buffer_ref& r, size_t skip_reads) {
     std::vector<std::pair<uint64_t, uint64_t>> live;
     if (r.len) live.push_back({r.offset, r.offset + r.len});
     for (size_t j = from; j < d->log.size() && !live.empty(); ++j) {

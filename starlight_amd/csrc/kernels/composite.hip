@@ -30,7 +30,7 @@ uint64_t swiglu_chunk_rows(uint64_t ws_floats, uint64_t inter) {
 
 hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up, const WeightRef& down,
                          float* out, uint64_t rows, uint64_t hidden, uint64_t inter, const Workspace& ws,
-                         hipStream_t s, const float* resid, float* out2) {
+                         hipStream_t s, const float* resid, float* out2, bool out_dead) {
     if (rows == 0) return hipSuccess;
     const uint64_t budget = ws.floats / 2;
     uint64_t chunk = swiglu_chunk_rows(ws.floats, inter);
@@ -79,7 +79,7 @@ hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef&
         if (down.quantized() && rc > 16 && qgemm_mfma_takes(g, dw, 1, rc, rest)) {
             // many rows: silu(g) * u formed by the down projection's
             // activation split (no h pass), the residual in its epilogue
-            float* outs[1] = {out_r};
+            float* outs[1] = {out_dead && out2_r != nullptr ? nullptr : out_r};
             float* out2s[1] = {out2_r};
             e = launch_qgemm_multi(g, dw, outs, 1, rc, rest, s, u, &resid_r, out2s);
         } else {

@@ -209,8 +209,9 @@ hipError_t launch_qgemm_mfma(const float* a, const QuantWeight& w, float* out, u
 // the same activations (one activation split, one launch): out[i] =
 // a * dequant(w[i])^T. With u, the activations are silu(a) * u (SwiGlu's
 // down projection, elementwise); with out2[i] set, also out2[i] = resid[i]
-// + out[i] (a residual Add). qgemm_mfma_takes says whether a launch would
-// run.
+// + out[i] (a residual Add), and out[i] may then be null (the product
+// itself not written, when nothing reads it). qgemm_mfma_takes says whether
+// a launch would run.
 bool qgemm_mfma_takes(const float* a, const QuantWeight* const* w, uint32_t nseg, uint64_t m, const Workspace& ws);
 hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float* const* out, uint32_t nseg,
                               uint64_t m, const Workspace& ws, hipStream_t s, const float* u = nullptr,
@@ -263,11 +264,12 @@ hipError_t launch_linear(const float* a, const WeightRef& w, float* out, uint64_
 // Rows per chunk of launch_swiglu for a workspace of ws_floats floats.
 uint64_t swiglu_chunk_rows(uint64_t ws_floats, uint64_t inter);
 // SwiGlu (reference/swiglu.rs): out = (silu(x Wg^T) * (x Wu^T)) Wd^T.
-// With out2, also out2 = resid + out (a residual Add after the SwiGlu).
+// With out2, also out2 = resid + out (a residual Add after the SwiGlu);
+// out_dead: nothing reads out afterwards, so the q-GEMM route may skip it.
 hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up,
                          const WeightRef& down, float* out, uint64_t rows, uint64_t hidden,
                          uint64_t inter, const Workspace& ws, hipStream_t s, const float* resid = nullptr,
-                         float* out2 = nullptr);
+                         float* out2 = nullptr, bool out_dead = false);
 // gate/up epilogue: h = silu(g) * u, elementwise over n values.
 hipError_t launch_silu_mul(const float* g, const float* u, float* h, uint64_t n, hipStream_t s);
 // RmsNormMatMul (reference/fused.rs): out = rms_norm(x, weight) W^T.

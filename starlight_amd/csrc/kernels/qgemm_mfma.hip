@@ -136,14 +136,15 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, c
 }
 
 // out[i] = the k slices' partial sums of element i, added in slice order;
-// with resid, out2[i] = resid[i] + out[i] (the residual Add's order).
+// with resid, out2[i] = resid[i] + out[i] (the residual Add's order), and
+// out may then be null (the sum itself not written).
 __global__ __launch_bounds__(256) void gemm_slices_sum(const float* __restrict__ partial, uint32_t slices,
                                                        uint64_t count, float* out, const float* resid, float* out2) {
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
          i += static_cast<uint64_t>(gridDim.x) * 256) {
         float v = partial[i];
         for (uint32_t z = 1; z < slices; ++z) v += partial[z * count + i];
-        out[i] = v;
+        if (out != nullptr) out[i] = v;
         if (out2 != nullptr) out2[i] = resid[i] + v;
     }
 }
@@ -444,7 +445,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q
                     p.partial[static_cast<uint64_t>(bz) * p.m * n + o] = val;
                     continue;
                 }
-                out[o] = val;
+                if (out != nullptr) out[o] = val;
                 if (out2 != nullptr) out2[o] = resid[o] + val;
             }
         }

@@ -358,9 +358,10 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         const uint32_t r = ru[u];
         // max|x| of the chunk as a bit pattern (non-negative floats order as
         // unsigned integers) and ex = its biased exponent - 126: frexp's
-        // exponent, max|x| < 2^ex. A zero or subnormal maximum gives -126;
-        // such a chunk's limbs are then at most 2^9 and its factor 2^(ex-22)
-        // underflows to zero, as with frexp's smaller exponent.
+        // exponent, max|x| < 2^ex. A zero or subnormal maximum gives -126:
+        // the chunk's X are then its values in units of 2^-148 (|X| < 2^22),
+        // which drops at most the last bit of a subnormal, and its factor
+        // 2^(ex-22) is itself subnormal (zero for INT4).
         const uint32_t mb = wave_max_u32(__float_as_uint(
             fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w)))));
         const int ex = static_cast<int>(mb >> 23) - 126;

@@ -89,8 +89,6 @@ struct Seg {
 };
 
 struct Args {
-    const float* a;
-    const float* gamma;
     float* normed;
     float eps;
     Seg seg[kFusedMaxSegs];
@@ -119,9 +117,13 @@ struct Item {
 // p.sb_total, and writes its partial sums m n floats after slice y - 1's
 // (the launcher adds the slices up). Every slice geometry follows from the
 // grid, so the arguments are the same as for one slice.
+// The activations a, the RMSNorm weight gamma (null: no norm) and the
+// m x k shape lead the arguments: the library is built to preload leading
+// scalar arguments into scalar registers, so the activation loads go out
+// at once, while the argument block is still being fetched.
 template <int BITS, int NT, int SPG, bool LR, int F4, int W, bool SLICED>
-__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(Args p) {
-    prefetch_kernarg<arg_bytes<Args>()>();
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(
+    const float* __restrict__ a_in, const float* __restrict__ gamma, uint32_t m_in, uint32_t k_in, Args p) {
     constexpr int kThreads = W * kWave, kWaves = W;
     static_assert(F4 <= kMaxF4, "activations per thread beyond the block's budget");
     constexpr int GPS = SPG == 1 ? 2 : 1;
@@ -136,13 +138,43 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
 
     const int tid = threadIdx.x, lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, kept in scalar registers
-    const uint32_t M = p.m, K = p.k, K4 = K / 4;
+    const uint32_t M = m_in, K = k_in, K4 = K / 4;
     const uint32_t ks = SLICED ? blockIdx.y : 0u;  // k slice
-    const float* const a_slice = SLICED ? p.a + static_cast<uint64_t>(ks) * K : p.a;
+    const float* const a_slice = SLICED ? a_in + static_cast<uint64_t>(ks) * K : a_in;
     const uint32_t a_stride4 = SLICED ? gridDim.y * K4 : K4;
-    const uint32_t sb_stride = SLICED ? gridDim.y * p.sb_total : p.sb_total;
     const uint32_t RS = K + kLimbPad;  // limb row stride
     float* tres = reinterpret_cast<float*>(limbs + 3 * M * RS);
+
+    // ---- activations first, from the leading arguments alone (the
+    // prologue waits for them only): element float4 f = tid + kThreads * u
+    // of [m][k/4] ----
+    const uint32_t total4 = M * K4;
+    // k % 256 == 0 keeps a wave's 64 float4 inside one row: run (u, wave)
+    // starts at float4 fb = wave * 64 + u * kThreads, row ru[u] = fb / k4,
+    // column cb[u] = fb % k4, all wave-uniform (a wave past the end takes
+    // the last run), so no lane divides.
+    uint32_t ru[F4], cb[F4];
+#pragma unroll
+    for (int u = 0; u < F4; ++u) {
+        const uint32_t fb = min(static_cast<uint32_t>(wave * kWave + kThreads * u), total4 - kWave);
+        ru[u] = __builtin_amdgcn_readfirstlane(fb / K4);
+        cb[u] = fb - ru[u] * K4;
+    }
+    float4 v[F4], gv[F4];
+#pragma unroll
+    for (int u = 0; u < F4; ++u) {
+        if (kThreads * u < total4) {  // block-uniform: runs past the input load nothing
+            const uint32_t c4 = cb[u] + lane;
+            // rows of a k slice are a_stride4 float4 apart
+            v[u] = reinterpret_cast<const float4*>(a_slice)[ru[u] * a_stride4 + c4];
+            if (gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(gamma)[c4];
+        } else {
+            v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    // the rest of the arguments, in one batch of loads (the activations are in flight)
+    prefetch_kernarg<arg_bytes<const float*, const float*, uint32_t, uint32_t, Args>()>();
+    const uint32_t sb_stride = SLICED ? gridDim.y * p.sb_total : p.sb_total;
 
     // ---- this wave's stream: for each block tile j (global tile
     // blockIdx.x + j * gridDim.x) the superblocks [sbA, sbA + len); every
@@ -242,32 +274,6 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         }
     };
 
-    // ---- activations first (the prologue waits for them only), then the
-    // weight window: element float4 f = tid + kThreads * u of [m][k/4] ----
-    const uint32_t total4 = M * K4;
-    // k % 256 == 0 keeps a wave's 64 float4 inside one row: run (u, wave)
-    // starts at float4 fb = wave * 64 + u * kThreads, row ru[u] = fb / k4,
-    // column cb[u] = fb % k4, all wave-uniform (a wave past the end takes
-    // the last run), so no lane divides.
-    uint32_t ru[F4], cb[F4];
-#pragma unroll
-    for (int u = 0; u < F4; ++u) {
-        const uint32_t fb = min(static_cast<uint32_t>(wave * kWave + kThreads * u), total4 - kWave);
-        ru[u] = __builtin_amdgcn_readfirstlane(fb / K4);
-        cb[u] = fb - ru[u] * K4;
-    }
-    float4 v[F4], gv[F4];
-#pragma unroll
-    for (int u = 0; u < F4; ++u) {
-        if (kThreads * u < total4) {  // block-uniform: runs past the input load nothing
-            const uint32_t c4 = cb[u] + lane;
-            // rows of a k slice are a_stride4 float4 apart
-            v[u] = reinterpret_cast<const float4*>(a_slice)[ru[u] * a_stride4 + c4];
-            if (p.gamma != nullptr) gv[u] = reinterpret_cast<const float4*>(p.gamma)[c4];
-        } else {
-            v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
     // Output element e of the block's [tiles][16][m] results: its segment
     // and offset, false past the segment's rows.
     auto out_at = [&](uint32_t e, uint32_t& si, uint64_t& o) -> bool {
@@ -284,7 +290,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     // after the weight window, so the epilogue does not wait a memory round
     // trip for it. Every thread loads (threads without one re-read an
     // activation), which keeps the compiler's wait counts exact.
-    const float* res_src = p.a;
+    const float* res_src = a_in;
     if (p.epilogue == kFusedResidual && static_cast<uint32_t>(tid) < my_tiles * 16 * M) {
         uint32_t si;
         uint64_t o;
@@ -299,7 +305,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     for (int u = 0; u < F4; ++u)
         if (static_cast<uint32_t>(wave) * kWave + kThreads * u >= total4) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
 
-    if (p.gamma != nullptr) {
+    if (gamma != nullptr) {
 #pragma unroll
         for (int u = 0; u < F4; ++u) {
             float ss = 0.f;
@@ -601,8 +607,6 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     }
     const uint64_t kc = k / slices;
     Args p;
-    p.a = f.a;
-    p.gamma = f.gamma;
     p.normed = f.normed;
     p.eps = f.eps;
     p.nseg = f.nseg;
@@ -678,19 +682,19 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const uint32_t f4 = (p.m * p.k / 4 + threads - 1) / threads;
     const dim3 grid(blocks, slices);
 #define SL_QGEMV_FUSED_F(B, T, G, L)                                                                  \
-    (waves == 16 ? (f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 16, false><<<grid, threads, lds, s>>>(p)         \
-                    : f4 <= 4 ? qgemv_fused<B, T, G, L, 4, 16, false><<<grid, threads, lds, s>>>(p)         \
-                              : qgemv_fused<B, T, G, L, 8, 16, false><<<grid, threads, lds, s>>>(p))        \
-     : f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 8, false><<<grid, threads, lds, s>>>(p)                       \
-     : f4 <= 4   ? qgemv_fused<B, T, G, L, 4, 8, false><<<grid, threads, lds, s>>>(p)                       \
-                 : qgemv_fused<B, T, G, L, 8, 8, false><<<grid, threads, lds, s>>>(p))
+    (waves == 16 ? (f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 16, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)         \
+                    : f4 <= 4 ? qgemv_fused<B, T, G, L, 4, 16, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)         \
+                              : qgemv_fused<B, T, G, L, 8, 16, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p))        \
+     : f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 8, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)                       \
+     : f4 <= 4   ? qgemv_fused<B, T, G, L, 4, 8, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)                       \
+                 : qgemv_fused<B, T, G, L, 8, 8, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p))
 #define SL_QGEMV_FUSED(B, T, G) (lr ? SL_QGEMV_FUSED_F(B, T, G, true) : SL_QGEMV_FUSED_F(B, T, G, false))
 #define SL_QGEMV_FUSED_G(B, T) \
     (spg == 1 ? SL_QGEMV_FUSED(B, T, 1) : spg == 2 ? SL_QGEMV_FUSED(B, T, 2) : SL_QGEMV_FUSED(B, T, 0))
     if (slices > 1) {
         // k slices: many rows (not LR), 16 waves, 8 float4 per thread
         if (waves != 16 || f4 > 8 || lr) return hipErrorNotSupported;
-#define SL_QGEMV_SLICED(B, G) qgemv_fused<B, 1, G, false, 8, 16, true><<<grid, threads, lds, s>>>(p)
+#define SL_QGEMV_SLICED(B, G) qgemv_fused<B, 1, G, false, 8, 16, true><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)
         if (int4) {
             if (spg == 1) SL_QGEMV_SLICED(4, 1);
             else if (spg == 2) SL_QGEMV_SLICED(4, 2);

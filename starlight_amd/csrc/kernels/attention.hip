@@ -238,7 +238,6 @@ __device__ __forceinline__ void rope_table(const Geo& g, uint64_t b, uint32_t S,
 
 __global__ __launch_bounds__(256) void rope_sincos(const uint32_t* __restrict__ pos, uint32_t tokens, uint32_t D,
                                                    double theta, float* __restrict__ table) {
-    prefetch_kernarg<arg_bytes<const uint32_t*, uint32_t, uint32_t, double, float*>()>();
     const uint32_t half = D / 2;
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= tokens * half) return;

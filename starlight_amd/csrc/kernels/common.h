@@ -142,6 +142,9 @@ __device__ __forceinline__ float lane_xor32(float v) {
 // memory round trip (about 0.6 us) before the kernel's first global load.
 // BYTES is the explicit arguments' size (arg_bytes below); the last word
 // is touched too, so the lines are covered whatever the segment's alignment.
+// Kernels whose explicit arguments are all scalars or pointers, at most
+// six, do not call it: the library is built to preload up to six leading
+// such arguments into scalar registers, so they have nothing to fetch.
 template <uint32_t BYTES>
 __device__ __forceinline__ void prefetch_kernarg() {
     static_assert(BYTES >= 4, "no arguments to fetch");

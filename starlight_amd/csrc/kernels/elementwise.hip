@@ -29,7 +29,6 @@ __device__ __forceinline__ float apply(float a, float b, float factor) {
 template <Ew OP>
 __global__ __launch_bounds__(256) void ew_vec4(const float4* __restrict__ a, const float4* __restrict__ b,
                                                float4* __restrict__ out, uint64_t n4, float factor) {
-    prefetch_kernarg<arg_bytes<const float4*, const float4*, float4*, uint64_t, float>()>();
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
         float4 x = OP == Ew::Zero ? make_float4(0.f, 0.f, 0.f, 0.f) : a[i];
@@ -47,7 +46,6 @@ template <Ew OP>
 __global__ __launch_bounds__(256) void ew_scalar(const float* __restrict__ a, const float* __restrict__ b,
                                                  float* __restrict__ out, uint64_t begin, uint64_t n,
                                                  float factor) {
-    prefetch_kernarg<arg_bytes<const float*, const float*, float*, uint64_t, uint64_t, float>()>();
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
     for (uint64_t i = begin + static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
          i += stride) {

@@ -15,7 +15,6 @@ namespace {
 // Mapping kinds: gather (src row = ids[r]), fixed stride pairs.
 __global__ __launch_bounds__(256) void gather_rows(const float* __restrict__ table, const uint32_t* __restrict__ ids,
                                                    float* __restrict__ out, uint64_t hidden, bool vec) {
-    prefetch_kernarg<arg_bytes<const float*, const uint32_t*, float*, uint64_t, bool>()>();
     const uint64_t r = blockIdx.x;
     const uint64_t src = static_cast<uint64_t>(ids[r]) * hidden;
     const uint64_t dst = r * hidden;
@@ -30,7 +29,6 @@ __global__ __launch_bounds__(256) void gather_rows(const float* __restrict__ tab
 
 __global__ __launch_bounds__(256) void last_token_rows(const float* __restrict__ in, float* __restrict__ out,
                                                        uint64_t seq, uint64_t hidden, uint64_t position) {
-    prefetch_kernarg<arg_bytes<const float*, float*, uint64_t, uint64_t, uint64_t>()>();
     const uint64_t b = blockIdx.x;
     const float* src = in + (b * seq + position) * hidden;
     float* dst = out + b * hidden;
@@ -42,7 +40,6 @@ template <int VEC, bool SPLIT>
 __global__ __launch_bounds__(256) void heads_permute(const float* __restrict__ in, float* __restrict__ out,
                                                      uint64_t seq, uint64_t heads, uint64_t head_dim,
                                                      uint64_t total) {
-    prefetch_kernarg<arg_bytes<const float*, float*, uint64_t, uint64_t, uint64_t, uint64_t>()>();
     const uint64_t dv = head_dim / VEC;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {

@@ -18,7 +18,6 @@ template <int VPT>
 __global__ __launch_bounds__(256) void rms_norm_vec(const float4* __restrict__ x, const float4* __restrict__ w,
                                                     float4* __restrict__ out, uint32_t hidden4, float hidden_f,
                                                     float eps) {
-    prefetch_kernarg<arg_bytes<const float4*, const float4*, float4*, uint32_t, float, float>()>();
     __shared__ float scratch[4];
     const uint64_t row = blockIdx.x;
     const float4* xr = x + row * hidden4;
@@ -62,7 +61,6 @@ __global__ __launch_bounds__(256) void rms_norm_vec(const float4* __restrict__ x
 // General RMSNorm: any hidden size and alignment, two passes over the row.
 __global__ __launch_bounds__(256) void rms_norm_any(const float* __restrict__ x, const float* __restrict__ w,
                                                     float* __restrict__ out, uint64_t hidden, float eps) {
-    prefetch_kernarg<arg_bytes<const float*, const float*, float*, uint64_t, float>()>();
     __shared__ float scratch[4];
     const float* xr = x + blockIdx.x * hidden;
     float ss = 0.f;
@@ -78,7 +76,6 @@ template <int VPT, bool CAUSAL>
 __global__ __launch_bounds__(256) void softmax_regs(const float* __restrict__ x, float* __restrict__ out,
                                                     uint32_t cols, uint32_t seq, uint32_t past_len,
                                                     const uint32_t* __restrict__ dyn) {
-    prefetch_kernarg<arg_bytes<const float*, float*, uint32_t, uint32_t, uint32_t, const uint32_t*>()>();
     __shared__ float scratch[4];
     const uint64_t row = blockIdx.x;
     if (CAUSAL && dyn != nullptr) past_len = dyn[0];
@@ -115,7 +112,6 @@ template <bool CAUSAL>
 __global__ __launch_bounds__(256) void softmax_any(const float* __restrict__ x, float* __restrict__ out,
                                                    uint64_t cols, uint64_t seq, uint64_t past_len,
                                                    const uint32_t* __restrict__ dyn) {
-    prefetch_kernarg<arg_bytes<const float*, float*, uint64_t, uint64_t, uint64_t, const uint32_t*>()>();
     __shared__ float scratch[4];
     const uint64_t row = blockIdx.x;
     if (CAUSAL && dyn != nullptr) past_len = dyn[0];

@@ -250,7 +250,6 @@ __global__ __launch_bounds__(256) void qgemv_mfma(QgemvArgs p) {
 // out[i] = sum over splits (in order) of partial[split][i], i < m * n.
 __global__ __launch_bounds__(256) void qgemv_reduce(const float* __restrict__ partial, float* __restrict__ out,
                                                     uint64_t count, uint32_t splits) {
-    prefetch_kernarg<arg_bytes<const float*, float*, uint64_t, uint32_t>()>();
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
         float sum = 0.f;

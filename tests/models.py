@@ -19,7 +19,7 @@ from oracle.cpu_device import OracleDevice
 from starlight_amd import device as hipdevice
 from starlight_amd import engine, formats, graph, synth
 from starlight_amd.graph import LlamaConfig, weight_specs
-from starlight_amd.ir import QuantFormat
+from starlight_amd.ir import QuantFormat, ValueRole
 
 _F32: Dict[Tuple, Dict[str, np.ndarray]] = {}
 _QUANT: Dict[Tuple, Tuple[Dict[str, np.ndarray], Dict[str, formats.QuantTensor]]] = {}
@@ -78,8 +78,12 @@ class Pair:
 
     def __init__(self, hip, cfg: LlamaConfig, batch: int, prompt_len: int, max_seq: int, seed: int):
         self.cfg, self.batch, self.prompt_len, self.max_seq = cfg, batch, prompt_len, max_seq
+        self.hip = hip
+        self.past0 = 0  # positions already in the cache when the prompt starts
         caps = graph.DeviceCapabilities.from_c(hipdevice.capabilities())
         pre_l = graph.compile_for(graph.lower_llama(cfg, batch, prompt_len, max_seq), caps)
+        self.kv_value = next(i for i, v in enumerate(pre_l.ir.values) if v.role == ValueRole.STATE)
+        self.kv_shape = pre_l.ir.values[self.kv_value].shape
         dec_l = graph.compile_for(graph.lower_llama(cfg, batch, 1, max_seq), caps)
         gb = upload(hip, cfg, seed)
         self.gpu = engine.NativeEngine(hip, engine.compile_program(pre_l, gb), engine.compile_program(dec_l, gb),
@@ -101,15 +105,27 @@ class Pair:
                 self.mismatched_ids += 1
         return c.argmax(axis=1).astype(np.uint32)
 
+    def seed_cache(self, past: int, seed: int) -> None:
+        """Writes the same keys and values ~N(0, 1) at positions [0, past)
+        of every layer into both engines' KV caches (uploaded through the
+        Device contract), so the prompt starts at past_len = past and
+        attends over past + prompt_len positions."""
+        cache = np.zeros(self.kv_shape, np.float32)  # [B, layers, 2, max_seq, Hkv, D]
+        prefix = cache[:, :, :, :past]
+        prefix[...] = np.random.default_rng(seed).standard_normal(prefix.shape, dtype=np.float32)
+        self.hip.upload_f32(self.gpu.state_buffer(self.kv_value), cache.ravel())
+        self.cdev.upload_f32(self.cpu.states[self.kv_value], cache.ravel())
+        self.past0 = past
+
     def prefill(self, repeats: int = 1) -> np.ndarray:
-        B, S, V = self.batch, self.prompt_len, self.cfg.vocab
-        pos = np.tile(np.arange(S, dtype=np.uint32), B)
+        B, S, V, P = self.batch, self.prompt_len, self.cfg.vocab, self.past0
+        pos = np.tile(np.arange(P, P + S, dtype=np.uint32), B)
         c = np.zeros(B * V, np.float32)
-        self.cpu.step(self.cpu.PREFILL, self.prompts, pos, S, 0, c)
+        self.cpu.step(self.cpu.PREFILL, self.prompts, pos, S, P, c)
         ids = None
         for _ in range(repeats):
             g = np.zeros(B * V, np.float32)
-            self.gpu.step(self.gpu.PREFILL, self.prompts, pos, S, 0, g)
+            self.gpu.step(self.gpu.PREFILL, self.prompts, pos, S, P, g)
             ids = self._compare(g, c)
         return ids
 
@@ -119,7 +135,7 @@ class Pair:
         B, V = self.batch, self.cfg.vocab
         out = []
         for s in range(steps):
-            past = self.prompt_len + s
+            past = self.past0 + self.prompt_len + s
             pos = np.full(B, past, np.uint32)
             g = np.zeros(B * V, np.float32)
             c = np.zeros(B * V, np.float32)

@@ -477,6 +477,47 @@ def cpu_model():
     return "unknown CPU"
 
 
+def fusion_guard(dev, eng, vocab, batch, prompt, positions, prompt_len, steps=8):
+    """The benchmarked configuration (fusion on, submissions graph-replayed)
+    against the device with both off, on the same prompt and `steps`
+    teacher-forced decode steps (both runs take the fused run's greedy ids).
+    Per row, logits must agree within 1e-4 normwise and greedy ids must be
+    equal unless the top-2 gap is below 1e-4 * ||logits||_2. A guard of the
+    timed path, not parity (the tests hold that); raises on a mismatch."""
+    runs = []
+    feed = None
+    for fused in (True, False):
+        dev.set_options(fusion=fused, graphs=fused)
+        logits = np.zeros(batch * vocab, np.float32)
+        eng.step(eng.PREFILL, prompt, positions, prompt_len, 0, logits)
+        rows = [logits.reshape(batch, vocab).copy()]
+        for s in range(steps):
+            ids = feed[s] if feed is not None else rows[-1].argmax(axis=1).astype(np.uint32)
+            past = prompt_len + s
+            eng.step(eng.DECODE, ids, np.full(batch, past, np.uint32), 1, past, logits)
+            rows.append(logits.reshape(batch, vocab).copy())
+        if feed is None:
+            feed = [r.argmax(axis=1).astype(np.uint32) for r in rows[:-1]]
+        runs.append(rows)
+    dev.set_options()
+    worst, ties = 0.0, 0
+    for s, (f, u) in enumerate(zip(*runs)):
+        for b in range(batch):
+            fb, ub = f[b].astype(np.float64), u[b].astype(np.float64)
+            norm = np.linalg.norm(ub)
+            err = float(np.linalg.norm(fb - ub) / norm)
+            worst = max(worst, err)
+            if err > 1e-4:
+                raise SystemExit(f"fusion guard: step {s} row {b}: fused logits differ by {err:.2e} normwise")
+            if int(np.argmax(fb)) != int(np.argmax(ub)):
+                top2 = np.sort(ub)[-2:]
+                if top2[1] - top2[0] >= 1e-4 * norm:
+                    raise SystemExit(f"fusion guard: step {s} row {b}: greedy id {int(np.argmax(fb))} fused, "
+                                     f"{int(np.argmax(ub))} unfused")
+                ties += 1
+    return {"steps": steps, "max_rel_l2": float(f"{worst:.3e}"), "near_tie_ids": ties}
+
+
 def cpu_baseline(cfg, prompt_len=PROMPT_LEN, label="8B", budget_s=25.0):
     """Times the oracle (scalar C restatement of backend-cpu, one core) on one
     layer of the model's shape decoding with prompt_len positions already
@@ -640,6 +681,8 @@ def main():
     step_bytes = linear + B * (cfg.hidden * 4 + kv_bytes)
     hbm_frac = step_bytes / (ms_per_step * 1e-3) / (HBM_PEAK_GBS * 1e9)
 
+    guard = fusion_guard(dev, eng, cfg.vocab, B, prompt, positions, prompt_len)
+    log(f"fusion guard (fused + graphs vs neither): {guard}")
     roof = qgemv_roofline(dev, int8=args.int8, **gemv_shape)
     log(f"q-GEMV roofline: {roof}")
     norm = rmsnorm_roofline(dev)
@@ -676,6 +719,7 @@ def main():
         "decode_hbm_frac": round(hbm_frac, 4),
         "prefill_tok_s": round(B * prompt_len / prefill_s, 1),
         "prefill_warm_tok_s": round(B * prompt_len / prefill_warm_s, 1),
+        "fusion_guard": guard,
         "roofline": roof,
         "rmsnorm": norm,
         "read_floor": {"gemv": gemv_floor, "decode_step": step_floor},

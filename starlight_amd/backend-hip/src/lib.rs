@@ -194,7 +194,12 @@ impl HipDevice {
                 offset: e.offset as usize,
                 len: e.len as usize,
             },
-            ffi::SL_ERR_UNSUPPORTED_OP => DeviceError::UnsupportedOp(opcode_from_u32(e.op)),
+            ffi::SL_ERR_UNSUPPORTED_OP => match opcode_from_u32(e.op) {
+                Some(op) => DeviceError::UnsupportedOp(op),
+                // a code this binding does not know: the library is newer
+                // than the binding, which must not guess an op
+                None => DeviceError::Execution("HIP library reported UnsupportedOp with an op code unknown to this binding"),
+            },
             ffi::SL_ERR_SHAPE_OVERFLOW => DeviceError::ShapeOverflow,
             ffi::SL_ERR_EXECUTION => DeviceError::Execution(message),
             _ => DeviceError::Unimplemented(message),
@@ -466,8 +471,10 @@ const OPCODES: [OpCode; 18] = [
     OpCode::RmsNormMatMul,
 ];
 
-fn opcode_from_u32(code: u32) -> OpCode {
-    OPCODES.get(code as usize).copied().unwrap_or(OpCode::MatMulNT)
+/// The OpCode of a C `sl_opcode` value (declaration order), or None for a
+/// value past the known ops.
+fn opcode_from_u32(code: u32) -> Option<OpCode> {
+    OPCODES.get(code as usize).copied()
 }
 
 /// The backend's DeviceCapabilities (ARCH-0004 §8), from

@@ -699,10 +699,18 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
     AttentionArgs a{fptr(d, sq.in[0]), fptr(d, sk.in[0]), fptr(d, sv.in[0]), fptr(d, cache),
                     att_dead ? nullptr : fptr(d, att), B, ap.layers, ap.layer, H, Hkv, S, ap.past_len, D,
                     ap.max_seq, ap.scale, dyn_of(d, at)};
-    // Workspace: the decode partials, the mirror of the merged heads, then
-    // the staged intermediates.
+    // The prefill form writes its rotated q to a workspace area and takes
+    // no other live intermediate: a live rotated q (the last layer's, which
+    // nothing overwrites before the submission ends) is staged there and
+    // copied to its place like the decode form's.
+    if (attention_fused_prefill(a)) {
+        if (live[0] || live[1] || live[2] || live[4]) return 0;
+        staged[3] = live[3];
+    }
+    // Workspace: the decode partials (prefill: the rotated q), the mirror of
+    // the merged heads, then the staged intermediates.
     const Workspace ws{d->workspace, d->workspace_floats};
-    const uint64_t mirror_at = (attention_workspace_floats(a) + 63) / 64 * 64;
+    const uint64_t mirror_at = (attention_fused_workspace_floats(a) + 63) / 64 * 64;
     // The output projection is chained (it reads the mirror, not MergeHeads'
     // output) only for decode (at most 16 rows, the fused GEMV's) and when
     // the mirror fits; otherwise it runs on its own and reads MergeHeads'

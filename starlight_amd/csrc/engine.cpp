@@ -118,7 +118,7 @@ sl_status bind_quantized_params(sl_engine* e, const sl_compiled_program* p) {
 
 sl_status resolve_program(sl_engine* e, const sl_compiled_program* p, Program* out) {
     const sl_command_buffer& ir = p->ir;
-    if (ir.ir_version != SL_IR_VERSION) return SL_ERR_EXECUTION;
+    if (ir.ir_version != SL_IR_VERSION) return slhip_fail_execution(e->device, "CommandBuffer IR version does not match this engine");
     const sl_status bq = bind_quantized_params(e, p);
     if (bq != SL_OK) return bq;
     const size_t nv = ir.n_values;
@@ -131,14 +131,15 @@ sl_status resolve_program(sl_engine* e, const sl_compiled_program* p, Program* o
     };
     for (size_t i = 0; i < p->n_weights; ++i) {
         const uint32_t vid = p->weight_values[i];
-        if (vid >= nv) return SL_ERR_EXECUTION;
+        if (vid >= nv) return slhip_fail_execution(e->device, "weight binding names a value outside the CommandBuffer");
         const sl_value& v = ir.values[vid];
         const uint64_t len = v.encoding == SL_ENCODING_GROUPWISE_QUANTIZED ? payload_words(v) : element_count(v);
         bind(vid, p->weight_buffers[i], 0, len);
     }
     for (size_t i = 0; i < ir.n_slots; ++i) {
         const sl_slot& s = ir.slots[i];
-        if (s.value >= nv || s.offset % 4 != 0 || s.bytes % 4 != 0) return SL_ERR_EXECUTION;
+        if (s.value >= nv || s.offset % 4 != 0 || s.bytes % 4 != 0)
+            return slhip_fail_execution(e->device, "memory plan slot is outside the CommandBuffer or not 4-byte aligned");
         bind(s.value, e->scratchpad, s.offset / 4, s.bytes / 4);
     }
     for (size_t vid = 0; vid < nv; ++vid) {
@@ -171,19 +172,20 @@ sl_status resolve_program(sl_engine* e, const sl_compiled_program* p, Program* o
         }
         bind(static_cast<uint32_t>(vid), buf, 0, element_count(v));
     }
-    if (p->token_ids >= nv || !bound[p->token_ids]) return SL_ERR_EXECUTION;
+    if (p->token_ids >= nv || !bound[p->token_ids]) return slhip_fail_execution(e->device, "token_ids is not an Input value of the CommandBuffer");
     out->token_buffer = refs[p->token_ids].buffer;
     out->token_elements = element_count(ir.values[p->token_ids]);
     const sl_value& tv = ir.values[p->token_ids];
     out->batch = tv.rank >= 1 ? tv.dims[0] : 1;
     out->seq = tv.rank >= 2 ? tv.dims[1] : 1;
     if (p->positions >= 0) {
-        if (static_cast<size_t>(p->positions) >= nv || !bound[p->positions]) return SL_ERR_EXECUTION;
+        if (static_cast<size_t>(p->positions) >= nv || !bound[p->positions])
+            return slhip_fail_execution(e->device, "positions is not an Input value of the CommandBuffer");
         out->has_positions = true;
         out->position_buffer = refs[p->positions].buffer;
         out->position_elements = element_count(ir.values[p->positions]);
     }
-    if (p->logits >= nv || !bound[p->logits]) return SL_ERR_EXECUTION;
+    if (p->logits >= nv || !bound[p->logits]) return slhip_fail_execution(e->device, "logits is not an Output value of the CommandBuffer");
     out->logits_buffer = refs[p->logits].buffer;
     out->logits_elements = element_count(ir.values[p->logits]);
 
@@ -192,32 +194,33 @@ sl_status resolve_program(sl_engine* e, const sl_compiled_program* p, Program* o
         const sl_command& cmd = ir.commands[c];
         Resolved& r = out->commands[c];
         r.op = cmd.op;
-        if (cmd.n_inputs > SL_MAX_INPUTS || cmd.n_outputs > SL_MAX_OUTPUTS) return SL_ERR_EXECUTION;
+        if (cmd.n_inputs > SL_MAX_INPUTS || cmd.n_outputs > SL_MAX_OUTPUTS)
+            return slhip_fail_execution(e->device, "command has more ports than the device contract allows");
         for (uint32_t i = 0; i < cmd.n_inputs; ++i) {
             const uint32_t vid = cmd.inputs[i];
-            if (vid >= nv) return SL_ERR_EXECUTION;
+            if (vid >= nv) return slhip_fail_execution(e->device, "command input names a value outside the CommandBuffer");
             const sl_value& v = ir.values[vid];
             if (v.role == SL_ROLE_SCALAR) {
                 if (vid == p->seq_len) r.scalars[r.n_scalars++] = ScalarSource::SeqLen;
                 else if (static_cast<int32_t>(vid) == p->past_len) r.scalars[r.n_scalars++] = ScalarSource::PastLen;
-                else return SL_ERR_EXECUTION;
+                else return slhip_fail_execution(e->device, "command reads a Scalar that is neither seq_len nor past_len");
                 continue;
             }
-            if (!bound[vid]) return SL_ERR_EXECUTION;
+            if (!bound[vid]) return slhip_fail_execution(e->device, "command input has no buffer (unbound Param or Temp without a plan slot)");
             r.in[r.n_in] = refs[vid];
             r.in_vals[r.n_in] = v;
             ++r.n_in;
         }
         // Stateful commands get their State as an extra input port.
         if (cmd.effect != SL_EFFECT_NONE) {
-            if (cmd.state >= nv || !bound[cmd.state]) return SL_ERR_EXECUTION;
+            if (cmd.state >= nv || !bound[cmd.state]) return slhip_fail_execution(e->device, "stateful command has no State buffer");
             r.in[r.n_in] = refs[cmd.state];
             r.in_vals[r.n_in] = ir.values[cmd.state];
             ++r.n_in;
         }
         for (uint32_t i = 0; i < cmd.n_outputs; ++i) {
             const uint32_t vid = cmd.outputs[i];
-            if (vid >= nv || !bound[vid]) return SL_ERR_EXECUTION;
+            if (vid >= nv || !bound[vid]) return slhip_fail_execution(e->device, "command output has no buffer");
             r.out[r.n_out] = refs[vid];
             r.out_vals[r.n_out] = ir.values[vid];
             ++r.n_out;
@@ -303,13 +306,13 @@ sl_status sl_engine_build(sl_hip_device* device, const sl_compiled_program* pref
 sl_status sl_engine_step(sl_engine* e, uint32_t mode, const uint32_t* token_ids, size_t n_token_ids,
                          const uint32_t* positions, size_t n_positions, uint32_t seq_len, uint32_t past_len,
                          float* logits, size_t n_logits) {
-    if (mode > SL_STEP_DECODE) return SL_ERR_EXECUTION;
+    if (mode > SL_STEP_DECODE) return slhip_fail_execution(e->device, "step mode is neither Prefill nor Decode");
     Program& p = e->programs[mode];
     // step responsibility 1: inputs against the compiled capacities
     if (n_token_ids != p.token_elements || (p.has_positions && n_positions != p.position_elements) ||
         n_logits != p.logits_elements || seq_len == 0 || seq_len > p.seq ||
         static_cast<uint64_t>(past_len) + seq_len > e->max_context)
-        return SL_ERR_EXECUTION;
+        return slhip_fail_execution(e->device, "step input exceeds the compiled capacity");
     // 2: upload token ids and positions
     sl_status st = sl_hip_upload_u32(e->device, p.token_buffer, token_ids, n_token_ids);
     if (st != SL_OK) return st;
@@ -338,7 +341,7 @@ sl_status sl_engine_generate(sl_engine* e, const uint32_t* prompt, size_t prompt
     Program& dc = e->programs[SL_STEP_DECODE];
     if (pf.batch != 1 || dc.batch != 1 || prompt_len != pf.seq || pf.logits_elements != vocab ||
         dc.logits_elements != vocab || dc.seq != 1)
-        return SL_ERR_EXECUTION;
+        return slhip_fail_execution(e->device, "generate needs batch-1 programs whose prompt length and vocabulary match");
     for (size_t i = 0; i < prompt_len; ++i) e->position_host[i] = static_cast<uint32_t>(i);
     float* row = logits_out ? logits_out : e->logits_host.data();
     sl_status st = sl_engine_step(e, SL_STEP_PREFILL, prompt, prompt_len, e->position_host.data(), prompt_len,
@@ -363,7 +366,7 @@ sl_status sl_engine_decode_batch(sl_engine* e, const uint32_t* tokens, uint32_t 
     const size_t batch = dc.batch;
     if (dc.seq != 1 || dc.token_elements != batch || (dc.has_positions && dc.position_elements != batch) ||
         dc.logits_elements % batch != 0)
-        return SL_ERR_EXECUTION;
+        return slhip_fail_execution(e->device, "decode program is not one token per row");
     const size_t vocab = dc.logits_elements / batch;
     std::vector<uint32_t> cur(tokens, tokens + batch), pos(batch);
     for (uint32_t s = 0; s < steps; ++s) {
@@ -383,7 +386,7 @@ sl_status sl_engine_decode_batch(sl_engine* e, const uint32_t* tokens, uint32_t 
 sl_status sl_engine_decode(sl_engine* e, uint32_t token, uint32_t past_len, uint32_t steps,
                            uint32_t* tokens_out) {
     const Program& dc = e->programs[SL_STEP_DECODE];
-    if (dc.batch != 1 || dc.seq != 1) return SL_ERR_EXECUTION;
+    if (dc.batch != 1 || dc.seq != 1) return slhip_fail_execution(e->device, "decode needs a batch-1, one-token decode program");
     return sl_engine_decode_batch(e, &token, past_len, steps, tokens_out);
 }
 

@@ -1069,6 +1069,17 @@ uint64_t attention_workspace_floats(const AttentionArgs& a) {
     return a.batch * a.kv_heads * decode_parts(a) * rows * (kDecodePartStride + a.head_dim);
 }
 
+bool attention_fused_prefill(const AttentionArgs& a) {
+    const uint64_t rows = a.heads / (a.kv_heads ? a.kv_heads : 1) * a.seq;
+    const uint64_t dv = a.head_dim / 64;
+    const uint64_t rt = rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
+    return !(rows <= kDecodeMaxRows && a.head_dim % 64 == 0 && dv >= 1 && dv <= 4 && rt * dv <= 32);
+}
+
+uint64_t attention_fused_workspace_floats(const AttentionArgs& a) {
+    return attention_fused_prefill(a) ? a.batch * a.seq * a.heads * a.head_dim : attention_workspace_floats(a);
+}
+
 hipError_t launch_paged_attention(const PagedAttentionArgs& p, const Workspace& ws, hipStream_t s) {
     AttentionArgs a{p.q, p.k_new, p.v_new, p.pool, p.out, p.batch, p.layers, p.layer, p.heads, p.kv_heads, 1,
                     0, p.head_dim, static_cast<uint64_t>(p.pages_per_seq) * p.page_size, p.scale, nullptr};
@@ -1104,17 +1115,20 @@ hipError_t launch_attention_fused(const AttentionArgs& a, const Workspace& ws, h
     if (d != hipErrorNotSupported) return d;
     // Prefill: prefill_prep (SplitHeads, Rope, KvAppend), then attn_prefill
     // writing the attention output and / or MergeHeads' layout. The rotated q
-    // goes to the workspace; the unit's other intermediates must be dead (no
-    // staging) and the output projection not chained.
+    // goes to q_rot when set (the caller's staging area, which nothing the
+    // kernels read or write overlaps), else to the workspace; the unit's
+    // other intermediates must be dead (no staging) and the output
+    // projection not chained.
     const uint64_t qr_floats = a.batch * a.seq * a.heads * a.head_dim;
     const bool aligned = aligned16(a.q) && aligned16(a.k_new) && aligned16(a.v_new) && aligned16(a.cache) &&
-                         (a.out == nullptr || aligned16(a.out)) && (a.merged == nullptr || aligned16(a.merged));
+                         (a.out == nullptr || aligned16(a.out)) && (a.merged == nullptr || aligned16(a.merged)) &&
+                         (a.q_rot == nullptr || aligned16(a.q_rot));
     if (a.seq < 16 || !(a.head_dim == 64 || a.head_dim == 128) || !aligned || a.positions == nullptr ||
         a.rope_variant > SL_ROPE_GPTJ || a.mirror != nullptr || a.q_split != nullptr || a.k_split != nullptr ||
-        a.v_split != nullptr || a.q_rot != nullptr || a.k_rot != nullptr || (a.out == nullptr && a.merged == nullptr) ||
-        qr_floats > ws.floats || a.batch * a.seq > 0x7fffffffull)
+        a.v_split != nullptr || a.k_rot != nullptr || (a.out == nullptr && a.merged == nullptr) ||
+        (a.q_rot == nullptr && qr_floats > ws.floats) || a.batch * a.seq > 0x7fffffffull)
         return hipErrorNotSupported;
-    float* qr = ws.data;
+    float* qr = a.q_rot != nullptr ? a.q_rot : ws.data;
     Geo g = make_geo(a, ws);
     const unsigned tokens = static_cast<unsigned>(a.batch * a.seq);
     if (a.head_dim == 64) prefill_prep<64><<<tokens, 256, 0, s>>>(g, qr);

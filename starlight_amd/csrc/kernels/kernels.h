@@ -144,6 +144,12 @@ hipError_t launch_attention(const AttentionArgs& a, const Workspace& ws, hipStre
 // attention_workspace_floats(a) floats.
 hipError_t launch_attention_fused(const AttentionArgs& a, const Workspace& ws, hipStream_t s);
 uint64_t attention_workspace_floats(const AttentionArgs& a);
+// Whether launch_attention_fused takes the prefill form for this shape
+// (more query rows per KV head than the decode kernel serves), and the
+// workspace floats its kernels use before any caller area: the decode
+// partials, or the prefill form's rotated q.
+bool attention_fused_prefill(const AttentionArgs& a);
+uint64_t attention_fused_workspace_floats(const AttentionArgs& a);
 
 // Decode attention over a paged KV cache (one new token per row): row b has
 // seq_lens[b] cached positions; its new K/V row is appended at position

@@ -237,3 +237,36 @@ def test_native_build_binds_scale_params_and_rejects_a_missing_one(hip):
     want = np.zeros(cfg.vocab, np.float32)
     cpu.step(cpu.DECODE, [3], [0], 1, 0, want)
     assert_normwise(out, want)
+
+
+def test_native_step_errors_carry_their_own_message(hip):
+    """Every failing engine call records its reason (the reference's step
+    returns a typed StepError, ARCH-0007 §3.2): a step past the compiled
+    capacity, an unknown mode and a wrong token count each raise Execution
+    with their message, not the device's previous error, and a valid step
+    still runs afterwards."""
+    from starlight_amd.device import DeviceError
+    from starlight_amd.ir import BufferRef, Op, Value
+    cfg = LlamaConfig(layers=1, hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=384,
+                      theta=500_000.0)
+    bufs = engine.upload_weights(hip, cfg, synth.llama_weights(cfg, 6))
+    eng = engine.NativeEngine(hip, engine.compile_program(graph.lower_llama(cfg, 1, 4, 16), bufs),
+                              engine.compile_program(graph.lower_llama(cfg, 1, 1, 16), bufs), 1, 16)
+    out = np.zeros(cfg.vocab, np.float32)
+    # leave an unrelated error behind on the device first
+    x = hip.upload_new_f32(np.zeros(8, np.float32))
+    with pytest.raises(DeviceError):
+        hip.dispatch(Op.add(), [BufferRef(x, 0, 8), BufferRef(x, 0, 4)], [Value.f32([8]), Value.f32([4])],
+                     [BufferRef(x, 0, 8)], [Value.f32([8])])
+    with pytest.raises(DeviceError) as e:
+        eng.step(eng.DECODE, [3], [15], 1, 16, out)
+    assert e.value == DeviceError.execution("step input exceeds the compiled capacity")
+    with pytest.raises(DeviceError) as e:
+        eng.step(7, [3], [0], 1, 0, out)
+    assert e.value == DeviceError.execution("step mode is neither Prefill nor Decode")
+    with pytest.raises(DeviceError) as e:
+        eng.step(eng.DECODE, [3, 4], [0, 1], 1, 0, out)
+    assert e.value == DeviceError.execution("step input exceeds the compiled capacity")
+    eng.step(eng.PREFILL, [1, 2, 3, 4], [0, 1, 2, 3], 4, 0, out)
+    assert np.isfinite(out).all()
+    eng.close()

@@ -170,37 +170,44 @@ def test_attention_group_keeps_every_live_intermediate(hip, case):
     assert fused >= 7 if fusable(case, live=True) else fused == 0
 
 
-# The scratch layout of the last layer of an 8B-shaped decode step as the
-# memory plan lays it out (floats): q/k/v projections, then the split and
+# The scratch layout of the last layer of an 8B-shaped step as the memory
+# plan lays it out (floats per token): q/k/v projections, then the split and
 # rotated heads reusing their space. The rotated q overlaps the q tail, k and
-# v, which the fused kernel still reads, and MergeHeads leaves its last 1024
-# floats holding it when nothing after the group overwrites them.
+# v, which the fused kernels still read, and MergeHeads leaves its last 1024
+# floats per token holding it when nothing after the group overwrites them.
 LAST_LAYER = {"q": (8192, 4096), "k": (12288, 1024), "v": (13312, 1024), "qh": (4096, 4096),
               "kh": (8192, 1024), "vh": (9216, 1024), "qr": (10240, 4096), "kr": (4096, 1024),
               "att": (5120, 4096), "merged": (9216, 4096)}
 
 
 @pytest.mark.parametrize("projection_after", [True, False])
-def test_attention_group_stages_rotated_q_that_overlaps_its_inputs(hip, projection_after):
-    B, H, Hkv, S, past, D, max_seq = 1, 32, 8, 1, 1000, 128, 1100
+@pytest.mark.parametrize("S,past,max_seq", [(1, 1000, 1100), (64, 100, 256)])
+def test_attention_group_stages_rotated_q_that_overlaps_its_inputs(hip, projection_after, S, past, max_seq):
+    """A decode step (one token) and a 64-token prefill chunk laid out as
+    the last layer's plan: the rotated q is live (its tail survives) and is
+    staged and copied into place. The prefill form takes no other live
+    intermediate, so without the projection (which overwrites the rotated
+    k) its unit runs unfused."""
+    B, H, Hkv, D = 1, 32, 8, 128
     theta, scale = 500000.0, float(np.float32(1.0 / math.sqrt(D)))
-    r = np.random.default_rng(31)
-    nq, nk, total = B * S * H * D, B * S * Hkv * D, 14336
+    r = np.random.default_rng(31 + S)
+    nq, nk, total = B * S * H * D, B * S * Hkv * D, 14336 * S
+    layout = {name: (o * S, n * S) for name, (o, n) in LAST_LAYER.items()}
     q = r.uniform(-1, 1, nq).astype(np.float32)
     k = r.uniform(-1, 1, nk).astype(np.float32)
     v = r.uniform(-1, 1, nk).astype(np.float32)
     cache = r.uniform(-1, 1, B * 2 * max_seq * Hkv * D).astype(np.float32)
-    pos = np.full(B * S, past, np.uint32)
+    pos = (past + np.arange(B * S)).astype(np.uint32)
     init = np.zeros(total, np.float32)
     for name, arr in (("q", q), ("k", k), ("v", v)):
-        o, n = LAST_LAYER[name]
+        o, n = layout[name]
         init[o:o + n] = arr
     scratch = hip.upload_new_f32(init)
     cb = hip.upload_new_f32(cache)
     pb = hip.upload_new_u32(pos)
-    proj = r.uniform(-1, 1, 4096).astype(np.float32)
+    proj = r.uniform(-1, 1, 4096 * S).astype(np.float32)
     pr = hip.upload_new_f32(proj)
-    ref = {name: BufferRef(scratch, o, n) for name, (o, n) in LAST_LAYER.items()}
+    ref = {name: BufferRef(scratch, o, n) for name, (o, n) in layout.items()}
     posr = BufferRef(pb, 0, B * S)
     qf, kf = Value.f32([B, S, H * D]), Value.f32([B, S, Hkv * D])
     q4, k4 = Value.f32([B, H, S, D]), Value.f32([B, Hkv, S, D])
@@ -217,12 +224,17 @@ def test_attention_group_stages_rotated_q_that_overlaps_its_inputs(hip, projecti
                  [ref["att"]], [q4], [past])
     hip.dispatch(Op.merge_heads(H, D), [ref["att"]], [q4], [ref["merged"]], [qf])
     if projection_after:
-        # in place of the output projection, which writes [4096, 8192)
-        pvv = Value.f32([4096])
-        hip.dispatch(Op.scale_by(2.0), [BufferRef(pr, 0, 4096)], [pvv], [BufferRef(scratch, 4096, 4096)], [pvv])
+        # in place of the output projection, which writes [4096, 8192) per token
+        pvv = Value.f32([4096 * S])
+        hip.dispatch(Op.scale_by(2.0), [BufferRef(pr, 0, 4096 * S)], [pvv], [BufferRef(scratch, 4096 * S, 4096 * S)],
+                     [pvv])
     hip.synchronize()
     after = hip.stats()
-    assert after["fused_commands"] - before["fused_commands"] >= 7
+    fused = after["fused_commands"] - before["fused_commands"]
+    if S == 1 or projection_after:
+        assert fused >= 7
+    else:
+        assert fused == 0
 
     # the op sequence on the oracle, writing the same layout in order
     qh = oracle.split_heads(q, B, S, H, D)
@@ -237,18 +249,18 @@ def test_attention_group_stages_rotated_q_that_overlaps_its_inputs(hip, projecti
     steps = [("qh", qh, 0), ("kh", kh, 0), ("vh", vh, 0), ("qr", qr, 1), ("kr", kr, 1), ("att", att, 2),
              ("merged", merged, 2)]
     for name, val, kd in steps:
-        o, n = LAST_LAYER[name]
+        o, n = layout[name]
         want[o:o + n] = val
         kind[o:o + n] = kd
     if projection_after:
-        want[4096:8192] = proj * np.float32(2.0)
-        kind[4096:8192] = 0
+        want[4096 * S:8192 * S] = proj * np.float32(2.0)
+        kind[4096 * S:8192 * S] = 0
     got = hip.read_f32(scratch, total)
     np.testing.assert_array_equal(got[kind == 0], want[kind == 0])
     assert_elementwise(got[kind == 1], want[kind == 1])
     assert_normwise(got[kind == 2], want[kind == 2])
     # the rotated q tail is what the staged copy wrote
-    assert np.count_nonzero(kind == 1) >= 1024
+    assert np.count_nonzero(kind == 1) >= 1024 * S
     assert_elementwise(hip.read_f32(cb, cache.size), want_cache)
 
 

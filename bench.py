@@ -477,6 +477,56 @@ def cpu_model():
     return "unknown CPU"
 
 
+def paged_decode(dev, cfg, bufs, batch, steps, warmup, max_seq):
+    """Continuous batching through the engine: `batch` prompts of different
+    lengths (640 + 96 b tokens, row b) prefilled one at a time on a batch-1
+    engine and stored into 16-position pages, then decoded together by the
+    batch decode program whose KV State is bound to the pages, every row at
+    its own length (sl_engine_decode_rows). Returns the timing figures."""
+    from starlight_amd import device as hipdev
+    from starlight_amd import engine, graph, synth
+    from starlight_amd.ir import ValueRole
+    from starlight_amd.paged import ContinuousBatcher, PagedKvCache, PagePool
+
+    lengths = [640 + 96 * b for b in range(batch)]
+    cap, page = max(lengths), 16
+    caps = graph.DeviceCapabilities.from_c(hipdev.capabilities())
+    pre = graph.compile_for(graph.lower_llama(cfg, 1, cap, max_seq), caps)
+    pre_dec = graph.compile_for(graph.lower_llama(cfg, 1, 1, max_seq), caps)
+    dec = graph.compile_for(graph.lower_llama(cfg, batch, 1, 16), caps)
+    kv = next(i for i, v in enumerate(pre.ir.values) if v.role == ValueRole.STATE)
+    peng = engine.NativeEngine(dev, engine.compile_program(pre, bufs), engine.compile_program(pre_dec, bufs), 1,
+                               max_seq)
+    deng = engine.NativeEngine(dev, engine.compile_program(dec, bufs), engine.compile_program(dec, bufs), batch, 16)
+    pps = max_seq // page
+    pool = PagePool(num_pages=batch * pps + batch, page_size=page, pages_per_seq=pps, max_batch=batch)
+    cache = PagedKvCache(dev, cfg.layers, cfg.kv_heads, cfg.head_dim, pool)
+    batcher = ContinuousBatcher(dev, peng, peng.state_buffer(kv), max_seq, cap, deng, deng.state_buffer(kv), cache,
+                                cfg.vocab)
+    t0 = time.perf_counter()
+    first = np.zeros(batch, np.uint32)
+    for b, n in enumerate(lengths):
+        first[b] = int(np.argmax(batcher.admit(b, synth.prompt(cfg.vocab, n, 100 + b))))
+    dev.synchronize()
+    prefill_s = time.perf_counter() - t0
+    for b, n in enumerate(lengths):
+        pool.reserve(b, n + warmup + steps + 1)
+    batcher.sync()
+    starts = pool.seq_lens()
+    tokens = deng.decode_rows(first, starts, cache.lens_buffer, warmup)[-1] if warmup else first
+    dev.synchronize()
+    t0 = time.perf_counter()
+    deng.decode_rows(tokens, starts + warmup, cache.lens_buffer, steps)
+    dev.synchronize()
+    elapsed = time.perf_counter() - t0
+    dev.bind_paged_state(deng.state_buffer(kv), None)
+    peng.close()
+    deng.close()
+    mean_keys = float(np.mean(lengths)) + warmup + (steps + 1) / 2
+    return {"tok_s": batch * steps / elapsed, "ms_per_step": elapsed * 1000.0 / steps, "lengths": lengths,
+            "prefill_s": prefill_s, "mean_keys": mean_keys}
+
+
 def fusion_guard(dev, eng, vocab, batch, prompt, positions, prompt_len, steps=8):
     """The benchmarked configuration (fusion on, submissions graph-replayed)
     against the device with both off, on the same prompt and `steps`
@@ -581,6 +631,8 @@ def main():
     ap.add_argument("--int8", action="store_true", help="INT8 g128 weights instead of INT4")
     ap.add_argument("--batch", type=int, default=1, help="sequences decoded together (value counts all of them)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--paged", action="store_true",
+                    help="continuous batching: rows at different lengths in a paged KV cache (--batch rows)")
     ap.add_argument("--mode", choices=["full", "roofline", "copy", "micro"], default="full")
     ap.add_argument("--no-graphs", action="store_true", help="roofline/copy modes: launch eagerly")
     args = ap.parse_args()
@@ -627,6 +679,35 @@ def main():
     bufs = upload_synthetic_weights(dev, cfg, seed=0)
     log(f"weights generated and uploaded in {time.perf_counter() - t0:.1f} s")
     B = args.batch
+    if args.paged:
+        r = paged_decode(dev, cfg, bufs, B, args.steps, args.warmup, max_seq)
+        log(f"paged decode: {r['tok_s']:.1f} tok/s ({r['ms_per_step']:.3f} ms/step, batch {B}, lengths "
+            f"{r['lengths'][0]}..{r['lengths'][-1]}); {B} prefills {r['prefill_s'] * 1000:.1f} ms")
+        linear = 0
+        from starlight_amd.graph import weight_specs
+        for spec in weight_specs(cfg):
+            if spec.quantized:
+                n, k = spec.shape
+                linear += n * k // (2 if cfg.quant == QuantFormat.INT4 else 1) + n * (k // cfg.group) * 4
+            elif spec.kind == "norm":
+                linear += spec.shape[0] * 4
+        step_bytes = linear + B * (cfg.hidden * 4 + r["mean_keys"] * cfg.layers * 2 * cfg.kv_heads * cfg.head_dim * 4)
+        quant_name = "INT8" if args.int8 else "INT4"
+        print(json.dumps({
+            "metric": f"decode tok/s ({label}-shape {quant_name} g128, bs={B}, paged KV, rows at their own lengths)",
+            "value": round(r["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(r["ms_per_step"], 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": f"{'Llama-3-8B' if label == '8B' else '1B-class'}-shaped llama-dense decode, "
+                                   f"{quant_name} g128, batch {B} rows with prompts of "
+                                   f"{r['lengths'][0]}..{r['lengths'][-1]} tokens in a paged KV cache "
+                                   f"(16-position pages), continuous batching",
+                       "batch": B, "prompt_lens": r["lengths"], "kv_capacity": max_seq},
+            "decode_step_bytes": int(step_bytes),
+            "decode_hbm_frac": round(step_bytes / (r["ms_per_step"] * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}),
+            flush=True)
+        dev.close()
+        return
     from starlight_amd import device as hipdev
     caps = graph.DeviceCapabilities.from_c(hipdev.capabilities())
     pre = engine.compile_program(graph.compile_for(graph.lower_llama(cfg, B, prompt_len, max_seq), caps), bufs)

@@ -117,6 +117,18 @@ sl_status sl_engine_decode(sl_engine *engine, uint32_t token, uint32_t past_len,
 sl_status sl_engine_decode_batch(sl_engine *engine, const uint32_t *tokens, uint32_t past_len, uint32_t steps,
                                  uint32_t *tokens_out);
 
+/* Greedy decode of a batch whose rows sit at their own lengths, for a
+ * decode program whose KV State is bound to a paged cache
+ * (sl_hip_bind_paged_state; no reference counterpart, gaps G-17 / G-18,
+ * ARCH-0008:123-124): in step s row b takes its token at position
+ * positions[b] + s; before each step those positions are written to the
+ * u32 buffer `lengths` (the binding's seq_lens, one word per row), and the
+ * step's past_len scalar is 0 (a paged State does not read it). The block
+ * tables must already cover positions[b] + steps of every row. tokens_out
+ * receives steps x batch ids, step-major. */
+sl_status sl_engine_decode_rows(sl_engine *engine, const uint32_t *tokens, const uint32_t *positions,
+                                uint32_t lengths, uint32_t steps, uint32_t *tokens_out);
+
 /* The BufferId the engine allocated for a State value (e.g. to inspect or
  * reset the KV cache), or UINT32_MAX. */
 uint32_t sl_engine_state_buffer(const sl_engine *engine, uint32_t value);

@@ -277,6 +277,39 @@ sl_status sl_hip_paged_attention(sl_hip_device *device, const sl_op *op, const s
                                  const sl_buffer_ref *k_new, const sl_buffer_ref *v_new, const sl_buffer_ref *out,
                                  uint32_t batch, const sl_paged_kv *kv);
 
+/* Continuous batching through a compiled decode program (no reference
+ * counterpart: gaps G-17 / G-18, ARCH-0008:123-124). Binds the State buffer
+ * `state` (the KV cache value [batch, layers, 2, max_seq, kv_heads,
+ * head_dim] of a program) to the paged cache `kv`; kv == NULL removes the
+ * binding. While bound, every CausalAttention command whose State port is
+ * `state` reads and appends K/V through the block tables instead: row b
+ * attends over its own seq_lens[b] cached positions plus its new token and
+ * appends at position seq_lens[b]; the command's past_len scalar is not
+ * read (pass 0). The lengths and tables are read when the work runs, so a
+ * replayed submission serves every step; upload them before the step, and
+ * advance seq_lens after it. dispatch() then fails with Unimplemented for a
+ * CausalAttention on `state` with more than one token per row or a KvAppend
+ * on it, and with Execution for the table checks of sl_hip_paged_attention
+ * or a pool whose size does not match the command's layers, kv_heads and
+ * head_dim. Logged commands are submitted first; cached graphs are dropped.
+ * Errors: InvalidBuffer for a state that is not an f32 buffer or pool /
+ * table / lengths buffers of the wrong kind; Unimplemented for tables or
+ * lengths above 16 MiB or page_size not a multiple of 16. */
+sl_status sl_hip_bind_paged_state(sl_hip_device *device, uint32_t state, const sl_paged_kv *kv);
+
+/* Copies positions [0, length) of batch index `index` of a contiguous KV
+ * State buffer `state` ([batch, layers, 2, max_seq, kv_heads, head_dim], as
+ * a prefill program wrote it) into row `row` of the paged cache `kv`, every
+ * layer's K and V, through the row's block table: how a sequence prefilled
+ * on its own joins a paged decode batch. Logged commands are submitted
+ * first; the copy is enqueued at once. Errors: Execution when a position
+ * below `length` falls outside the row's table, a page id is not below
+ * num_pages, length exceeds max_seq, or the buffer sizes do not match;
+ * InvalidBuffer for buffers of the wrong kind. No reference counterpart. */
+sl_status sl_hip_paged_store(sl_hip_device *device, const sl_paged_kv *kv, uint32_t row, uint32_t state,
+                             uint32_t index, uint32_t max_seq, uint32_t kv_heads, uint32_t head_dim,
+                             uint32_t length);
+
 /* One entry of the buffer table sl_hip_validate_dispatch checks against. */
 typedef enum sl_buffer_kind {
     SL_BUFFER_NONE = 0,

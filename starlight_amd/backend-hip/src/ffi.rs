@@ -248,6 +248,18 @@ extern "C" {
         batch: u32,
         kv: *const sl_paged_kv,
     ) -> sl_status;
+    pub fn sl_hip_bind_paged_state(device: *mut sl_hip_device, state: u32, kv: *const sl_paged_kv) -> sl_status;
+    pub fn sl_hip_paged_store(
+        device: *mut sl_hip_device,
+        kv: *const sl_paged_kv,
+        row: u32,
+        state: u32,
+        index: u32,
+        max_seq: u32,
+        kv_heads: u32,
+        head_dim: u32,
+        length: u32,
+    ) -> sl_status;
     pub fn sl_hip_validate_dispatch(
         buffers: *const sl_buffer_desc,
         n_buffers: usize,

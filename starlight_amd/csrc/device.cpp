@@ -101,6 +101,13 @@ struct Device : BufferView {
     uint32_t* dyn = nullptr;  // device past_len slots, kLogFlushLength of them
     std::vector<uint32_t> dyn_values;
     std::vector<uint32_t> paged_readers;  // host scratch of the paged-attention page check
+    // State buffers bound to a paged cache (sl_hip_bind_paged_state)
+    std::vector<std::pair<uint32_t, sl_paged_kv>> paged_states;
+    const sl_paged_kv* paged_of(uint32_t state) const {
+        for (const auto& p : paged_states)
+            if (p.first == state) return &p.second;
+        return nullptr;
+    }
     std::vector<uint64_t> key, prev_key;
     std::vector<GraphEntry> graphs;
     size_t last_graph = SIZE_MAX;  // entry of graphs the previous replay or capture used
@@ -326,6 +333,28 @@ hipError_t launch(Device* d, const Plan& p, const sl_buffer_ref* in, const sl_bu
             return launch_kv_append(fptr(d, in[0]), fptr(d, in[1]), fptr(d, in[p.state_index]), p.batch, p.layers,
                                     p.layer, p.kv_heads, p.head_dim, p.max_seq, p.past_len, p.seq, dyn, s);
         case SL_OP_CAUSAL_ATTENTION: {
+            if (const sl_paged_kv* kv = d->paged_of(in[p.state_index].buffer)) {
+                PagedAttentionArgs a{};
+                a.q = fptr(d, in[0]);
+                a.k_new = fptr(d, in[1]);
+                a.v_new = fptr(d, in[2]);
+                a.pool = static_cast<float*>(d->buffers[kv->pool].ptr);
+                a.out = fptr(d, out[0]);
+                a.block_table = static_cast<const uint32_t*>(d->buffers[kv->block_table].ptr);
+                a.seq_lens = static_cast<const uint32_t*>(d->buffers[kv->seq_lens].ptr);
+                a.batch = p.batch;
+                a.layers = kv->layers;
+                a.layer = p.layer;
+                a.heads = p.heads;
+                a.kv_heads = p.kv_heads;
+                a.head_dim = p.head_dim;
+                a.num_pages = kv->num_pages;
+                a.page_size = kv->page_size;
+                a.pages_per_seq = kv->pages_per_seq;
+                a.scale = p.scale;
+                if (paged_attention_workspace_floats(a) > ws.floats) return hipErrorNotSupported;
+                return launch_paged_attention(a, ws, s);
+            }
             AttentionArgs a{fptr(d, in[0]), fptr(d, in[1]), fptr(d, in[2]), fptr(d, in[p.state_index]),
                             fptr(d, out[0]), p.batch, p.layers, p.layer, p.heads, p.kv_heads, p.seq,
                             p.past_len, p.head_dim, p.max_seq, p.scale, dyn};
@@ -381,6 +410,119 @@ bool mfma_weight(const Device* d, const Logged& c, size_t port) {
     if (!c.plan.quant[port].present) return false;
     const Buffer& b = d->buffers[c.in[port].buffer];
     return b.layout == QuantLayout::Mfma && b.tile_scales != nullptr;
+}
+
+// The paged cache's buffers: pool f32 of layers * num_pages * 2 * page_size
+// * kv_heads * head_dim elements, block table and lengths u32 buffers with
+// host copies, page_size a multiple of the decode tile.
+bool check_paged_buffers(const Device* d, const sl_paged_kv& kv, uint64_t kv_heads, uint64_t head_dim,
+                         Error* err) {
+    if (kv.page_size == 0 || kv.page_size % 16 != 0) {
+        *err = Error::unimplemented("page_size must be a nonzero multiple of 16");
+        return false;
+    }
+    if (kv.layers == 0 || kv.num_pages == 0 || kv.pages_per_seq == 0) {
+        *err = Error::execution("the page pool is empty");
+        return false;
+    }
+    if (kv.pool >= d->buffers.size() || d->buffers[kv.pool].desc.kind != SL_BUFFER_F32) {
+        *err = Error::invalid_buffer(kv.pool);
+        return false;
+    }
+    for (uint32_t id : {kv.block_table, kv.seq_lens})
+        if (id >= d->buffers.size() || d->buffers[id].desc.kind != SL_BUFFER_U32) {
+            *err = Error::invalid_buffer(id);
+            return false;
+        }
+    if (!d->buffers[kv.block_table].mirrored || !d->buffers[kv.seq_lens].mirrored) {
+        *err = Error::unimplemented("block table and lengths must be u32 buffers of at most 16 MiB");
+        return false;
+    }
+    if (kv_heads != 0 && d->buffers[kv.pool].desc.elements !=
+                             static_cast<uint64_t>(kv.layers) * kv.num_pages * 2 * kv.page_size * kv_heads * head_dim) {
+        *err = Error::execution("page pool size does not match its layout");
+        return false;
+    }
+    return true;
+}
+
+// The block tables and lengths of rows 0..B-1, from the host copies: every
+// position 0..L of a row maps to a page below num_pages, and the page a row
+// appends into is read by no other row (rows run in parallel; pages shared
+// read-only, such as a common prefix, are fine).
+bool check_paged_tables(Device* d, const sl_paged_kv& kv, uint64_t B, Error* err) {
+    const Buffer& tb = d->buffers[kv.block_table];
+    const Buffer& lb = d->buffers[kv.seq_lens];
+    if (tb.desc.elements < B * kv.pages_per_seq || lb.desc.elements < B) {
+        *err = Error::execution("block table or lengths buffer is too small for the batch");
+        return false;
+    }
+    for (uint64_t b = 0; b < B; ++b) {
+        const uint64_t L = lb.mirror[b];
+        if (L / kv.page_size >= kv.pages_per_seq) {
+            *err = Error::execution("paged KV length exceeds the row's block table");
+            return false;
+        }
+        for (uint64_t pi = 0; pi <= L / kv.page_size; ++pi)
+            if (tb.mirror[b * kv.pages_per_seq + pi] >= kv.num_pages) {
+                *err = Error::execution("page id out of range");
+                return false;
+            }
+    }
+    // readers[p]: the one row reading page p, kNone, or kShared for several
+    constexpr uint32_t kNone = 0xffffffffu, kShared = 0xfffffffeu;
+    std::vector<uint32_t>& readers = d->paged_readers;
+    readers.assign(kv.num_pages, kNone);
+    for (uint64_t b = 0; b < B; ++b)
+        for (uint64_t pi = 0; pi <= lb.mirror[b] / kv.page_size; ++pi) {
+            uint32_t& r = readers[tb.mirror[b * kv.pages_per_seq + pi]];
+            r = (r == kNone || r == b) ? static_cast<uint32_t>(b) : kShared;
+        }
+    for (uint64_t b = 0; b < B; ++b)
+        if (readers[tb.mirror[b * kv.pages_per_seq + lb.mirror[b] / kv.page_size]] != b) {
+            *err = Error::execution("a row appends into a page another row reads");
+            return false;
+        }
+    return true;
+}
+
+// A command on a State buffer bound to a paged cache: CausalAttention with
+// one new token per row over pages that its shapes match.
+bool check_paged_command(Device* d, const Plan& p, const sl_paged_kv& kv, Error* err) {
+    if (p.code != SL_OP_CAUSAL_ATTENTION) {
+        *err = Error::unimplemented("only CausalAttention reads a paged State on HipDevice");
+        return false;
+    }
+    if (p.seq != 1) {
+        *err = Error::unimplemented("a paged State takes one new token per row");
+        return false;
+    }
+    if (p.head_dim == 0 || p.head_dim % 64 != 0 || p.head_dim > 256) {
+        *err = Error::unimplemented("paged attention needs head_dim a multiple of 64 up to 256");
+        return false;
+    }
+    if (p.heads / p.kv_heads > 16) {
+        *err = Error::unimplemented("paged attention takes at most 16 query heads per KV head");
+        return false;
+    }
+    if (p.layers != kv.layers) {
+        *err = Error::execution("paged State layers do not match the page pool");
+        return false;
+    }
+    return check_paged_buffers(d, kv, p.kv_heads, p.head_dim, err) && check_paged_tables(d, kv, p.batch, err);
+}
+
+// The paged decode arguments of a CausalAttention on a bound State.
+void set_paged(const Device* d, const sl_paged_kv& kv, AttentionArgs* a) {
+    a->cache = static_cast<float*>(d->buffers[kv.pool].ptr);
+    a->block_table = static_cast<const uint32_t*>(d->buffers[kv.block_table].ptr);
+    a->seq_lens = static_cast<const uint32_t*>(d->buffers[kv.seq_lens].ptr);
+    a->num_pages = kv.num_pages;
+    a->page_size = kv.page_size;
+    a->pages_per_seq = kv.pages_per_seq;
+    a->max_seq = static_cast<uint64_t>(kv.pages_per_seq) * kv.page_size;
+    a->past_len = 0;
+    a->dyn = nullptr;
 }
 
 // An Add right after a command that wrote `o` (rows * n values), adding it to
@@ -681,13 +823,18 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
     // of the unit writes are copied to their place (the rotated q of a last
     // layer, whose tail nothing overwrites before the submission ends).
     const sl_buffer_ref& cache = at.in[ap.state_index];
+    // what the kernels read and write of the cache: the State, or the page
+    // pool bound to it
+    const sl_paged_kv* paged = d->paged_of(cache.buffer);
+    const sl_buffer_ref cache_ref =
+        paged ? sl_buffer_ref{paged->pool, 0, 0, d->buffers[paged->pool].desc.elements} : cache;
     const sl_buffer_ref inter[5] = {sq.out, sk.out, sv.out, rq.out, rk.out};
     const size_t after_reader[5] = {i + 4, i + 5, i + 6, i + 6, i + 6};
     bool live[5], staged[5] = {false, false, false, false, false};
     for (int x = 0; x < 5; ++x) {
         live[x] = !dead_after(d, after_reader[x], inter[x]);
         if (!live[x]) continue;
-        if (overlaps(inter[x], cache)) return 0;
+        if (overlaps(inter[x], cache_ref)) return 0;
         const sl_buffer_ref read[4] = {sq.in[0], sk.in[0], sv.in[0], rq.in[1]};
         for (const sl_buffer_ref& t : read)
             if (overlaps(inter[x], t)) staged[x] = true;
@@ -699,6 +846,7 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
     AttentionArgs a{fptr(d, sq.in[0]), fptr(d, sk.in[0]), fptr(d, sv.in[0]), fptr(d, cache),
                     att_dead ? nullptr : fptr(d, att), B, ap.layers, ap.layer, H, Hkv, S, ap.past_len, D,
                     ap.max_seq, ap.scale, dyn_of(d, at)};
+    if (paged) set_paged(d, *paged, &a);
     // The prefill form writes its rotated q to a workspace area and takes
     // no other live intermediate: a live rotated q (the last layer's, which
     // nothing overwrites before the submission ends) is staged there and
@@ -721,7 +869,7 @@ size_t try_fuse_attention(Device* d, size_t i, hipError_t* err) {
                        B * S <= 16 && mirror_at + B * S * H * D <= ws.floats;
     const bool merged_needed = mh != nullptr && !dead_after(d, i + used, mh->out, chain ? i + used : SIZE_MAX);
     // outputs of the merge kernel: no overlap with the cache, or with each other
-    if (overlaps(att, cache) || (mh && overlaps(mh->out, cache)) ||
+    if (overlaps(att, cache_ref) || (mh && overlaps(mh->out, cache_ref)) ||
         (mh && !att_dead && merged_needed && overlaps(att, mh->out) && !same_ref(att, mh->out)))
         return 0;
     a.positions = uptr(d, rq.in[1]);
@@ -1146,6 +1294,9 @@ sl_status sl_hip_dispatch(sl_hip_device* d, const sl_op* op, const sl_buffer_ref
     if (!slhip::device_limits(plan, d->workspace_floats, &err)) return d->fail(err);
     if (plan.code == SL_OP_GATHER && !slhip::gather_ids_in_range(d, inputs[1], plan.vocab, &err))
         return d->fail(err);
+    if (plan.state_index >= 0)
+        if (const sl_paged_kv* kv = d->paged_of(inputs[plan.state_index].buffer))
+            if (!slhip::check_paged_command(d, plan, *kv, &err)) return d->fail(err);
     slhip::Logged c;
     c.plan = plan;
     c.n_in = static_cast<uint32_t>(n_inputs);
@@ -1194,10 +1345,7 @@ sl_status sl_hip_paged_attention(sl_hip_device* d, const sl_op* op, const sl_buf
     if (D == 0 || D % 64 != 0 || D > 256)
         return d->fail(Error::unimplemented("paged attention needs head_dim a multiple of 64 up to 256"));
     if (H / Hkv > 16) return d->fail(Error::unimplemented("paged attention takes at most 16 query heads per KV head"));
-    if (kv->page_size == 0 || kv->page_size % 16 != 0)
-        return d->fail(Error::unimplemented("page_size must be a nonzero multiple of 16"));
     if (kv->layers == 0 || op->layer >= kv->layers) return d->fail(Error::execution("layer is out of range"));
-    if (kv->num_pages == 0 || kv->pages_per_seq == 0) return d->fail(Error::execution("the page pool is empty"));
     // ports: f32 ranges of the stated sizes, the output disjoint from the inputs
     const struct {
         const sl_buffer_ref* r;
@@ -1214,47 +1362,14 @@ sl_status sl_hip_paged_attention(sl_hip_device* d, const sl_op* op, const sl_buf
     for (int i = 0; i < 3; ++i)
         if (slhip::overlaps(*ports[i].r, *out))
             return d->fail(Error::execution("a command output aliases an overlapping input range"));
-    const uint64_t pool_len = static_cast<uint64_t>(kv->layers) * kv->num_pages * 2 * kv->page_size * Hkv * D;
-    if (kv->pool >= d->buffers.size() || d->buffers[kv->pool].desc.kind != SL_BUFFER_F32)
-        return d->fail(Error::invalid_buffer(kv->pool));
-    if (d->buffers[kv->pool].desc.elements != pool_len)
-        return d->fail(Error::execution("page pool size does not match its layout"));
+    Error err;
+    if (!slhip::check_paged_buffers(d, *kv, Hkv, D, &err)) return d->fail(err);
     for (const auto& pt : ports)
         if (pt.r->buffer == kv->pool)
             return d->fail(Error::execution("a command output aliases an overlapping input range"));
-    for (uint32_t id : {kv->block_table, kv->seq_lens})
-        if (id >= d->buffers.size() || d->buffers[id].desc.kind != SL_BUFFER_U32)
-            return d->fail(Error::invalid_buffer(id));
+    if (!slhip::check_paged_tables(d, *kv, B, &err)) return d->fail(err);
     const slhip::Buffer& tb = d->buffers[kv->block_table];
     const slhip::Buffer& lb = d->buffers[kv->seq_lens];
-    if (!tb.mirrored || !lb.mirrored)
-        return d->fail(Error::unimplemented("block table and lengths must be u32 buffers of at most 16 MiB"));
-    if (tb.desc.elements < B * kv->pages_per_seq || lb.desc.elements < B)
-        return d->fail(Error::execution("block table or lengths buffer is too small for the batch"));
-    // contents, from the host copies: every position 0..L of a row maps to a
-    // page below num_pages
-    for (uint64_t b = 0; b < B; ++b) {
-        const uint64_t L = lb.mirror[b];
-        if (L / kv->page_size >= kv->pages_per_seq)
-            return d->fail(Error::execution("paged KV length exceeds the row's block table"));
-        for (uint64_t pi = 0; pi <= L / kv->page_size; ++pi)
-            if (tb.mirror[b * kv->pages_per_seq + pi] >= kv->num_pages)
-                return d->fail(Error::execution("page id out of range"));
-    }
-    // the page a row appends into is read by no other row (rows run in
-    // parallel; pages shared read-only, such as a common prefix, are fine).
-    // readers[p]: the one row reading page p, kNone, or kShared for several.
-    constexpr uint32_t kNone = 0xffffffffu, kShared = 0xfffffffeu;
-    std::vector<uint32_t>& readers = d->paged_readers;
-    readers.assign(kv->num_pages, kNone);
-    for (uint64_t b = 0; b < B; ++b)
-        for (uint64_t pi = 0; pi <= lb.mirror[b] / kv->page_size; ++pi) {
-            uint32_t& r = readers[tb.mirror[b * kv->pages_per_seq + pi]];
-            r = (r == kNone || r == b) ? static_cast<uint32_t>(b) : kShared;
-        }
-    for (uint64_t b = 0; b < B; ++b)
-        if (readers[tb.mirror[b * kv->pages_per_seq + lb.mirror[b] / kv->page_size]] != b)
-            return d->fail(Error::execution("a row appends into a page another row reads"));
     if (B == 0) return SL_OK;  // an empty batch: nothing to read or append
     if (slhip::flush(d) != SL_OK) return d->last.status;
     slhip::PagedAttentionArgs a{};
@@ -1287,6 +1402,62 @@ sl_status sl_hip_paged_attention(sl_hip_device* d, const sl_op* op, const sl_buf
 sl_status sl_hip_synchronize(sl_hip_device* d) {
     if (slhip::flush(d) != SL_OK) return d->last.status;
     hipError_t e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) return d->hip_fail(e);
+    return SL_OK;
+}
+
+sl_status sl_hip_bind_paged_state(sl_hip_device* d, uint32_t state, const sl_paged_kv* kv) {
+    using slhip::Error;
+    if (state >= d->buffers.size() || d->buffers[state].desc.kind != SL_BUFFER_F32)
+        return d->fail(Error::invalid_buffer(state));
+    if (kv != nullptr) {
+        Error err;
+        if (!slhip::check_paged_buffers(d, *kv, 0, 0, &err)) return d->fail(err);
+        if (kv->pool == state) return d->fail(Error::execution("a State cannot be bound to itself as a page pool"));
+    }
+    // logged commands read the previous binding; graphs hold its addresses
+    if (slhip::flush(d) != SL_OK) return d->last.status;
+    slhip::drop_graphs(d);
+    auto& v = d->paged_states;
+    for (size_t i = 0; i < v.size(); ++i)
+        if (v[i].first == state) {
+            v.erase(v.begin() + static_cast<std::ptrdiff_t>(i));
+            break;
+        }
+    if (kv != nullptr) v.push_back({state, *kv});
+    return SL_OK;
+}
+
+sl_status sl_hip_paged_store(sl_hip_device* d, const sl_paged_kv* kv, uint32_t row, uint32_t state, uint32_t index,
+                             uint32_t max_seq, uint32_t kv_heads, uint32_t head_dim, uint32_t length) {
+    using slhip::Error;
+    if (kv == nullptr) return d->fail(Error::execution("paged store received a null argument"));
+    Error err;
+    if (!slhip::check_paged_buffers(d, *kv, kv_heads, head_dim, &err)) return d->fail(err);
+    if (state >= d->buffers.size() || d->buffers[state].desc.kind != SL_BUFFER_F32)
+        return d->fail(Error::invalid_buffer(state));
+    const uint64_t row_floats = static_cast<uint64_t>(kv_heads) * head_dim;
+    const uint64_t per_index = static_cast<uint64_t>(kv->layers) * 2 * max_seq * row_floats;
+    if (row_floats == 0 || row_floats % 4 != 0 || per_index == 0 ||
+        d->buffers[state].desc.elements % per_index != 0 || index >= d->buffers[state].desc.elements / per_index)
+        return d->fail(Error::execution("State buffer size does not match [batch, layers, 2, max_seq, kv_heads, "
+                                        "head_dim]"));
+    if (length > max_seq) return d->fail(Error::execution("paged store length exceeds max_seq"));
+    const slhip::Buffer& tb = d->buffers[kv->block_table];
+    if (tb.desc.elements < (static_cast<uint64_t>(row) + 1) * kv->pages_per_seq)
+        return d->fail(Error::execution("block table or lengths buffer is too small for the batch"));
+    if (length != 0) {
+        const uint64_t last = (static_cast<uint64_t>(length) - 1) / kv->page_size;
+        if (last >= kv->pages_per_seq) return d->fail(Error::execution("paged KV length exceeds the row's block table"));
+        for (uint64_t pi = 0; pi <= last; ++pi)
+            if (tb.mirror[static_cast<uint64_t>(row) * kv->pages_per_seq + pi] >= kv->num_pages)
+                return d->fail(Error::execution("page id out of range"));
+    }
+    if (slhip::flush(d) != SL_OK) return d->last.status;
+    const hipError_t e = slhip::launch_paged_store(
+        static_cast<const float*>(d->buffers[state].ptr), static_cast<float*>(d->buffers[kv->pool].ptr),
+        static_cast<const uint32_t*>(tb.ptr) + static_cast<uint64_t>(row) * kv->pages_per_seq, index, kv->layers,
+        max_seq, row_floats, kv->num_pages, kv->page_size, length, d->stream);
     if (e != hipSuccess) return d->hip_fail(e);
     return SL_OK;
 }

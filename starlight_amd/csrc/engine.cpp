@@ -383,6 +383,30 @@ sl_status sl_engine_decode_batch(sl_engine* e, const uint32_t* tokens, uint32_t 
     return SL_OK;
 }
 
+sl_status sl_engine_decode_rows(sl_engine* e, const uint32_t* tokens, const uint32_t* positions, uint32_t lengths,
+                                uint32_t steps, uint32_t* tokens_out) {
+    Program& dc = e->programs[SL_STEP_DECODE];
+    const size_t batch = dc.batch;
+    if (dc.seq != 1 || dc.token_elements != batch || (dc.has_positions && dc.position_elements != batch) ||
+        dc.logits_elements % batch != 0)
+        return slhip_fail_execution(e->device, "decode program is not one token per row");
+    const size_t vocab = dc.logits_elements / batch;
+    std::vector<uint32_t> cur(tokens, tokens + batch), pos(positions, positions + batch);
+    for (uint32_t s = 0; s < steps; ++s) {
+        sl_status st = sl_hip_upload_u32(e->device, lengths, pos.data(), batch);
+        if (st != SL_OK) return st;
+        st = sl_engine_step(e, SL_STEP_DECODE, cur.data(), batch, pos.data(), batch, 1, 0, e->logits_host.data(),
+                            dc.logits_elements);
+        if (st != SL_OK) return st;
+        for (size_t b = 0; b < batch; ++b) {
+            cur[b] = first_argmax(e->logits_host.data() + b * vocab, vocab);
+            tokens_out[static_cast<size_t>(s) * batch + b] = cur[b];
+            ++pos[b];
+        }
+    }
+    return SL_OK;
+}
+
 sl_status sl_engine_decode(sl_engine* e, uint32_t token, uint32_t past_len, uint32_t steps,
                            uint32_t* tokens_out) {
     const Program& dc = e->programs[SL_STEP_DECODE];

@@ -989,6 +989,17 @@ Geo make_geo(const AttentionArgs& a, const Workspace& ws) {
     g.q_rot = a.q_rot;
     g.k_rot = a.k_rot;
     g.rope_tab = a.rope_table;
+    if (a.block_table != nullptr) {  // paged cache: a pool of pages, rows at their own lengths
+        const uint64_t row = a.kv_heads * a.head_dim;
+        g.parity_stride = static_cast<uint64_t>(a.page_size) * row;
+        g.page_stride = 2 * g.parity_stride;
+        g.layer_offset = a.layer * a.num_pages * g.page_stride;
+        g.batch_stride = 0;
+        g.block_table = a.block_table;
+        g.seq_past = a.seq_lens;
+        g.page_size = a.page_size;
+        g.pages_per_seq = a.pages_per_seq;
+    }
     return g;
 }
 
@@ -1030,10 +1041,11 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
     g.chunk = kDecodeTile;
     const dim3 grid(static_cast<unsigned>(parts), g.kv_heads, static_cast<unsigned>(a.batch));
     const size_t lds = fused ? a.seq * a.head_dim * sizeof(float) : 0;
-#define SL_DECODE(DVv, RTv)                                                   \
-    (fused ? attn_decode<DVv, RTv, true, false><<<grid, 256, lds, s>>>(g)     \
-     : paged ? attn_decode<DVv, RTv, false, true><<<grid, 256, lds, s>>>(g)   \
-           : attn_decode<DVv, RTv, false, false><<<grid, 256, lds, s>>>(g))
+#define SL_DECODE(DVv, RTv)                                                             \
+    (fused ? (paged ? attn_decode<DVv, RTv, true, true><<<grid, 256, lds, s>>>(g)       \
+                    : attn_decode<DVv, RTv, true, false><<<grid, 256, lds, s>>>(g))     \
+     : paged ? attn_decode<DVv, RTv, false, true><<<grid, 256, lds, s>>>(g)             \
+             : attn_decode<DVv, RTv, false, false><<<grid, 256, lds, s>>>(g))
     switch (dv * 100 + rt) {
         case 104: SL_DECODE(1, 4); break;
         case 108: SL_DECODE(1, 8); break;
@@ -1085,17 +1097,12 @@ hipError_t launch_paged_attention(const PagedAttentionArgs& p, const Workspace& 
                     0, p.head_dim, static_cast<uint64_t>(p.pages_per_seq) * p.page_size, p.scale, nullptr};
     if (a.batch * a.heads == 0 || a.head_dim == 0 || a.kv_heads == 0 || p.page_size % kDecodeTile != 0)
         return hipErrorNotSupported;
-    Geo g = make_geo(a, ws);
-    const uint64_t row = static_cast<uint64_t>(p.kv_heads) * p.head_dim;
-    g.parity_stride = p.page_size * row;
-    g.page_stride = 2 * g.parity_stride;
-    g.layer_offset = static_cast<uint64_t>(p.layer) * p.num_pages * g.page_stride;
-    g.batch_stride = 0;
-    g.block_table = p.block_table;
-    g.seq_past = p.seq_lens;
-    g.page_size = p.page_size;
-    g.pages_per_seq = p.pages_per_seq;
-    return launch_decode(a, g, ws, s, false, true);
+    a.block_table = p.block_table;
+    a.seq_lens = p.seq_lens;
+    a.num_pages = p.num_pages;
+    a.page_size = p.page_size;
+    a.pages_per_seq = p.pages_per_seq;
+    return launch_decode(a, make_geo(a, ws), ws, s, false, true);
 }
 
 uint64_t paged_attention_workspace_floats(const PagedAttentionArgs& p) {
@@ -1111,8 +1118,10 @@ uint64_t paged_attention_workspace_floats(const PagedAttentionArgs& p) {
 
 hipError_t launch_attention_fused(const AttentionArgs& a, const Workspace& ws, hipStream_t s) {
     if (a.batch * a.heads * a.seq == 0 || a.head_dim == 0 || a.kv_heads == 0) return hipErrorNotSupported;
-    const hipError_t d = launch_decode(a, make_geo(a, ws), ws, s, true);
-    if (d != hipErrorNotSupported) return d;
+    const bool paged = a.block_table != nullptr;
+    if (paged && (a.seq != 1 || a.page_size % kDecodeTile != 0)) return hipErrorNotSupported;
+    const hipError_t d = launch_decode(a, make_geo(a, ws), ws, s, true, paged);
+    if (d != hipErrorNotSupported || paged) return d;
     // Prefill: prefill_prep (SplitHeads, Rope, KvAppend), then attn_prefill
     // writing the attention output and / or MergeHeads' layout. The rotated q
     // goes to q_rot when set (the caller's staging area, which nothing the

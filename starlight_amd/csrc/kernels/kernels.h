@@ -123,6 +123,14 @@ struct AttentionArgs {
     // Fused form: the Rope sine / cosine table of these positions
     // (launch_rope_sincos), or null to compute it in every block.
     const float* rope_table = nullptr;
+    // Decode form over a paged cache, when block_table is set: `cache` is
+    // the page pool [layers][num_pages][2][page_size][kv_heads][head_dim],
+    // row b has seq_lens[b] cached positions (past_len and max_seq are not
+    // read: the capacity is pages_per_seq * page_size), position j lives in
+    // page block_table[b * pages_per_seq + j / page_size].
+    const uint32_t* block_table = nullptr;
+    const uint32_t* seq_lens = nullptr;
+    uint32_t num_pages = 0, page_size = 0, pages_per_seq = 0;
 };
 // Rope angles' sine and cosine for `tokens` positions: table[t * head_dim +
 // pair] = sin, table[t * head_dim + head_dim / 2 + pair] = cos, from f64
@@ -173,6 +181,14 @@ struct PagedAttentionArgs {
     float scale;
 };
 hipError_t launch_paged_attention(const PagedAttentionArgs& p, const Workspace& ws, hipStream_t s);
+// Copies positions [0, length) of batch index `index` of a contiguous cache
+// [batch, layers, 2, max_seq, kv_heads, head_dim] into the pages `table`
+// (pages_per_seq ids) of a pool [layers][num_pages][2][page_size][row_floats]
+// with row_floats = kv_heads * head_dim (a multiple of 4). The caller checks
+// the table.
+hipError_t launch_paged_store(const float* state, float* pool, const uint32_t* table, uint64_t index,
+                              uint64_t layers, uint64_t max_seq, uint64_t row_floats, uint64_t num_pages,
+                              uint64_t page_size, uint64_t length, hipStream_t s);
 uint64_t paged_attention_workspace_floats(const PagedAttentionArgs& p);
 
 // ---- dense f32 matmul (reference/matmul.rs) ----

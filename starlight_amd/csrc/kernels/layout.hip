@@ -96,6 +96,28 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
     }
 }
 
+// Row `index` of a contiguous cache [B, layers, 2, max_seq, row] -> pages of
+// a pool [layers][num_pages][2][page_size][row]: float4 i of every cached
+// row of positions [0, length), position j in page table[j / page_size].
+__global__ __launch_bounds__(256) void paged_store_rows(const float* __restrict__ state, float* __restrict__ pool,
+                                                        const uint32_t* __restrict__ table, uint64_t index,
+                                                        uint64_t layers, uint64_t max_seq, uint64_t row4,
+                                                        uint64_t num_pages, uint64_t page_size, uint64_t length,
+                                                        uint64_t total) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const uint64_t c = i % row4;
+        uint64_t rest = i / row4;
+        const uint64_t j = rest % length;
+        rest /= length;
+        const uint64_t kv = rest % 2, layer = rest / 2;
+        const uint64_t src = (((index * layers + layer) * 2 + kv) * max_seq + j) * row4 + c;
+        const uint64_t dst = (((layer * num_pages + table[j / page_size]) * 2 + kv) * page_size + j % page_size) *
+                                 row4 + c;
+        reinterpret_cast<float4*>(pool)[dst] = reinterpret_cast<const float4*>(state)[src];
+    }
+}
+
 }  // namespace
 
 hipError_t launch_gather(const float* table, const uint32_t* ids, float* out, uint64_t rows,
@@ -148,6 +170,17 @@ hipError_t launch_kv_append(const float* k, const float* v, float* cache, uint64
     else
         kv_append_kernel<1><<<grid, 256, 0, s>>>(k, v, cache, kv_heads, head_dim, seq, batch_stride,
                                                  layer * layer_stride, parity_stride, past_len, dyn, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_paged_store(const float* state, float* pool, const uint32_t* table, uint64_t index,
+                              uint64_t layers, uint64_t max_seq, uint64_t row_floats, uint64_t num_pages,
+                              uint64_t page_size, uint64_t length, hipStream_t s) {
+    if (row_floats % 4 != 0 || !aligned16(state) || !aligned16(pool) || page_size == 0) return hipErrorInvalidValue;
+    const uint64_t row4 = row_floats / 4, total = layers * 2 * length * row4;
+    if (total == 0) return hipSuccess;
+    paged_store_rows<<<grid_for(total, 256, 256 * 16), 256, 0, s>>>(state, pool, table, index, layers, max_seq, row4,
+                                                                   num_pages, page_size, length, total);
     return hipGetLastError();
 }
 

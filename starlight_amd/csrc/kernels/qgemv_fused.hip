@@ -34,6 +34,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 // Calls f(std::integral_constant<int, I>) for I = 0 .. N-1, unrolled.
 template <int I, int N, typename F>
@@ -76,6 +77,12 @@ constexpr uint32_t kLimbPad = 64;
 constexpr int kMaxF4 = 8;  // float4 of activations per thread, at most
 // activations a block holds: 16384 with 8 waves, 32768 with 16
 constexpr uint32_t max_elems(int w) { return static_cast<uint32_t>(w) * kWave * 4 * kMaxF4; }
+// float4 of scales each thread loads at launch: a block's tiles hold at
+// most this many per thread (more spills the registers of the pair kernels
+// and of INT8 with group 64)
+constexpr int qgemv_scale_slots(int nt, int gps, int bits) {
+    return (nt == 2 || (bits == 8 && gps == 2) ? 1 : 2) * gps;
+}
 // static LDS of the kernel with W waves: red, row_val, cfac, wres
 constexpr size_t static_lds(int w) { return sizeof(float) * (kMaxF4 * w + 16 + max_elems(w) / 256 + 2 * w * 16 * 16); }
 
@@ -96,15 +103,15 @@ struct Args {
     uint32_t m, k, group, unit, sb_total, groups_total, sb_per_wave;
     uint32_t tiles_total;  // block tiles (pair mode: gate tiles)
     uint32_t epilogue;
+    uint32_t tile_slots;   // tiles one block holds at most (LDS areas are sized for it)
 };
 
 
-// One weight superblock of a wave's stream: codes (16 bytes per lane, INT8
-// two loads) and the scales of its groups for the lane's row.
+// One weight superblock of a wave's stream: its codes, 16 bytes per lane
+// (INT8: two loads). The scales of the block's tiles wait in LDS.
 template <int BITS>
 struct Item {
     uint4 c0, c1;
-    float s0, s1;  // s1: the second group's scale (group 64 only)
 };
 
 // SPG: 64-k steps per group (1: group 64, 2: group 128, 0: a multiple of 256,
@@ -130,7 +137,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     constexpr int PF = 4;  // superblocks in flight per wave
     constexpr int WPT = kWaves / NT;  // waves per tile
     constexpr uint32_t SB_BYTES = BITS == 4 ? 1024 : 2048;
-    extern __shared__ __align__(16) int8_t limbs[];  // [3][m][k + kLimbPad], tres [tiles][16][m]
+    // [3][m][k + kLimbPad] limbs, tres [tile_slots][16][m] results, tsc
+    // [tile_slots][NT][sb][16][gps] scales
+    extern __shared__ __align__(16) int8_t limbs[];
     __shared__ float red[kMaxF4][kWaves];
     __shared__ float row_val[16];
     __shared__ float cfac[max_elems(W) / 256];  // per 256-element chunk: 2^(E-22)
@@ -144,6 +153,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     const uint32_t a_stride4 = SLICED ? gridDim.y * K4 : K4;
     const uint32_t RS = K + kLimbPad;  // limb row stride
     float* tres = reinterpret_cast<float*>(limbs + 3 * M * RS);
+    float* tsc = tres + 16 * M * p.tile_slots;
 
     // ---- activations first, from the leading arguments alone (the
     // prologue waits for them only): element float4 f = tid + kThreads * u
@@ -228,28 +238,70 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     const uint32_t nlive = sbA < p.sb_total ? min(len, p.sb_total - sbA) : 0;
     const uint32_t sb0 = min(sbA, p.sb_total - 1);
     constexpr uint32_t kMetaLive = 1u << 16, kMetaTileEnd = 1u << 17;
-    uint32_t tw_lo, tw_hi, ts_lo, ts_hi, tmeta;
+    uint32_t tw_lo, tw_hi, tmeta;
+    // Segment si's scale array as segment 0's plus a difference chosen per
+    // lane: a per-lane choice among the three pointers compiles to an
+    // indexed load from a scratch copy of the argument block.
+    static_assert(kFusedMaxSegs == 3, "one scale pointer per segment");
+    const float* const tsc0 = uniform_ptr(p.seg[0].tscales);
+    const int64_t tsc_d1 = uniform_ptr(p.seg[1].tscales) - tsc0;
+    const int64_t tsc_d2 = uniform_ptr(p.seg[2].tscales) - tsc0;
+    // the first superblock of tile `tile` of this slice, in a segment's
+    // tile-ordered arrays
+    auto tile_sb = [&](uint32_t tile) -> uint64_t {
+        return static_cast<uint64_t>(tile) * (SLICED ? sb_stride : p.sb_total) + (SLICED ? ks * p.sb_total : 0u);
+    };
     {
         const uint8_t* s_tiles[kFusedMaxSegs];
-        const float* s_tsc[kFusedMaxSegs];
 #pragma unroll
-        for (uint32_t x = 0; x < kFusedMaxSegs; ++x) {
-            s_tiles[x] = uniform_ptr(p.seg[x].tiles);
-            s_tsc[x] = uniform_ptr(p.seg[x].tscales);
-        }
+        for (uint32_t x = 0; x < kFusedMaxSegs; ++x) s_tiles[x] = uniform_ptr(p.seg[x].tiles);
         const uint32_t i = min(static_cast<uint32_t>(lane), items - 1);
         const uint32_t j = i / len, q = i % len;
         uint32_t tile;
         const uint32_t si = seg_of(blockIdx.x + j * gridDim.x, tile);
-        const uint64_t ts = static_cast<uint64_t>(tile) * (SLICED ? sb_stride : p.sb_total) +
-                            (SLICED ? ks * p.sb_total : 0u) + sb0 + (q < nlive ? q : (nlive ? nlive - 1 : 0));
+        const uint64_t ts = tile_sb(tile) + sb0 + (q < nlive ? q : (nlive ? nlive - 1 : 0));
         const uint64_t w = reinterpret_cast<uint64_t>(SEG_PICK(s_tiles, si) + ts * SB_BYTES);
-        const uint64_t sc = reinterpret_cast<uint64_t>(SEG_PICK(s_tsc, si) + ts * 16 * gps);
         tw_lo = static_cast<uint32_t>(w);
         tw_hi = static_cast<uint32_t>(w >> 32);
-        ts_lo = static_cast<uint32_t>(sc);
-        ts_hi = static_cast<uint32_t>(sc >> 32);
         tmeta = (q < nlive ? (sbA + q) | kMetaLive : 0u) | (q == len - 1 ? kMetaTileEnd : 0u);
+    }
+    // The scales of the block's tiles, [tile j][segment slot][sb][16][gps]
+    // in LDS: each tile's run is contiguous in the tile-ordered scale array,
+    // so the block loads them all at launch, ahead of the codes, at most SC
+    // float4 per thread (the launch caps a block's tiles to fit): per
+    // superblock the loop then issues one code load and reads its scale from
+    // LDS.
+    constexpr int SC = qgemv_scale_slots(NT, GPS, BITS);
+    const uint32_t run4 = p.sb_total * 16 * gps / 4;  // float4 per tile and segment
+    const uint32_t sc4_total = my_tiles * NT * run4;
+    float4 scv[SC];
+    {
+        // float4 f of the block's runs is float4 o of run r = f / run4: the
+        // quotient from a float reciprocal is within one of the true one
+        // (f < 2^16), and one correction each way makes it exact
+        const uint32_t last = sc4_total ? sc4_total - 1 : 0;  // the launch gives every block a tile
+        const float inv = __builtin_amdgcn_rcpf(static_cast<float>(run4));
+        // first tiles of segments 1 and 2 (past the end when absent), as
+        // scalars: a per-lane p.seg[si] would copy the argument block to
+        // scratch memory to index it
+        const uint32_t t1 = __builtin_amdgcn_readfirstlane(p.nseg > 1 ? p.seg[1].tile0 : 0xffffffffu);
+        const uint32_t t2 = __builtin_amdgcn_readfirstlane(p.nseg > 2 ? p.seg[2].tile0 : 0xffffffffu);
+        static_for<SC>([&](auto u_c) {
+            constexpr int u = decltype(u_c)::value;
+            const uint32_t f = min(static_cast<uint32_t>(tid + kThreads * u), last);
+            uint32_t r = static_cast<uint32_t>(static_cast<float>(f) * inv);
+            r = r * run4 > f ? r - 1 : (r + 1) * run4 <= f ? r + 1 : r;
+            const uint32_t o = f - r * run4;
+            uint32_t tile = blockIdx.x + (r / NT) * gridDim.x;
+            uint32_t si = r % NT;
+            if (NT == 1) {
+                si = (tile >= t1 ? 1u : 0u) + (tile >= t2 ? 1u : 0u);
+                tile -= si == 0 ? 0u : si == 1 ? t1 : t2;
+            }
+            const float* const base = tsc0 + (si == 1 ? tsc_d1 : 0) + (si == 2 ? tsc_d2 : 0);
+            const v4f x = global_ptr(reinterpret_cast<const v4f*>(base + tile_sb(tile) * 16 * gps))[o];
+            scv[u] = make_float4(x[0], x[1], x[2], x[3]);
+        });
     }
     auto lane_u64 = [&](uint32_t lo, uint32_t hi, uint32_t k) {
         return static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(hi), k))) << 32 |
@@ -263,14 +315,6 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         if constexpr (BITS == 8) {
             const v4u w1 = wp[64];
             it.c1 = make_uint4(w1[0], w1[1], w1[2], w1[3]);
-        }
-        const auto sp = global_ptr(reinterpret_cast<const float*>(lane_u64(ts_lo, ts_hi, k))) + (lane % 16) * gps;
-        if constexpr (GPS == 2) {
-            const v2f s2 = *reinterpret_cast<const __attribute__((address_space(1))) v2f*>(sp);
-            it.s0 = s2[0];
-            it.s1 = s2[1];
-        } else {
-            it.s0 = sp[0];
         }
     };
 
@@ -406,6 +450,11 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         for (int limb = 0; limb < 3; ++limb)  // row limb * M + r, columns 4 cb[u] + 4 lane
             *reinterpret_cast<uint32_t*>(limb_lane + ((limb * M + r) * RS + 4 * cb[u])) = packed[limb];
     }
+    static_for<SC>([&](auto u_c) {
+        constexpr int u = decltype(u_c)::value;
+        const uint32_t f = tid + kThreads * u;
+        if (f < sc4_total) reinterpret_cast<float4*>(tsc)[f] = scv[u];
+    });
     __syncthreads();
 
     // ---- main loop over the stream ----
@@ -430,6 +479,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     // wave runs are group-aligned, so a group never spans two runs)
     v4i acc0 = zero, acc1 = zero, acc2 = zero;
     uint32_t cj = 0;                      // block tile of the item being consumed
+    // this lane's scales: row lane % 16 of its segment slot, tile cj
+    const float* const tsc_lane = tsc + slot * p.sb_total * 16 * gps + (lane % 16) * gps;
+    const uint32_t tile_stride = NT * p.sb_total * 16 * gps;
     uint32_t gstep = 0;                   // 64-k steps into the current unit
     const int8_t* a_col = limbs + a_off + kb4 * 16;
     // One item of the stream: win[S] is used in place (a copy would make the
@@ -479,7 +531,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
             else group_end = ++gstep == steps_per_unit;
             if (group_end) {
                 if constexpr (SPG == 0) gstep = 0;
-                const float sc = GPS == 2 && st == 1 ? cur.s1 : cur.s0;
+                const float sc = tsc_lane[cj * tile_stride + sbi * 16 * gps + (GPS == 2 && st == 1 ? 1 : 0)];
                 const uint32_t chunk = (sbi * 128 + st * 64) / 256;
                 if constexpr (LR) {
                     // rows 4 * kb4 + limb: this lane holds all three limbs of m = kb4
@@ -666,13 +718,21 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
         per_block = (tiles + max_blocks - 1) / max_blocks;
         blocks = 0;
     }
-    // the per-lane item table holds at most 64 items per wave
-    const uint32_t item_cap = 64 / per, cap = per_cap < item_cap ? per_cap : item_cap;
+    // the per-lane item table holds at most 64 items per wave, and the
+    // tiles' scales at most qgemv_scale_slots float4 per thread
+    const uint32_t gps = p.group == 64 ? 2 : 1, nt = pair ? 2 : 1;
+    const uint32_t scale_cap =
+        static_cast<uint32_t>(qgemv_scale_slots(nt, gps, int4 ? 4 : 8)) * threads / (nt * p.sb_total * 4 * gps);
+    uint32_t item_cap = 64 / per;
+    if (scale_cap < item_cap) item_cap = scale_cap;
+    const uint32_t cap = per_cap < item_cap ? per_cap : item_cap;
     if (cap == 0) return hipErrorNotSupported;
     if (per_block > cap) per_block = cap;
     if (blocks == 0 || per_block == cap) blocks = (tiles + per_block - 1) / per_block;
+    p.tile_slots = per_block;
     const size_t lds = static_cast<size_t>(3) * p.m * (p.k + kLimbPad) +
-                       sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m;
+                       sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m +
+                       sizeof(float) * static_cast<size_t>(per_block) * nt * p.sb_total * 16 * gps;
     if (lds + static_lds(waves) > max_lds_per_block()) return hipErrorNotSupported;
     const int spg = p.group == 64 ? 1 : p.group == 128 ? 2 : 0;
     // Float4 of activations per thread, a compile-time count: the prologue

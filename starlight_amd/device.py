@@ -171,6 +171,8 @@ def load_library() -> ctypes.CDLL:
         "sl_hip_paged_attention": ([P, ctypes.POINTER(ir.COp), ctypes.POINTER(ir.CBufferRef),
                                     ctypes.POINTER(ir.CBufferRef), ctypes.POINTER(ir.CBufferRef),
                                     ctypes.POINTER(ir.CBufferRef), ctypes.c_uint32, ctypes.c_void_p], ctypes.c_int),
+        "sl_hip_bind_paged_state": ([P, ctypes.c_uint32, ctypes.c_void_p], ctypes.c_int),
+        "sl_hip_paged_store": ([P, ctypes.c_void_p] + [ctypes.c_uint32] * 7, ctypes.c_int),
         "sl_hip_synchronize": ([P], ctypes.c_int),
         "sl_hip_last_error": ([P, ctypes.POINTER(ir.CError)], None),
         "sl_hip_bind_quantized": ([P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
@@ -312,6 +314,20 @@ class HipDevice:
         refs = [r.to_c() for r in (q, k_new, v_new, out)]
         self._check(self._lib.sl_hip_paged_attention(self._h, ctypes.byref(c_op), *[ctypes.byref(r) for r in refs],
                                                       batch, ctypes.addressof(paged_kv)))
+
+    def bind_paged_state(self, state: int, paged_kv=None) -> None:
+        """sl_hip_bind_paged_state: CausalAttention commands on the State
+        buffer `state` read and append through the paged cache `paged_kv`
+        (an sl_paged_kv structure; None removes the binding)."""
+        self._check(self._lib.sl_hip_bind_paged_state(
+            self._h, state, None if paged_kv is None else ctypes.addressof(paged_kv)))
+
+    def paged_store(self, paged_kv, row: int, state: int, index: int, max_seq: int, kv_heads: int, head_dim: int,
+                    length: int) -> None:
+        """sl_hip_paged_store: positions [0, length) of batch index `index`
+        of a contiguous KV State into row `row`'s pages."""
+        self._check(self._lib.sl_hip_paged_store(self._h, ctypes.addressof(paged_kv), row, state, index, max_seq,
+                                                 kv_heads, head_dim, length))
 
     def synchronize(self) -> None:
         self._check(self._lib.sl_hip_synchronize(self._h))

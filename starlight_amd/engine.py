@@ -165,6 +165,8 @@ def _declare_engine(lib):
     lib.sl_engine_decode.restype = ctypes.c_int
     lib.sl_engine_decode_batch.argtypes = [P, U32P, ctypes.c_uint32, ctypes.c_uint32, U32P]
     lib.sl_engine_decode_batch.restype = ctypes.c_int
+    lib.sl_engine_decode_rows.argtypes = [P, U32P, U32P, ctypes.c_uint32, ctypes.c_uint32, U32P]
+    lib.sl_engine_decode_rows.restype = ctypes.c_int
     lib.sl_engine_state_buffer.argtypes = [P, ctypes.c_uint32]
     lib.sl_engine_state_buffer.restype = ctypes.c_uint32
     lib.sl_engine_destroy.argtypes = [P]
@@ -243,6 +245,17 @@ class NativeEngine:
         first = np.ascontiguousarray(tokens, dtype=np.uint32)
         out = np.zeros((max(steps, 1), first.size), np.uint32)
         self._raise(self._lib.sl_engine_decode_batch(self._h, _u32p(first), past_len, steps, _u32p(out)))
+        return out[:steps]
+
+    def decode_rows(self, tokens, positions, lengths_buffer: int, steps: int) -> np.ndarray:
+        """Greedy decode of rows at their own positions (a decode program
+        whose KV State is bound to a paged cache; `lengths_buffer` is the
+        binding's seq_lens): ids [steps, batch]."""
+        first = np.ascontiguousarray(tokens, dtype=np.uint32)
+        pos = np.ascontiguousarray(positions, dtype=np.uint32)
+        out = np.zeros((max(steps, 1), first.size), np.uint32)
+        self._raise(self._lib.sl_engine_decode_rows(self._h, _u32p(first), _u32p(pos), lengths_buffer, steps,
+                                                    _u32p(out)))
         return out[:steps]
 
     def state_buffer(self, value: int) -> int:

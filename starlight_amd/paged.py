@@ -124,3 +124,117 @@ class PagedKvCache:
         if missing:
             raise ValueError(f"rows {missing} hold no sequence")
         self.device.paged_attention(op, q, k_new, v_new, out, batch, self.c_struct())
+
+    def bind_state(self, state_buffer: int) -> None:
+        """Binds a decode program's KV State buffer to this cache
+        (sl_hip_bind_paged_state): its CausalAttention commands then read
+        and append through the block tables at each row's own length."""
+        self.device.bind_paged_state(state_buffer, self.c_struct())
+
+    def store(self, seq, state_buffer: int, index: int, max_seq: int, length: int) -> None:
+        """Copies positions [0, length) of batch index `index` of a
+        contiguous KV State (a prefill program's) into `seq`'s pages, which
+        must already be reserved (sl_hip_paged_store)."""
+        self.sync()
+        self.device.paged_store(self.c_struct(), self.pool.rows[seq], state_buffer, index, max_seq, self.kv_heads,
+                                self.head_dim, length)
+
+
+class ContinuousBatcher:
+    """Continuous batching through the engine: the per-step calls a request
+    scheduler makes (the scheduler itself, admission policy and sampling
+    are the control plane's and not part of this backend).
+
+    A batch-1 prefill engine runs each new prompt on its own contiguous KV
+    State (padded to the compiled prompt length; LastToken takes the last
+    real token), and the prompt's K/V rows are stored into the sequence's
+    pages. A batch-`max_batch` decode engine, whose KV State is bound to the
+    paged cache, then decodes every admitted sequence in one step at its own
+    length: row b reads its seq_lens[b] cached positions and appends one.
+    Rows without a sequence hold a placeholder with one page of its own, so
+    every row's append has a page no other row reads; their logits are
+    ignored.
+    """
+
+    def __init__(self, device, prefill_engine, prefill_state: int, prefill_max_seq: int, prompt_capacity: int,
+                 decode_engine, decode_state: int, cache: PagedKvCache, vocab: int):
+        self.device, self.cache, self.pool = device, cache, cache.pool
+        self.prefill_engine, self.prefill_state = prefill_engine, prefill_state
+        self.prefill_max_seq, self.prompt_capacity = prefill_max_seq, prompt_capacity
+        self.decode_engine, self.vocab = decode_engine, vocab
+        self.batch = self.pool.max_batch
+        self._idle = {}  # row -> placeholder key
+        for row in range(self.batch):
+            self._park(row)
+        self._tables = None
+        cache.bind_state(decode_state)
+
+    def _park(self, row: int) -> None:
+        key = ("idle", row)
+        assert self.pool.admit(key) == row
+        self.pool.set_length(key, 0)
+        self._idle[row] = key
+
+    def sync(self) -> None:
+        """Uploads the block tables (when they changed) and the lengths."""
+        tables = self.pool.tables()
+        if self._tables is None or not np.array_equal(tables, self._tables):
+            self.device.upload_u32(self.cache.table_buffer, tables.ravel())
+            self._tables = tables
+        self.device.upload_u32(self.cache.lens_buffer, self.pool.seq_lens())
+
+    def sequences(self) -> Dict[object, int]:
+        """Active sequence -> batch row."""
+        return {s: r for s, r in self.pool.rows.items() if not (isinstance(s, tuple) and s[:1] == ("idle",))}
+
+    def admit(self, seq, prompt) -> np.ndarray:
+        """Prefills `prompt` for a new sequence in a free row and returns the
+        logits of its last token."""
+        prompt = np.asarray(prompt, np.uint32)
+        n = prompt.size
+        if n == 0 or n > self.prompt_capacity:
+            raise ValueError(f"prompt length {n} is outside 1..{self.prompt_capacity}")
+        if not self._idle:
+            raise ValueError("every batch row is in use")
+        row = min(self._idle)
+        self.pool.release(self._idle.pop(row))
+        assert self.pool.admit(seq) == row
+        try:
+            self.pool.set_length(seq, n)
+        except Exception:
+            self.pool.release(seq)
+            self._park(row)
+            raise
+        tokens = np.zeros(self.prompt_capacity, np.uint32)
+        tokens[:n] = prompt
+        logits = np.zeros(self.vocab, np.float32)
+        self.prefill_engine.step(self.prefill_engine.PREFILL, tokens,
+                                 np.arange(self.prompt_capacity, dtype=np.uint32), n, 0, logits)
+        self.cache.store(seq, self.prefill_state, 0, self.prefill_max_seq, n)
+        self._tables = None
+        return logits
+
+    def release(self, seq) -> None:
+        """The sequence leaves: its pages return to the pool, its row idles."""
+        row = self.pool.rows[seq]
+        self.pool.release(seq)
+        self._park(row)
+
+    def step(self, tokens: Dict[object, int]) -> Dict[object, np.ndarray]:
+        """One decode step of every active sequence: `tokens` maps each to
+        its next input token; returns each one's logits. Every sequence's
+        length grows by one."""
+        active = self.sequences()
+        if set(tokens) != set(active):
+            raise ValueError("a decode step takes one token for every active sequence")
+        ids = np.zeros(self.batch, np.uint32)
+        for seq, row in active.items():
+            ids[row] = tokens[seq]
+        positions = self.pool.seq_lens().copy()  # each row's token sits at its cached length
+        self.sync()
+        logits = np.zeros(self.batch * self.vocab, np.float32)
+        self.decode_engine.step(self.decode_engine.DECODE, ids, positions, 1, 0, logits)
+        for key in list(self.pool.rows):
+            self.pool.set_length(key, self.pool.lengths[key] + (0 if key in self._idle.values() else 1))
+        rows = logits.reshape(self.batch, self.vocab)
+        return {seq: rows[row].copy() for seq, row in active.items()}

@@ -78,11 +78,9 @@ constexpr int kMaxF4 = 8;  // float4 of activations per thread, at most
 // activations a block holds: 16384 with 8 waves, 32768 with 16
 constexpr uint32_t max_elems(int w) { return static_cast<uint32_t>(w) * kWave * 4 * kMaxF4; }
 // float4 of scales each thread loads at launch: a block's tiles hold at
-// most this many per thread (more spills the registers of the pair kernels
-// and of INT8 with group 64)
-constexpr int qgemv_scale_slots(int nt, int gps, int bits) {
-    return (nt == 2 || (bits == 8 && gps == 2) ? 1 : 2) * gps;
-}
+// most this many per thread (more spills registers: pair kernels hold one
+// per group of a superblock, INT8 two, INT4 four)
+constexpr int qgemv_scale_slots(int nt, int gps, int bits) { return nt == 2 ? gps : bits == 4 ? 4 : 2; }
 // static LDS of the kernel with W waves: red, row_val, cfac, wres
 constexpr size_t static_lds(int w) { return sizeof(float) * (kMaxF4 * w + 16 + max_elems(w) / 256 + 2 * w * 16 * 16); }
 

@@ -8,8 +8,10 @@
 //  * a block of 8 waves owns one 16-row tile (or, for a gate/up pair, one
 //    tile of each with 4 waves apiece) and the whole K range; its waves take
 //    contiguous, group-aligned runs of superblocks and start their weight
-//    and scale loads (4 superblocks, rolling) before the
-//    activation prologue, then add their partial sums in LDS in wave order.
+//    loads (4 superblocks, rolling) before the activation prologue, then
+//    add their partial sums in LDS in wave order. The group scales come
+//    with each superblock's codes, or (long streams at m = 1) are loaded
+//    into LDS for all the block's tiles at launch.
 //    No split partials in HBM, no second launch, deterministic. Blocks stay
 //    resident over several tiles (at most two per CU), so the prologue is
 //    paid once per block, and the per-tile LDS sums are double-buffered;
@@ -75,6 +77,7 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* global_ptr(T* p)
 // and rows a multiple of the bank width apart would all hit the same banks.
 constexpr uint32_t kLimbPad = 64;
 constexpr int kMaxF4 = 8;  // float4 of activations per thread, at most
+constexpr int kWindow = 4;  // superblocks in flight per wave
 // activations a block holds: 16384 with 8 waves, 32768 with 16
 constexpr uint32_t max_elems(int w) { return static_cast<uint32_t>(w) * kWave * 4 * kMaxF4; }
 // float4 of scales each thread loads at launch: a block's tiles hold at
@@ -106,10 +109,13 @@ struct Args {
 
 
 // One weight superblock of a wave's stream: its codes, 16 bytes per lane
-// (INT8: two loads). The scales of the block's tiles wait in LDS.
+// (INT8: two loads), and unless the scales of the block's tiles wait in LDS,
+// the scales of its groups for the lane's row (s1: the second group of a
+// superblock, group 64 only).
 template <int BITS>
 struct Item {
     uint4 c0, c1;
+    float s0, s1;
 };
 
 // SPG: 64-k steps per group (1: group 64, 2: group 128, 0: a multiple of 256,
@@ -122,21 +128,26 @@ struct Item {
 // p.sb_total, and writes its partial sums m n floats after slice y - 1's
 // (the launcher adds the slices up). Every slice geometry follows from the
 // grid, so the arguments are the same as for one slice.
+// LS: the scales of the block's tiles are loaded into LDS at launch (one
+// load per thread or a few, before the code window) instead of with each
+// superblock's codes; that pays where a wave streams more superblocks than
+// its window holds, and costs a dependent load before the prologue's
+// barrier where it does not.
 // The activations a, the RMSNorm weight gamma (null: no norm) and the
 // m x k shape lead the arguments: the library is built to preload leading
 // scalar arguments into scalar registers, so the activation loads go out
 // at once, while the argument block is still being fetched.
-template <int BITS, int NT, int SPG, bool LR, int F4, int W, bool SLICED>
+template <int BITS, int NT, int SPG, bool LR, int F4, int W, bool SLICED, bool LS>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(
     const float* __restrict__ a_in, const float* __restrict__ gamma, uint32_t m_in, uint32_t k_in, Args p) {
     constexpr int kThreads = W * kWave, kWaves = W;
     static_assert(F4 <= kMaxF4, "activations per thread beyond the block's budget");
     constexpr int GPS = SPG == 1 ? 2 : 1;
-    constexpr int PF = 4;  // superblocks in flight per wave
+    constexpr int PF = kWindow;
     constexpr int WPT = kWaves / NT;  // waves per tile
     constexpr uint32_t SB_BYTES = BITS == 4 ? 1024 : 2048;
-    // [3][m][k + kLimbPad] limbs, tres [tile_slots][16][m] results, tsc
-    // [tile_slots][NT][sb][16][gps] scales
+    // [3][m][k + kLimbPad] limbs, tres [tile_slots][16][m] results, and
+    // with LS tsc [tile_slots][NT][sb][16][gps] scales
     extern __shared__ __align__(16) int8_t limbs[];
     __shared__ float red[kMaxF4][kWaves];
     __shared__ float row_val[16];
@@ -236,7 +247,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     const uint32_t nlive = sbA < p.sb_total ? min(len, p.sb_total - sbA) : 0;
     const uint32_t sb0 = min(sbA, p.sb_total - 1);
     constexpr uint32_t kMetaLive = 1u << 16, kMetaTileEnd = 1u << 17;
-    uint32_t tw_lo, tw_hi, tmeta;
+    uint32_t tw_lo, tw_hi, ts_lo = 0, ts_hi = 0, tmeta;
     // Segment si's scale array as segment 0's plus a difference chosen per
     // lane: a per-lane choice among the three pointers compiles to an
     // indexed load from a scratch copy of the argument block.
@@ -261,19 +272,25 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         const uint64_t w = reinterpret_cast<uint64_t>(SEG_PICK(s_tiles, si) + ts * SB_BYTES);
         tw_lo = static_cast<uint32_t>(w);
         tw_hi = static_cast<uint32_t>(w >> 32);
+        if constexpr (!LS) {
+            const float* const base = tsc0 + (si == 1 ? tsc_d1 : 0) + (si == 2 ? tsc_d2 : 0);
+            const uint64_t sc = reinterpret_cast<uint64_t>(base + ts * 16 * gps);
+            ts_lo = static_cast<uint32_t>(sc);
+            ts_hi = static_cast<uint32_t>(sc >> 32);
+        }
         tmeta = (q < nlive ? (sbA + q) | kMetaLive : 0u) | (q == len - 1 ? kMetaTileEnd : 0u);
     }
-    // The scales of the block's tiles, [tile j][segment slot][sb][16][gps]
-    // in LDS: each tile's run is contiguous in the tile-ordered scale array,
-    // so the block loads them all at launch, ahead of the codes, at most SC
-    // float4 per thread (the launch caps a block's tiles to fit): per
-    // superblock the loop then issues one code load and reads its scale from
-    // LDS.
-    constexpr int SC = qgemv_scale_slots(NT, GPS, BITS);
+    // LS: the scales of the block's tiles, [tile j][segment slot][sb][16]
+    // [gps] in LDS: each tile's run is contiguous in the tile-ordered scale
+    // array, so the block loads them all at launch, ahead of the codes, at
+    // most SC float4 per thread (the launch caps a block's tiles to fit):
+    // per superblock the loop then issues one code load and reads its scale
+    // from LDS.
+    constexpr int SC = LS ? qgemv_scale_slots(NT, GPS, BITS) : 0;
     const uint32_t run4 = p.sb_total * 16 * gps / 4;  // float4 per tile and segment
     const uint32_t sc4_total = my_tiles * NT * run4;
-    float4 scv[SC];
-    {
+    float4 scv[SC > 0 ? SC : 1];
+    if constexpr (LS) {
         // float4 f of the block's runs is float4 o of run r = f / run4: the
         // quotient from a float reciprocal is within one of the true one
         // (f < 2^16), and one correction each way makes it exact
@@ -313,6 +330,16 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         if constexpr (BITS == 8) {
             const v4u w1 = wp[64];
             it.c1 = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+        }
+        if constexpr (!LS) {
+            const auto sp = global_ptr(reinterpret_cast<const float*>(lane_u64(ts_lo, ts_hi, k))) + (lane % 16) * gps;
+            if constexpr (GPS == 2) {
+                const v2f s2 = *reinterpret_cast<const __attribute__((address_space(1))) v2f*>(sp);
+                it.s0 = s2[0];
+                it.s1 = s2[1];
+            } else {
+                it.s0 = sp[0];
+            }
         }
     };
 
@@ -529,7 +556,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
             else group_end = ++gstep == steps_per_unit;
             if (group_end) {
                 if constexpr (SPG == 0) gstep = 0;
-                const float sc = tsc_lane[cj * tile_stride + sbi * 16 * gps + (GPS == 2 && st == 1 ? 1 : 0)];
+                float sc;
+                if constexpr (LS) sc = tsc_lane[cj * tile_stride + sbi * 16 * gps + (GPS == 2 && st == 1 ? 1 : 0)];
+                else sc = GPS == 2 && st == 1 ? cur.s1 : cur.s0;
                 const uint32_t chunk = (sbi * 128 + st * 64) / 256;
                 if constexpr (LR) {
                     // rows 4 * kb4 + limb: this lane holds all three limbs of m = kb4
@@ -716,13 +745,27 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
         per_block = (tiles + max_blocks - 1) / max_blocks;
         blocks = 0;
     }
-    // the per-lane item table holds at most 64 items per wave, and the
-    // tiles' scales at most qgemv_scale_slots float4 per thread
+    // Float4 of activations per thread, a compile-time count: the prologue
+    // is straight-line code run once per wave, fetched cold by every CU at
+    // each launch, so its length shows in the launch time (about 1 us for
+    // the RMSNorm prologue at 8 float4 per thread against 2).
+    const uint32_t f4 = (p.m * p.k / 4 + threads - 1) / threads;
+    // Scales in LDS (LS) for one activation row, k >= 4096 and more
+    // superblocks per wave than the window holds. Measured on MI355X
+    // against scales loaded with each superblock: [14336 x 4096] 8.61 ->
+    // 8.45 us, [4096 x 14336] 9.24 -> 9.00 us, the gate/up pair [2 x 14336
+    // x 4096] 13.62 -> 13.32 us; but [2048 x 8192] (4 superblocks per
+    // wave) 5.80 -> 6.34 us, and M = 8 [14336 x 4096] 13.73 -> 14.38 us.
+    const bool ls = p.m == 1 && slices == 1 && p.k >= 4096 && f4 <= 4 && per_block * per > kWindow;
+    // the per-lane item table holds at most 64 items per wave, and with LS
+    // the tiles' scales at most qgemv_scale_slots float4 per thread
     const uint32_t gps = p.group == 64 ? 2 : 1, nt = pair ? 2 : 1;
-    const uint32_t scale_cap =
-        static_cast<uint32_t>(qgemv_scale_slots(nt, gps, int4 ? 4 : 8)) * threads / (nt * p.sb_total * 4 * gps);
     uint32_t item_cap = 64 / per;
-    if (scale_cap < item_cap) item_cap = scale_cap;
+    if (ls) {
+        const uint32_t scale_cap =
+            static_cast<uint32_t>(qgemv_scale_slots(nt, gps, int4 ? 4 : 8)) * threads / (nt * p.sb_total * 4 * gps);
+        if (scale_cap < item_cap) item_cap = scale_cap;
+    }
     const uint32_t cap = per_cap < item_cap ? per_cap : item_cap;
     if (cap == 0) return hipErrorNotSupported;
     if (per_block > cap) per_block = cap;
@@ -730,29 +773,28 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     p.tile_slots = per_block;
     const size_t lds = static_cast<size_t>(3) * p.m * (p.k + kLimbPad) +
                        sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m +
-                       sizeof(float) * static_cast<size_t>(per_block) * nt * p.sb_total * 16 * gps;
+                       (ls ? sizeof(float) * static_cast<size_t>(per_block) * nt * p.sb_total * 16 * gps : 0);
     if (lds + static_lds(waves) > max_lds_per_block()) return hipErrorNotSupported;
     const int spg = p.group == 64 ? 1 : p.group == 128 ? 2 : 0;
-    // Float4 of activations per thread, a compile-time count: the prologue
-    // is straight-line code run once per wave, fetched cold by every CU at
-    // each launch, so its length shows in the launch time (about 1 us for
-    // the RMSNorm prologue at 8 float4 per thread against 2).
-    const uint32_t f4 = (p.m * p.k / 4 + threads - 1) / threads;
     const dim3 grid(blocks, slices);
-#define SL_QGEMV_FUSED_F(B, T, G, L)                                                                  \
-    (waves == 16 ? (f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 16, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)         \
-                    : f4 <= 4 ? qgemv_fused<B, T, G, L, 4, 16, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)         \
-                              : qgemv_fused<B, T, G, L, 8, 16, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p))        \
-     : f4 <= 2   ? qgemv_fused<B, T, G, L, 2, 8, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)                       \
-     : f4 <= 4   ? qgemv_fused<B, T, G, L, 4, 8, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)                       \
-                 : qgemv_fused<B, T, G, L, 8, 8, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p))
-#define SL_QGEMV_FUSED(B, T, G) (lr ? SL_QGEMV_FUSED_F(B, T, G, true) : SL_QGEMV_FUSED_F(B, T, G, false))
+#define SL_QGEMV_LAUNCH(B, T, G, L, F, W, S) \
+    qgemv_fused<B, T, G, L, F, W, false, S><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)
+#define SL_QGEMV_FUSED_F(B, T, G, L)                                                                               \
+    (waves == 16 ? (f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, L, 2, 16, false)                                             \
+                            : f4 <= 4 ? SL_QGEMV_LAUNCH(B, T, G, L, 4, 16, false) : SL_QGEMV_LAUNCH(B, T, G, L, 8, 16, false)) \
+                 : f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, L, 2, 8, false)                                               \
+                           : f4 <= 4 ? SL_QGEMV_LAUNCH(B, T, G, L, 4, 8, false) : SL_QGEMV_LAUNCH(B, T, G, L, 8, 8, false))
+#define SL_QGEMV_FUSED_LS(B, T, G)                                                                                 \
+    (waves == 16 ? (f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, true, 2, 16, true) : SL_QGEMV_LAUNCH(B, T, G, true, 4, 16, true)) \
+                 : f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, true, 2, 8, true) : SL_QGEMV_LAUNCH(B, T, G, true, 4, 8, true))
+#define SL_QGEMV_FUSED(B, T, G) \
+    (ls ? SL_QGEMV_FUSED_LS(B, T, G) : lr ? SL_QGEMV_FUSED_F(B, T, G, true) : SL_QGEMV_FUSED_F(B, T, G, false))
 #define SL_QGEMV_FUSED_G(B, T) \
     (spg == 1 ? SL_QGEMV_FUSED(B, T, 1) : spg == 2 ? SL_QGEMV_FUSED(B, T, 2) : SL_QGEMV_FUSED(B, T, 0))
     if (slices > 1) {
         // k slices: many rows (not LR), 16 waves, 8 float4 per thread
         if (waves != 16 || f4 > 8 || lr) return hipErrorNotSupported;
-#define SL_QGEMV_SLICED(B, G) qgemv_fused<B, 1, G, false, 8, 16, true><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)
+#define SL_QGEMV_SLICED(B, G) qgemv_fused<B, 1, G, false, 8, 16, true, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)
         if (int4) {
             if (spg == 1) SL_QGEMV_SLICED(4, 1);
             else if (spg == 2) SL_QGEMV_SLICED(4, 2);
@@ -772,7 +814,9 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     }
 #undef SL_QGEMV_FUSED_G
 #undef SL_QGEMV_FUSED
+#undef SL_QGEMV_FUSED_LS
 #undef SL_QGEMV_FUSED_F
+#undef SL_QGEMV_LAUNCH
     if (slices > 1) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -45,8 +45,9 @@ of all B, and the step bytes count the weights once and the KV cache B times.
 copy (Scale by 1 over 64 Mi floats), for the counter runs. --mode micro
 prints one JSON line per microbenchmark: Softmax [32 x 2048 x 2048], Add and
 fused SiLU(gate)*up [4096 x 14336], RoPE [1, 32, 4096, 128], RMSNorm, the
-q-GEMV at M = 1 (both 8B shapes, INT4 and INT8) and M = 8, and the M = 512
-q-GEMM on the fp16 matrix cores.
+q-GEMV at M = 1 (both 8B shapes, INT4 and INT8) and M = 8, the M = 512
+q-GEMM on the fp16 matrix cores, and a dense f32 MatMulNT [4096 x 4096] x
+[4096 x 4096]^T on the f32 matrix cores.
 """
 from __future__ import annotations
 
@@ -64,6 +65,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix cores
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense f32 matrix peak
 PROMPT_LEN = 1024
 MAX_SEQ = 4096
 
@@ -445,6 +447,21 @@ def micro_lines(dev):
                   "achieved": round(tf, 2), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                   "frac": round(tf / FP16_PEAK_TFLOPS, 4), "mfma_flop_per_launch": mfma_flop,
                   "f32_result_tflops": round(flop / (us * 1e-6) / 1e12, 2), "avg_launch_us": round(us, 1)})
+    dev.synchronize()
+
+    # dense f32 MatMulNT [4096 x 4096] x [4096 x 4096]^T on the f32 matrix cores
+    md = 4096
+    fa, fb = dev.upload_new_f32(normal(md * md)), dev.upload_new_f32(normal(md * md))
+    fo = dev.allocate_f32(md * md, 256)
+    fv = Value.f32([md, md])
+    us = submission_us(dev, lambda: [dev.dispatch(Op.matmul_nt(), [BufferRef(fa, 0, md * md),
+                                                                   BufferRef(fb, 0, md * md)], [fv, fv],
+                                                  [BufferRef(fo, 0, md * md)], [fv]) for _ in range(5)]) / 5
+    tf = 2 * md ** 3 / (us * 1e-6) / 1e12
+    lines.append({"kernel": f"sgemm_mfma (MatMulNT f32 [{md}x{md}] x [{md}x{md}]^T)", "bound": "mfma",
+                  "achieved": round(tf, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                  "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "flop_per_launch": 2 * md ** 3,
+                  "avg_launch_us": round(us, 1)})
     dev.synchronize()
     return lines
 

@@ -279,7 +279,12 @@ def test_kv_append_parity(hip):
 @pytest.mark.parametrize("nt", [True, False])
 @pytest.mark.parametrize("a_shape,b_shape", [
     ((1, 1), (1, 1)), ((2, 3, 5), (2, 7, 5)), ((3, 4, 7), (5, 7)), ((1, 4, 9), (3, 6, 9)), ((64, 256), (300, 256)),
-    ((2, 130, 70), (2, 65, 70)), ((2, 0, 4), (3, 4)), ((1, 2, 0), (3, 0))])
+    ((2, 130, 70), (2, 65, 70)), ((2, 0, 4), (3, 4)), ((1, 2, 0), (3, 0)),
+    # k % 4 == 0 and m >= 32: the f32 matrix-core kernel (128x128 tiles,
+    # k staged 16 at a time): ragged m and n, a k tail, batch broadcast, NN
+    # rows of B with n % 4 == 0 (and != 0: the VALU kernel)
+    ((2, 130, 68), (2, 65, 68)), ((1, 257, 132), (3, 132, 132)), ((32, 512), (1000, 512)),
+    ((2, 96, 20), (2, 36, 20)), ((4, 33, 4), (4, 129, 4)), ((256, 1024), (1536, 1024))])
 def test_matmul_parity(hip, nt, a_shape, b_shape):
     r = rng(sum(a_shape) + sum(b_shape))
     if not nt:

@@ -78,12 +78,16 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* global_ptr(T* p)
 constexpr uint32_t kLimbPad = 64;
 constexpr int kMaxF4 = 8;  // float4 of activations per thread, at most
 constexpr int kWindow = 4;  // superblocks in flight per wave
+constexpr int kSmStream = 0, kSmLds = 1, kSmOneRound = 2;  // stream modes (qgemv_fused's SM)
 // activations a block holds: 16384 with 8 waves, 32768 with 16
 constexpr uint32_t max_elems(int w) { return static_cast<uint32_t>(w) * kWave * 4 * kMaxF4; }
 // float4 of scales each thread loads at launch: a block's tiles hold at
 // most this many per thread (more spills registers: pair kernels hold one
-// per group of a superblock, INT8 two, INT4 four)
-constexpr int qgemv_scale_slots(int nt, int gps, int bits) { return nt == 2 ? gps : bits == 4 ? 4 : 2; }
+// per group of a superblock, INT8 two, INT4 four at group 64). Every slot
+// is loaded (unused ones re-read a used float4), and each wave64 load
+// returns 1 KB to registers, so INT4 at one group per superblock keeps one
+// slot: [14336 x 4096] 8.43-8.47 -> 8.31-8.37 us against four.
+constexpr int qgemv_scale_slots(int nt, int gps, int bits) { return nt == 2 ? gps : bits == 4 ? (gps == 1 ? 1 : 4) : 2; }
 // static LDS of the kernel with W waves: red, row_val, cfac, wres
 constexpr size_t static_lds(int w) { return sizeof(float) * (kMaxF4 * w + 16 + max_elems(w) / 256 + 2 * w * 16 * 16); }
 
@@ -128,22 +132,29 @@ struct Item {
 // p.sb_total, and writes its partial sums m n floats after slice y - 1's
 // (the launcher adds the slices up). Every slice geometry follows from the
 // grid, so the arguments are the same as for one slice.
-// LS: the scales of the block's tiles are loaded into LDS at launch (one
-// load per thread or a few, before the code window) instead of with each
-// superblock's codes; that pays where a wave streams more superblocks than
-// its window holds, and costs a dependent load before the prologue's
-// barrier where it does not.
+// SM, how a wave streams its superblocks:
+//  * kSmStream: each superblock's scales load with its codes, and the
+//    window is refilled as it is consumed (past the stream's end with the
+//    last superblock again, so that every wait stays one item deep);
+//  * kSmLds: the scales of the block's tiles are loaded into LDS at launch
+//    (one load per thread or a few, before the code window) instead of with
+//    each superblock's codes; that pays where a wave streams more
+//    superblocks than its window holds, and costs a dependent load before
+//    the prologue's barrier where it does not;
+//  * kSmOneRound: the whole stream fits the first window (no refills; those
+//    would all re-read the last superblock, 1 KB of returns per wave each).
 // The activations a, the RMSNorm weight gamma (null: no norm) and the
 // m x k shape lead the arguments: the library is built to preload leading
 // scalar arguments into scalar registers, so the activation loads go out
 // at once, while the argument block is still being fetched.
-template <int BITS, int NT, int SPG, bool LR, int F4, int W, bool SLICED, bool LS>
+template <int BITS, int NT, int SPG, bool LR, int F4, int W, bool SLICED, int SM>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(
     const float* __restrict__ a_in, const float* __restrict__ gamma, uint32_t m_in, uint32_t k_in, Args p) {
     constexpr int kThreads = W * kWave, kWaves = W;
     static_assert(F4 <= kMaxF4, "activations per thread beyond the block's budget");
     constexpr int GPS = SPG == 1 ? 2 : 1;
     constexpr int PF = kWindow;
+    constexpr bool LS = SM == kSmLds;
     constexpr int WPT = kWaves / NT;  // waves per tile
     constexpr uint32_t SB_BYTES = BITS == 4 ? 1024 : 2048;
     // [3][m][k + kLimbPad] limbs, tres [tile_slots][16][m] results, and
@@ -627,7 +638,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
             const bool live = k < items;
             const uint32_t meta = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(tmeta), min(k, items - 1)));
             if (live) consume(s_c, meta);
-            fetch(win[decltype(s_c)::value], k + PF);
+            if constexpr (SM != kSmOneRound) fetch(win[decltype(s_c)::value], k + PF);
             if (live && (meta & kMetaTileEnd)) tile_end();
         });
     }
@@ -757,6 +768,13 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     // x 4096] 13.62 -> 13.32 us; but [2048 x 8192] (4 superblocks per
     // wave) 5.80 -> 6.34 us, and M = 8 [14336 x 4096] 13.73 -> 14.38 us.
     const bool ls = p.m == 1 && slices == 1 && p.k >= 4096 && f4 <= 4 && per_block * per > kWindow;
+    // A stream that fits the first window (every block's tiles times the
+    // superblocks per wave; the cap below only lowers per_block) is one
+    // round without refills: [2048 x 8192] 5.50 -> 5.20 us, [2048 x 2048]
+    // 3.77 -> 3.60 us. Dropping the refills of a longer stream's last round
+    // instead makes the compiler's waits cover more than one item:
+    // [14336 x 4096] 8.45 -> 8.69 us.
+    const bool one_round = !ls && lr && slices == 1 && f4 <= 4 && per_block * per <= kWindow;
     // the per-lane item table holds at most 64 items per wave, and with LS
     // the tiles' scales at most qgemv_scale_slots float4 per thread
     const uint32_t gps = p.group == 64 ? 2 : 1, nt = pair ? 2 : 1;
@@ -780,21 +798,23 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
 #define SL_QGEMV_LAUNCH(B, T, G, L, F, W, S) \
     qgemv_fused<B, T, G, L, F, W, false, S><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)
 #define SL_QGEMV_FUSED_F(B, T, G, L)                                                                               \
-    (waves == 16 ? (f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, L, 2, 16, false)                                             \
-                            : f4 <= 4 ? SL_QGEMV_LAUNCH(B, T, G, L, 4, 16, false) : SL_QGEMV_LAUNCH(B, T, G, L, 8, 16, false)) \
-                 : f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, L, 2, 8, false)                                               \
-                           : f4 <= 4 ? SL_QGEMV_LAUNCH(B, T, G, L, 4, 8, false) : SL_QGEMV_LAUNCH(B, T, G, L, 8, 8, false))
-#define SL_QGEMV_FUSED_LS(B, T, G)                                                                                 \
-    (waves == 16 ? (f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, true, 2, 16, true) : SL_QGEMV_LAUNCH(B, T, G, true, 4, 16, true)) \
-                 : f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, true, 2, 8, true) : SL_QGEMV_LAUNCH(B, T, G, true, 4, 8, true))
+    (waves == 16 ? (f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, L, 2, 16, kSmStream)                                             \
+                            : f4 <= 4 ? SL_QGEMV_LAUNCH(B, T, G, L, 4, 16, kSmStream) : SL_QGEMV_LAUNCH(B, T, G, L, 8, 16, kSmStream)) \
+                 : f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, L, 2, 8, kSmStream)                                               \
+                           : f4 <= 4 ? SL_QGEMV_LAUNCH(B, T, G, L, 4, 8, kSmStream) : SL_QGEMV_LAUNCH(B, T, G, L, 8, 8, kSmStream))
+#define SL_QGEMV_FUSED_SM(B, T, G, S)                                                                               \
+    (waves == 16 ? (f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, true, 2, 16, S) : SL_QGEMV_LAUNCH(B, T, G, true, 4, 16, S)) \
+                 : f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, true, 2, 8, S) : SL_QGEMV_LAUNCH(B, T, G, true, 4, 8, S))
 #define SL_QGEMV_FUSED(B, T, G) \
-    (ls ? SL_QGEMV_FUSED_LS(B, T, G) : lr ? SL_QGEMV_FUSED_F(B, T, G, true) : SL_QGEMV_FUSED_F(B, T, G, false))
+    (ls ? SL_QGEMV_FUSED_SM(B, T, G, kSmLds)                                          \
+        : one_round ? SL_QGEMV_FUSED_SM(B, T, G, kSmOneRound)                         \
+                    : lr ? SL_QGEMV_FUSED_F(B, T, G, true) : SL_QGEMV_FUSED_F(B, T, G, false))
 #define SL_QGEMV_FUSED_G(B, T) \
     (spg == 1 ? SL_QGEMV_FUSED(B, T, 1) : spg == 2 ? SL_QGEMV_FUSED(B, T, 2) : SL_QGEMV_FUSED(B, T, 0))
     if (slices > 1) {
         // k slices: many rows (not LR), 16 waves, 8 float4 per thread
         if (waves != 16 || f4 > 8 || lr) return hipErrorNotSupported;
-#define SL_QGEMV_SLICED(B, G) qgemv_fused<B, 1, G, false, 8, 16, true, false><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)
+#define SL_QGEMV_SLICED(B, G) qgemv_fused<B, 1, G, false, 8, 16, true, kSmStream><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)
         if (int4) {
             if (spg == 1) SL_QGEMV_SLICED(4, 1);
             else if (spg == 2) SL_QGEMV_SLICED(4, 2);
@@ -814,7 +834,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     }
 #undef SL_QGEMV_FUSED_G
 #undef SL_QGEMV_FUSED
-#undef SL_QGEMV_FUSED_LS
+#undef SL_QGEMV_FUSED_SM
 #undef SL_QGEMV_FUSED_F
 #undef SL_QGEMV_LAUNCH
     if (slices > 1) {

@@ -248,9 +248,15 @@ __global__ __launch_bounds__(256) void rope_sincos(const uint32_t* __restrict__ 
     table[t * D + half + pair] = static_cast<float>(cos(angle));
 }
 
+// The leading arguments (preloaded into scalar registers with the wave)
+// are what the first loads need: past_len's source (dyn, seq_past for the
+// paged form, or null for past_fixed), the query rows and their geometry
+// (seq, group, heads). The past_len and query loads go out at once, and the
+// argument block is fetched meanwhile.
 template <int DV, int RT, bool FUSED, bool PAGED>
-__global__ __launch_bounds__(256) void attn_decode(Geo g) {
-    prefetch_kernarg<arg_bytes<Geo>()>();
+__global__ __launch_bounds__(256) void attn_decode(const uint32_t* past_src, uint32_t past_fixed,
+                                                   const float* q_in, uint32_t seq, uint32_t group, uint32_t heads,
+                                                   Geo g) {
     constexpr int D4 = 16 * DV;  // float4 per row
     extern __shared__ float sc[];  // FUSED: rope table [S][D]
     __shared__ float4 qs[RT * D4];
@@ -260,13 +266,27 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     constexpr int NS = RT * DV <= 8 ? 16 : 4;
     __shared__ float4 wacc[NS][RT][D4];
     __shared__ float wml[NS][RT][2];
-    const uint32_t S = g.seq, G = g.group, R = G * S;
+    const uint32_t S = seq, G = group, R = G * S;
     const uint32_t P = gridDim.x, p = blockIdx.x, kvh = blockIdx.y;
     const uint64_t b = blockIdx.z;
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const int grp = lane / kDecodeLanes, li = lane % kDecodeLanes;
-    const uint32_t past = PAGED ? g.seq_past[b] : past_of(g), keys = past + S;
+    const uint32_t past = past_src != nullptr ? past_src[PAGED ? b : 0] : past_fixed, keys = past + S;
     const uint32_t ntiles = (keys + kDecodeTile - 1) / kDecodeTile;
+    // query rows: loaded first (rows past R re-read row 0 and are zeroed),
+    // staged in LDS after the first tile's loads have gone out
+    constexpr int QPT = (RT * D4 + 255) / 256;
+    float4 qv[QPT];
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+        const uint32_t i = min(static_cast<uint32_t>(tid + 256 * u), static_cast<uint32_t>(RT * D4 - 1));
+        const uint32_t r = min(i / D4, R - 1), c = i % D4, gi = r / S, t = r % S;
+        const uint64_t h = kvh * G + gi;
+        const uint64_t row = FUSED ? (b * S + t) * heads + h : (b * heads + h) * S + t;
+        qv[u] = reinterpret_cast<const float4*>(q_in + row * (4 * D4))[c];
+    }
+    // the rest of the arguments, in one batch of loads
+    prefetch_kernarg<arg_bytes<const uint32_t*, uint32_t, const float*, uint32_t, uint32_t, uint32_t, Geo>()>();
 
     const uint64_t time_stride = static_cast<uint64_t>(g.kv_heads) * (4 * D4);
     float* kbase = g.wcache + (PAGED ? 0 : b * g.batch_stride) + g.layer_offset + kvh * (4 * D4);
@@ -309,18 +329,6 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     };
     // The first tile's loads go out before the query rows are staged, and
     // each iteration starts the next tile's loads before computing.
-    // query rows: loaded first (rows past R re-read row 0 and are zeroed),
-    // staged in LDS after the first tile's loads have gone out
-    constexpr int QPT = (RT * D4 + 255) / 256;
-    float4 qv[QPT];
-#pragma unroll
-    for (int u = 0; u < QPT; ++u) {
-        const uint32_t i = min(static_cast<uint32_t>(tid + 256 * u), static_cast<uint32_t>(RT * D4 - 1));
-        const uint32_t r = min(i / D4, R - 1), c = i % D4, gi = r / S, t = r % S;
-        const uint64_t h = kvh * G + gi;
-        const uint64_t row = FUSED ? (b * S + t) * g.heads + h : (b * g.heads + h) * S + t;
-        qv[u] = reinterpret_cast<const float4*>(g.q + row * (4 * D4))[c];
-    }
     // FUSED: the first entries of the Rope table, loaded with the query rows
     // and ahead of the K/V tile, whose bytes they would otherwise wait behind
     // (every thread loads: without a table, from the query rows)
@@ -328,7 +336,7 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
     float tabv[kTabRegs];
     if constexpr (FUSED) {
         const uint32_t SD = S * 4 * D4;
-        const float* tab = g.rope_tab != nullptr ? g.rope_tab + b * SD : g.q;
+        const float* tab = g.rope_tab != nullptr ? g.rope_tab + b * SD : q_in;
 #pragma unroll
         for (int u = 0; u < kTabRegs; ++u) tabv[u] = tab[min(static_cast<uint32_t>(tid + 256 * u), SD - 1)];
     }
@@ -641,16 +649,19 @@ __global__ __launch_bounds__(256) void attn_decode(Geo g) {
 // in thread order.
 constexpr int kMergeMaxParts = 64;
 
-__global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
-    prefetch_kernarg<arg_bytes<Geo, uint32_t>()>();
+// The leading (preloaded) arguments locate the partials: the workspace,
+// P partials per row, head_dim, R = group * seq rows per KV head, and the
+// KV heads; the loads go out while the argument block is fetched.
+__global__ __launch_bounds__(256) void attn_decode_merge(const float* ws, uint32_t P, uint32_t head_dim, uint32_t R,
+                                                         uint32_t kv_heads, Geo g) {
     __shared__ float coef[kMergeMaxParts];
     __shared__ float4 red[256];
-    const uint32_t D4 = g.head_dim / 4, S = g.seq, G = g.group, R = G * S;
+    const uint32_t D4 = head_dim / 4;
     const uint32_t kvh = blockIdx.x / R, r = blockIdx.x % R;
     const uint64_t b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid % kWave;
     const uint64_t row_stride = kDecodePartStride + 4 * D4;
-    const float* base = g.ws + (b * g.kv_heads + kvh) * P * R * row_stride;
+    const float* base = ws + (b * kv_heads + kvh) * P * R * row_stride;
     const uint32_t T = 256 / D4;  // threads per slot: 4 .. 16
     const uint32_t c = tid % D4, q = tid / D4;  // q >= T (head_dim 192): idle
     const bool mine = q < T;
@@ -672,6 +683,8 @@ __global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
         const float total = wave_sum(lp * e);
         if (on) coef[lane] = e / total;
     }
+    // the rest of the arguments (the outputs), in one batch of loads
+    prefetch_kernarg<arg_bytes<const float*, uint32_t, uint32_t, uint32_t, uint32_t, Geo>()>();
     __syncthreads();
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -689,8 +702,8 @@ __global__ __launch_bounds__(256) void attn_decode_merge(Geo g, uint32_t P) {
         a.z += x.z;
         a.w += x.w;
     }
-    const uint32_t gi = r / S, t = r % S;
-    const uint64_t h = kvh * G + gi;
+    const uint32_t S = g.seq, gi = r / S, t = r % S;
+    const uint64_t h = kvh * g.group + gi;
     if (g.out != nullptr) reinterpret_cast<float4*>(g.out + ((b * g.heads + h) * S + t) * (4 * D4))[c] = a;
     // MergeHeads layout [B, S, H * D] (reference/layout.rs merge_heads)
     const uint64_t mrow = (b * S + t) * g.heads + h;
@@ -1041,11 +1054,13 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
     g.chunk = kDecodeTile;
     const dim3 grid(static_cast<unsigned>(parts), g.kv_heads, static_cast<unsigned>(a.batch));
     const size_t lds = fused ? a.seq * a.head_dim * sizeof(float) : 0;
-#define SL_DECODE(DVv, RTv)                                                             \
-    (fused ? (paged ? attn_decode<DVv, RTv, true, true><<<grid, 256, lds, s>>>(g)       \
-                    : attn_decode<DVv, RTv, true, false><<<grid, 256, lds, s>>>(g))     \
-     : paged ? attn_decode<DVv, RTv, false, true><<<grid, 256, lds, s>>>(g)             \
-             : attn_decode<DVv, RTv, false, false><<<grid, 256, lds, s>>>(g))
+    const uint32_t* past_src = paged ? g.seq_past : g.dyn;
+#define SL_DECODE_ARGS past_src, g.past_len, g.q, g.seq, g.group, g.heads, g
+#define SL_DECODE(DVv, RTv)                                                                        \
+    (fused ? (paged ? attn_decode<DVv, RTv, true, true><<<grid, 256, lds, s>>>(SL_DECODE_ARGS)     \
+                    : attn_decode<DVv, RTv, true, false><<<grid, 256, lds, s>>>(SL_DECODE_ARGS))   \
+     : paged ? attn_decode<DVv, RTv, false, true><<<grid, 256, lds, s>>>(SL_DECODE_ARGS)           \
+             : attn_decode<DVv, RTv, false, false><<<grid, 256, lds, s>>>(SL_DECODE_ARGS))
     switch (dv * 100 + rt) {
         case 104: SL_DECODE(1, 4); break;
         case 108: SL_DECODE(1, 8); break;
@@ -1059,8 +1074,9 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
         default: SL_DECODE(4, 8); break;
     }
 #undef SL_DECODE
+#undef SL_DECODE_ARGS
     attn_decode_merge<<<dim3(g.kv_heads * static_cast<unsigned>(rows), static_cast<unsigned>(a.batch)), 256, 0, s>>>(
-        g, static_cast<uint32_t>(parts));
+        g.ws, static_cast<uint32_t>(parts), g.head_dim, static_cast<uint32_t>(rows), g.kv_heads, g);
     return hipGetLastError();
 }
 

@@ -737,8 +737,14 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 constexpr int kPfQ = 64;  // queries per block
 constexpr int kPfK = 32;  // keys per tile
 
+// Two waves per SIMD: at head_dim 128 the next tile's rows (kn / vn) then
+// fit in registers (132 VGPRs). Held to four waves per SIMD (128 VGPRs, two
+// blocks per CU by LDS), the compiler kept them in scratch memory instead,
+// storing each row as soon as it arrived, so the loads never overlapped a
+// tile's products: 153.3 -> 129.7 us per 8B layer at 1024 tokens.
 template <int D, int KH>
-__global__ __launch_bounds__(256 * KH) void attn_prefill(Geo g, uint32_t qtiles) {
+__global__ __launch_bounds__(256 * KH) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill(Geo g,
+                                                                                                  uint32_t qtiles) {
     prefetch_kernarg<arg_bytes<Geo, uint32_t>()>();
     constexpr int NT = 256 * KH;             // threads
     constexpr int LS = D + 4;                // LDS row stride (floats)
@@ -805,7 +811,9 @@ __global__ __launch_bounds__(256 * KH) void attn_prefill(Geo g, uint32_t qtiles)
             *reinterpret_cast<float4*>(vs + row * LS + 4 * col) = vn[u];
         }
         __syncthreads();
-        if (kt + kPfK < block_keys) load(kt + kPfK);
+        // the next tile's rows (past the block's keys they re-read its last
+        // key), waiting in registers while this tile is computed
+        load(kt + kPfK);
         // wave-uniform: no key of the wave's part of the tile is visible to it
         if (kt + 16 * half >= wave_keys) continue;
         // S^T: keys 16 sub + 4 kk + i of the tile, query c

@@ -737,11 +737,19 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 constexpr int kPfQ = 64;  // queries per block
 constexpr int kPfK = 32;  // keys per tile
 
-// Two waves per SIMD: at head_dim 128 the next tile's rows (kn / vn) then
-// fit in registers (132 VGPRs). Held to four waves per SIMD (128 VGPRs, two
-// blocks per CU by LDS), the compiler kept them in scratch memory instead,
-// storing each row as soon as it arrived, so the loads never overlapped a
-// tile's products: 153.3 -> 129.7 us per 8B layer at 1024 tokens.
+// The next tile's K/V rows wait in registers while a tile is computed; they
+// travel by value (PfRows). Filled through references into arrays, they were
+// kept in scratch memory (at 128 registers per lane) or in LDS slots (at
+// more), stored as soon as each load returned, so the loads never
+// overlapped a tile's products. 8B layer at 1024 tokens, attn_prefill<128,
+// 2>: 154.3 us in scratch, 129.1 in LDS slots, 106.0 in registers at two
+// waves per SIMD (144 registers, one block per CU), 108.9 at four (128
+// registers, two blocks per CU).
+template <int N>
+struct PfRows {
+    float4 k[N], v[N];
+};
+
 template <int D, int KH>
 __global__ __launch_bounds__(256 * KH) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill(Geo g,
                                                                                                   uint32_t qtiles) {
@@ -790,30 +798,32 @@ __global__ __launch_bounds__(256 * KH) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint64_t time_stride = static_cast<uint64_t>(g.kv_heads) * D;
     const float* kbase = g.cache + b * g.batch_stride + g.layer_offset + kvh * D;
     const float* vbase = kbase + g.parity_stride;
-    float4 kn[F4], vn[F4];
-    // rows past the block's keys re-read its last key (their scores are masked)
-    auto load = [&](uint32_t kt) {
+    // rows past the block's keys re-read its last key (their scores are
+    // masked); the rows travel by value (an array the lambda filled through a
+    // reference would be kept in memory, stored as soon as it arrived)
+    auto load = [&](uint32_t kt) -> PfRows<F4> {
+        PfRows<F4> n;
 #pragma unroll
         for (int u = 0; u < F4; ++u) {
             const uint32_t e = tid + NT * u, row = e / (D / 4), col = e % (D / 4);
             const uint64_t j = min(kt + row, block_keys - 1);
-            kn[u] = reinterpret_cast<const float4*>(kbase + j * time_stride)[col];
-            vn[u] = reinterpret_cast<const float4*>(vbase + j * time_stride)[col];
+            n.k[u] = reinterpret_cast<const float4*>(kbase + j * time_stride)[col];
+            n.v[u] = reinterpret_cast<const float4*>(vbase + j * time_stride)[col];
         }
+        return n;
     };
-    load(0);
+    PfRows<F4> nx = load(0);
     for (uint32_t kt = 0; kt < block_keys; kt += kPfK) {
         __syncthreads();  // every wave is done reading the previous tile
 #pragma unroll
         for (int u = 0; u < F4; ++u) {
             const uint32_t e = tid + NT * u, row = e / (D / 4), col = e % (D / 4);
-            *reinterpret_cast<float4*>(ks + row * LS + 4 * col) = kn[u];
-            *reinterpret_cast<float4*>(vs + row * LS + 4 * col) = vn[u];
+            *reinterpret_cast<float4*>(ks + row * LS + 4 * col) = nx.k[u];
+            *reinterpret_cast<float4*>(vs + row * LS + 4 * col) = nx.v[u];
         }
         __syncthreads();
-        // the next tile's rows (past the block's keys they re-read its last
-        // key), waiting in registers while this tile is computed
-        load(kt + kPfK);
+        // the next tile's rows, waiting in registers while this tile is computed
+        nx = load(kt + kPfK);
         // wave-uniform: no key of the wave's part of the tile is visible to it
         if (kt + 16 * half >= wave_keys) continue;
         // S^T: keys 16 sub + 4 kk + i of the tile, query c

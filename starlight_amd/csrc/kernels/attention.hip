@@ -181,8 +181,8 @@ __global__ __launch_bounds__(256) void attn_merge(Geo g) {
 // acc). Rows j >= past_len come from k_new / v_new and the lane group that
 // reads one also appends it to the cache.
 constexpr int kDecodeLanes = 16;                       // lanes per key
-constexpr int kDecodeKeys = 4;                         // keys per lane group per tile
-constexpr int kDecodeTile = kDecodeKeys * kWave / kDecodeLanes;  // 16 keys per wave tile
+constexpr int kDecodeKeys = 4;                         // keys per lane group per tile, at most
+constexpr int kDecodeTile = kDecodeKeys * kWave / kDecodeLanes;  // 16 keys per wave tile, at most
 constexpr int kDecodeMaxRows = 16;
 constexpr uint32_t kDecodePartStride = 4;              // floats before acc in a partial row
 
@@ -248,16 +248,22 @@ __global__ __launch_bounds__(256) void rope_sincos(const uint32_t* __restrict__ 
     table[t * D + half + pair] = static_cast<float>(cos(angle));
 }
 
-// The leading arguments (preloaded into scalar registers with the wave)
+// KEYS: keys per lane group per tile (a wave tile is 4 KEYS keys). Each
+// wave streams whole tiles, so a wave holding one tile more than the others
+// sets the launch's length: where the grid has few waves per key range
+// (batch > 1, partials capped by the grid size) 8-key tiles even that out,
+// and where every wave holds one tile or none (batch 1) 16-key tiles are
+// cheaper. The leading arguments (preloaded into scalar registers with the wave)
 // are what the first loads need: past_len's source (dyn, seq_past for the
 // paged form, or null for past_fixed), the query rows and their geometry
 // (seq, group, heads). The past_len and query loads go out at once, and the
 // argument block is fetched meanwhile.
-template <int DV, int RT, bool FUSED, bool PAGED>
+template <int DV, int RT, bool FUSED, bool PAGED, int KEYS>
 __global__ __launch_bounds__(256) void attn_decode(const uint32_t* past_src, uint32_t past_fixed,
                                                    const float* q_in, uint32_t seq, uint32_t group, uint32_t heads,
                                                    Geo g) {
     constexpr int D4 = 16 * DV;  // float4 per row
+    constexpr int kTileKeys = KEYS * kWave / kDecodeLanes;  // keys per wave tile
     extern __shared__ float sc[];  // FUSED: rope table [S][D]
     __shared__ float4 qs[RT * D4];
     // Softmax states combined through LDS at the end: with small per-lane
@@ -272,7 +278,7 @@ __global__ __launch_bounds__(256) void attn_decode(const uint32_t* past_src, uin
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const int grp = lane / kDecodeLanes, li = lane % kDecodeLanes;
     const uint32_t past = past_src != nullptr ? past_src[PAGED ? b : 0] : past_fixed, keys = past + S;
-    const uint32_t ntiles = (keys + kDecodeTile - 1) / kDecodeTile;
+    const uint32_t ntiles = (keys + kTileKeys - 1) / kTileKeys;
     // query rows: loaded first (rows past R re-read row 0 and are zeroed),
     // staged in LDS after the first tile's loads have gone out
     constexpr int QPT = (RT * D4 + 255) / 256;
@@ -302,10 +308,10 @@ __global__ __launch_bounds__(256) void attn_decode(const uint32_t* past_src, uin
     };
     // K/V rows of a tile for this lane: cached rows from the cache, new rows
     // from k_new / v_new, zeros past the end.
-    auto load_tile = [&](uint32_t tile, float4 (&kx)[kDecodeKeys][DV], float4 (&vx)[kDecodeKeys][DV]) {
-        const uint32_t j0 = tile * kDecodeTile + grp * kDecodeKeys;
+    auto load_tile = [&](uint32_t tile, float4 (&kx)[KEYS][DV], float4 (&vx)[KEYS][DV]) {
+        const uint32_t j0 = tile * kTileKeys + grp * KEYS;
 #pragma unroll
-        for (int kb = 0; kb < kDecodeKeys; ++kb) {
+        for (int kb = 0; kb < KEYS; ++kb) {
             // Every lane loads (keys past the end re-read the last row; their
             // scores are masked to -inf, so they weigh exactly 0), so the
             // loads carry no branch and the waits before their use are exact.
@@ -341,7 +347,7 @@ __global__ __launch_bounds__(256) void attn_decode(const uint32_t* past_src, uin
         for (int u = 0; u < kTabRegs; ++u) tabv[u] = tab[min(static_cast<uint32_t>(tid + 256 * u), SD - 1)];
     }
     uint32_t tile = p + P * wave;
-    float4 kv[kDecodeKeys][DV], vv[kDecodeKeys][DV];
+    float4 kv[KEYS][DV], vv[KEYS][DV];
     // Every wave loads a first tile, unconditionally (a wave without one
     // re-reads the last key row, which its neighbours load too): loads
     // under a branch leave register copies at the join that wait for the
@@ -415,15 +421,15 @@ __global__ __launch_bounds__(256) void attn_decode(const uint32_t* past_src, uin
     }
 
     for (; tile < ntiles; tile += 4 * P) {
-        const uint32_t j0 = tile * kDecodeTile + grp * kDecodeKeys;
-        float4 kn[kDecodeKeys][DV], vn[kDecodeKeys][DV];
+        const uint32_t j0 = tile * kTileKeys + grp * KEYS;
+        float4 kn[KEYS][DV], vn[KEYS][DV];
         // the next tile's loads only when there is one: loads still in flight
         // at the loop's end would hold the combine below (their registers are
         // reused), and most decode waves have a single tile
         const bool more = tile + 4 * P < ntiles;
         if (more) load_tile(tile + 4 * P, kn, vn);
 #pragma unroll
-        for (int kb = 0; kb < kDecodeKeys; ++kb) {
+        for (int kb = 0; kb < KEYS; ++kb) {
             const uint32_t j = j0 + kb;
             if (j >= past && j < keys) {
                 // the new row in SplitHeads / Rope layout [B, Hkv, S, D]
@@ -498,10 +504,10 @@ __global__ __launch_bounds__(256) void attn_decode(const uint32_t* past_src, uin
 #pragma unroll
             for (int u = 0; u < DV; ++u) qv[u] = qs[r * D4 + li + 16 * u];
             const uint32_t limit = past + r % S;  // last visible key of this row
-            float s[kDecodeKeys];
+            float s[KEYS];
             float tmax = -INFINITY;
 #pragma unroll
-            for (int kb = 0; kb < kDecodeKeys; ++kb) {
+            for (int kb = 0; kb < KEYS; ++kb) {
                 float dot = 0.f;
 #pragma unroll
                 for (int u = 0; u < DV; ++u) {
@@ -521,7 +527,7 @@ __global__ __launch_bounds__(256) void attn_decode(const uint32_t* past_src, uin
 #pragma unroll
             for (int u = 0; u < DV; ++u) acc[r][u] = f4_scale(acc[r][u], corr);
 #pragma unroll
-            for (int kb = 0; kb < kDecodeKeys; ++kb) {
+            for (int kb = 0; kb < KEYS; ++kb) {
                 const float pk = s[kb] == -INFINITY ? 0.f : expf(s[kb] - mn);
                 lsum += pk;
 #pragma unroll
@@ -532,7 +538,7 @@ __global__ __launch_bounds__(256) void attn_decode(const uint32_t* past_src, uin
         }
         if (more) {
 #pragma unroll
-            for (int kb = 0; kb < kDecodeKeys; ++kb) {
+            for (int kb = 0; kb < KEYS; ++kb) {
 #pragma unroll
                 for (int u = 0; u < DV; ++u) {
                     kv[kb][u] = kn[kb][u];
@@ -1074,11 +1080,17 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
     const size_t lds = fused ? a.seq * a.head_dim * sizeof(float) : 0;
     const uint32_t* past_src = paged ? g.seq_past : g.dyn;
 #define SL_DECODE_ARGS past_src, g.past_len, g.q, g.seq, g.group, g.heads, g
-#define SL_DECODE(DVv, RTv)                                                                        \
-    (fused ? (paged ? attn_decode<DVv, RTv, true, true><<<grid, 256, lds, s>>>(SL_DECODE_ARGS)     \
-                    : attn_decode<DVv, RTv, true, false><<<grid, 256, lds, s>>>(SL_DECODE_ARGS))   \
-     : paged ? attn_decode<DVv, RTv, false, true><<<grid, 256, lds, s>>>(SL_DECODE_ARGS)           \
-             : attn_decode<DVv, RTv, false, false><<<grid, 256, lds, s>>>(SL_DECODE_ARGS))
+#define SL_DECODE_K(DVv, RTv, K)                                                                      \
+    (fused ? (paged ? attn_decode<DVv, RTv, true, true, K><<<grid, 256, lds, s>>>(SL_DECODE_ARGS)     \
+                    : attn_decode<DVv, RTv, true, false, K><<<grid, 256, lds, s>>>(SL_DECODE_ARGS))   \
+     : paged ? attn_decode<DVv, RTv, false, true, K><<<grid, 256, lds, s>>>(SL_DECODE_ARGS)           \
+             : attn_decode<DVv, RTv, false, false, K><<<grid, 256, lds, s>>>(SL_DECODE_ARGS))
+    // 8-key tiles where the partials were capped by the grid size (batch 8,
+    // 8B: 2,617-2,624 -> 2,689-2,690 tok/s; at batch 1 they cost 642-644 ->
+    // 629-634 tok/s), for head_dim 64 and 128
+    const bool short_tiles = parts < (a.max_seq + 127) / 128 && dv <= 2;
+#define SL_DECODE(DVv, RTv) (short_tiles ? SL_DECODE_K(DVv, RTv, 2) : SL_DECODE_K(DVv, RTv, 4))
+#define SL_DECODE_LONG(DVv, RTv) SL_DECODE_K(DVv, RTv, 4)
     switch (dv * 100 + rt) {
         case 104: SL_DECODE(1, 4); break;
         case 108: SL_DECODE(1, 8); break;
@@ -1086,12 +1098,14 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
         case 204: SL_DECODE(2, 4); break;
         case 208: SL_DECODE(2, 8); break;
         case 216: SL_DECODE(2, 16); break;
-        case 304: SL_DECODE(3, 4); break;
-        case 308: SL_DECODE(3, 8); break;
-        case 404: SL_DECODE(4, 4); break;
-        default: SL_DECODE(4, 8); break;
+        case 304: SL_DECODE_LONG(3, 4); break;
+        case 308: SL_DECODE_LONG(3, 8); break;
+        case 404: SL_DECODE_LONG(4, 4); break;
+        default: SL_DECODE_LONG(4, 8); break;
     }
 #undef SL_DECODE
+#undef SL_DECODE_LONG
+#undef SL_DECODE_K
 #undef SL_DECODE_ARGS
     attn_decode_merge<<<dim3(g.kv_heads * static_cast<unsigned>(rows), static_cast<unsigned>(a.batch)), 256, 0, s>>>(
         g.ws, static_cast<uint32_t>(parts), g.head_dim, static_cast<uint32_t>(rows), g.kv_heads, g);

@@ -109,7 +109,22 @@ struct Args {
     uint32_t tiles_total;  // block tiles (pair mode: gate tiles)
     uint32_t epilogue;
     uint32_t tile_slots;   // tiles one block holds at most (LDS areas are sized for it)
+    // Divisions by per-launch values, worked out by the launcher (a division
+    // by a run-time value is about 15 instructions, and the prologue runs
+    // at four waves per SIMD, so its instruction count is its length):
+    // block b holds tiles_base + (b < tiles_rem) tiles; i / len = (i *
+    // len_magic) >> 16 for i < 64; e / m = (e * m_magic) >> 16 for e < 4096;
+    // f / run4 = mulhi(f, run4_magic) (run4 >= 8). Each exact over its range
+    // (magic16(d) = ceil(2^16 / d), run4_magic = ceil(2^32 / run4)).
+    uint32_t tiles_base, tiles_rem, len_magic, m_magic, run4_magic;
 };
+
+// ceil(2^16 / d): (n * magic16(d)) >> 16 == n / d for n < 2^16 / (d * ...)
+// within the ranges the kernel uses (checked exhaustively: n < 64 for d <=
+// 64, n < 128 for d <= 128, n < 4096 for d <= 16)
+constexpr uint32_t magic16(uint32_t d) { return (65536u + d - 1) / d; }
+// float4 of scales per tile and segment (sb_total superblocks, gps groups each)
+constexpr uint32_t run4_of(uint32_t sb_total, uint32_t gps) { return sb_total * 16 * gps / 4; }
 
 
 // One weight superblock of a wave's stream: its codes, 16 bytes per lane
@@ -146,10 +161,11 @@ struct Item {
 // The activations a, the RMSNorm weight gamma (null: no norm) and the
 // m x k shape lead the arguments: the library is built to preload leading
 // scalar arguments into scalar registers, so the activation loads go out
-// at once, while the argument block is still being fetched.
+// at once, while the argument block is still being fetched. mk packs m
+// (bits 0-4) and magic16(k / 256) (from bit 5), which finds a run's row.
 template <int BITS, int NT, int SPG, bool LR, int F4, int W, bool SLICED, int SM>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) void qgemv_fused(
-    const float* __restrict__ a_in, const float* __restrict__ gamma, uint32_t m_in, uint32_t k_in, Args p) {
+    const float* __restrict__ a_in, const float* __restrict__ gamma, uint32_t mk, uint32_t k_in, Args p) {
     constexpr int kThreads = W * kWave, kWaves = W;
     static_assert(F4 <= kMaxF4, "activations per thread beyond the block's budget");
     constexpr int GPS = SPG == 1 ? 2 : 1;
@@ -167,7 +183,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
 
     const int tid = threadIdx.x, lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform, kept in scalar registers
-    const uint32_t M = m_in, K = k_in, K4 = K / 4;
+    const uint32_t M = mk & 31u, K = k_in, K4 = K / 4;
     const uint32_t ks = SLICED ? blockIdx.y : 0u;  // k slice
     const float* const a_slice = SLICED ? a_in + static_cast<uint64_t>(ks) * K : a_in;
     const uint32_t a_stride4 = SLICED ? gridDim.y * K4 : K4;
@@ -180,14 +196,15 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     // of [m][k/4] ----
     const uint32_t total4 = M * K4;
     // k % 256 == 0 keeps a wave's 64 float4 inside one row: run (u, wave)
-    // starts at float4 fb = wave * 64 + u * kThreads, row ru[u] = fb / k4,
+    // starts at float4 fb = wave * 64 + u * kThreads, row ru[u] = fb / k4
+    // (both multiples of 64: (fb / 64) / (k / 256), fb / 64 < 128),
     // column cb[u] = fb % k4, all wave-uniform (a wave past the end takes
     // the last run), so no lane divides.
     uint32_t ru[F4], cb[F4];
 #pragma unroll
     for (int u = 0; u < F4; ++u) {
         const uint32_t fb = min(static_cast<uint32_t>(wave * kWave + kThreads * u), total4 - kWave);
-        ru[u] = __builtin_amdgcn_readfirstlane(fb / K4);
+        ru[u] = __builtin_amdgcn_readfirstlane(((fb >> 6) * (mk >> 5)) >> 16);
         cb[u] = fb - ru[u] * K4;
     }
     float4 v[F4], gv[F4];
@@ -212,8 +229,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     const int slot = wave / WPT, wi = wave % WPT;
     const uint32_t len = p.sb_per_wave;
     const uint32_t sbA = wi * len;
-    const uint32_t my_tiles =
-        p.tiles_total > blockIdx.x ? (p.tiles_total - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    // tiles blockIdx.x + j * gridDim.x: tiles_total / gridDim.x each, one
+    // more for the first tiles_total % gridDim.x blocks
+    const uint32_t my_tiles = p.tiles_base + (blockIdx.x < p.tiles_rem ? 1u : 0u);
     const uint32_t items = my_tiles * len;
     constexpr uint32_t gps = GPS;  // groups per superblock: 2 for group 64, else 1
 
@@ -276,7 +294,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
 #pragma unroll
         for (uint32_t x = 0; x < kFusedMaxSegs; ++x) s_tiles[x] = uniform_ptr(p.seg[x].tiles);
         const uint32_t i = min(static_cast<uint32_t>(lane), items - 1);
-        const uint32_t j = i / len, q = i % len;
+        const uint32_t j = (i * p.len_magic) >> 16, q = i - j * len;
         uint32_t tile;
         const uint32_t si = seg_of(blockIdx.x + j * gridDim.x, tile);
         const uint64_t ts = tile_sb(tile) + sb0 + (q < nlive ? q : (nlive ? nlive - 1 : 0));
@@ -302,11 +320,8 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     const uint32_t sc4_total = my_tiles * NT * run4;
     float4 scv[SC > 0 ? SC : 1];
     if constexpr (LS) {
-        // float4 f of the block's runs is float4 o of run r = f / run4: the
-        // quotient from a float reciprocal is within one of the true one
-        // (f < 2^16), and one correction each way makes it exact
+        // float4 f of the block's runs is float4 o of run r = f / run4
         const uint32_t last = sc4_total ? sc4_total - 1 : 0;  // the launch gives every block a tile
-        const float inv = __builtin_amdgcn_rcpf(static_cast<float>(run4));
         // first tiles of segments 1 and 2 (past the end when absent), as
         // scalars: a per-lane p.seg[si] would copy the argument block to
         // scratch memory to index it
@@ -315,8 +330,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         static_for<SC>([&](auto u_c) {
             constexpr int u = decltype(u_c)::value;
             const uint32_t f = min(static_cast<uint32_t>(tid + kThreads * u), last);
-            uint32_t r = static_cast<uint32_t>(static_cast<float>(f) * inv);
-            r = r * run4 > f ? r - 1 : (r + 1) * run4 <= f ? r + 1 : r;
+            const uint32_t r = __umulhi(f, p.run4_magic);
             const uint32_t o = f - r * run4;
             uint32_t tile = blockIdx.x + (r / NT) * gridDim.x;
             uint32_t si = r % NT;
@@ -357,7 +371,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     // Output element e of the block's [tiles][16][m] results: its segment
     // and offset, false past the segment's rows.
     auto out_at = [&](uint32_t e, uint32_t& si, uint64_t& o) -> bool {
-        const uint32_t j = e / (16 * M), col = (e / M) % 16, m = e % M;
+        const uint32_t q = (e * p.m_magic) >> 16, j = q / 16, col = q % 16, m = e - q * M;
         uint32_t tile = blockIdx.x + j * gridDim.x;
         si = 0;
         if (NT == 1) si = seg_of(tile, tile);
@@ -789,6 +803,12 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     if (per_block > cap) per_block = cap;
     if (blocks == 0 || per_block == cap) blocks = (tiles + per_block - 1) / per_block;
     p.tile_slots = per_block;
+    p.tiles_base = tiles / blocks;
+    p.tiles_rem = tiles % blocks;
+    p.len_magic = magic16(per);
+    p.m_magic = magic16(p.m);
+    p.run4_magic = static_cast<uint32_t>(((1ull << 32) + run4_of(p.sb_total, gps) - 1) / run4_of(p.sb_total, gps));
+    const uint32_t mk = p.m | (magic16(p.k / 256) << 5);
     const size_t lds = static_cast<size_t>(3) * p.m * (p.k + kLimbPad) +
                        sizeof(float) * static_cast<size_t>(per_block) * 16 * p.m +
                        (ls ? sizeof(float) * static_cast<size_t>(per_block) * nt * p.sb_total * 16 * gps : 0);
@@ -796,7 +816,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const int spg = p.group == 64 ? 1 : p.group == 128 ? 2 : 0;
     const dim3 grid(blocks, slices);
 #define SL_QGEMV_LAUNCH(B, T, G, L, F, W, S) \
-    qgemv_fused<B, T, G, L, F, W, false, S><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)
+    qgemv_fused<B, T, G, L, F, W, false, S><<<grid, threads, lds, s>>>(f.a, f.gamma, mk, p.k, p)
 #define SL_QGEMV_FUSED_F(B, T, G, L)                                                                               \
     (waves == 16 ? (f4 <= 2 ? SL_QGEMV_LAUNCH(B, T, G, L, 2, 16, kSmStream)                                             \
                             : f4 <= 4 ? SL_QGEMV_LAUNCH(B, T, G, L, 4, 16, kSmStream) : SL_QGEMV_LAUNCH(B, T, G, L, 8, 16, kSmStream)) \
@@ -814,7 +834,7 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     if (slices > 1) {
         // k slices: many rows (not LR), 16 waves, 8 float4 per thread
         if (waves != 16 || f4 > 8 || lr) return hipErrorNotSupported;
-#define SL_QGEMV_SLICED(B, G) qgemv_fused<B, 1, G, false, 8, 16, true, kSmStream><<<grid, threads, lds, s>>>(f.a, f.gamma, p.m, p.k, p)
+#define SL_QGEMV_SLICED(B, G) qgemv_fused<B, 1, G, false, 8, 16, true, kSmStream><<<grid, threads, lds, s>>>(f.a, f.gamma, mk, p.k, p)
         if (int4) {
             if (spg == 1) SL_QGEMV_SLICED(4, 1);
             else if (spg == 2) SL_QGEMV_SLICED(4, 2);

@@ -70,6 +70,13 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* global_ptr(T* p)
     return (__attribute__((address_space(1))) T*)p;
 }
 
+// a0, a1 or a2 for si = 0, 1, 2 (si per lane), as two selects
+template <typename T>
+__device__ __forceinline__ T pick3(uint32_t si, T a0, T a1, T a2) {
+    const T r = si >= 1 ? a1 : a0;
+    return si >= 2 ? a2 : r;
+}
+
 // W waves per block (8 or 16); each thread holds at most kMaxF4 float4 of
 // activations (F4: this launch's count), so a block holds max_elems(W).
 // Bytes between consecutive rows of the limb matrices beyond k: the A
@@ -238,11 +245,20 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     // Segment fields are read by constant index and chosen with selects: a
     // runtime index into the argument block (or a struct copy) would turn
     // every access into a dependent memory load.
+    // First tiles of segments 1 and 2 (past the end when absent), as
+    // scalars: a per-lane p.seg[si] would copy the argument block to scratch
+    // memory to index it. The choices below are two selects each: written as
+    // a nested conditional on a per-lane value, they compiled to branches.
+    const uint32_t t1 = __builtin_amdgcn_readfirstlane(p.nseg > 1 ? p.seg[1].tile0 : 0xffffffffu);
+    const uint32_t t2 = __builtin_amdgcn_readfirstlane(p.nseg > 2 ? p.seg[2].tile0 : 0xffffffffu);
     auto seg_of = [&](uint32_t t, uint32_t& tile) -> uint32_t {
         uint32_t si;
         if (NT == 1) {
-            si = (p.nseg > 1 && t >= p.seg[1].tile0 ? 1u : 0u) + (p.nseg > 2 && t >= p.seg[2].tile0 ? 1u : 0u);
-            tile = t - (si == 0 ? 0u : si == 1 ? p.seg[1].tile0 : p.seg[2].tile0);
+            const bool g1 = t >= t1, g2 = t >= t2;
+            si = (g1 ? 1u : 0u) + (g2 ? 1u : 0u);
+            uint32_t off = g1 ? t1 : 0u;
+            off = g2 ? t2 : off;
+            tile = t - off;
         } else {
             si = static_cast<uint32_t>(slot);
             tile = t;
@@ -264,7 +280,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         s_res[i] = uniform_ptr(p.seg[i].resid);
         s_n[i] = __builtin_amdgcn_readfirstlane(p.seg[i].n);
     }
-#define SEG_PICK(a, si) ((si) == 0 ? a[0] : (si) == 1 ? a[1] : a[2])
+#define SEG_PICK(a, si) pick3(si, a[0], a[1], a[2])
     // The stream as a table: lane l of the wave holds item l's weight and
     // scale addresses and its meta word (superblock along k, live flag,
     // last-of-tile flag), worked out once here in parallel; the loop then
@@ -322,11 +338,6 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     if constexpr (LS) {
         // float4 f of the block's runs is float4 o of run r = f / run4
         const uint32_t last = sc4_total ? sc4_total - 1 : 0;  // the launch gives every block a tile
-        // first tiles of segments 1 and 2 (past the end when absent), as
-        // scalars: a per-lane p.seg[si] would copy the argument block to
-        // scratch memory to index it
-        const uint32_t t1 = __builtin_amdgcn_readfirstlane(p.nseg > 1 ? p.seg[1].tile0 : 0xffffffffu);
-        const uint32_t t2 = __builtin_amdgcn_readfirstlane(p.nseg > 2 ? p.seg[2].tile0 : 0xffffffffu);
         static_for<SC>([&](auto u_c) {
             constexpr int u = decltype(u_c)::value;
             const uint32_t f = min(static_cast<uint32_t>(tid + kThreads * u), last);
@@ -334,10 +345,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
             const uint32_t o = f - r * run4;
             uint32_t tile = blockIdx.x + (r / NT) * gridDim.x;
             uint32_t si = r % NT;
-            if (NT == 1) {
-                si = (tile >= t1 ? 1u : 0u) + (tile >= t2 ? 1u : 0u);
-                tile -= si == 0 ? 0u : si == 1 ? t1 : t2;
-            }
+            if (NT == 1) si = seg_of(tile, tile);
             const float* const base = tsc0 + (si == 1 ? tsc_d1 : 0) + (si == 2 ? tsc_d2 : 0);
             const v4f x = global_ptr(reinterpret_cast<const v4f*>(base + tile_sb(tile) * 16 * gps))[o];
             scv[u] = make_float4(x[0], x[1], x[2], x[3]);

@@ -745,8 +745,15 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     const bool int4 = w0.format == SL_QFORMAT_INT4, pair = f.epilogue == kFusedPair, lr = p.m <= 4;
     // Waves per block: 16 for long k (the down projection, k = 14336), which
     // doubles the weight loads in flight per CU and halves each thread's
-    // share of the activation prologue; 8 otherwise.
-    const int waves = p.k >= 8192 || p.m * p.k > max_elems(8) ? 16 : 8;
+    // share of the activation prologue, and for a single weight above 24 MB
+    // whose tiles one round of 16-wave blocks holds (one block per CU
+    // instead of two converting the same activations): [14336 x 4096] 7.95-
+    // 8.04 -> 7.74-7.83 us. 8 otherwise: with 16, lm_head [128256 x 4096]
+    // 47.0 -> 48.1 us, q/k/v and o-proj [4096 x 4096] 0.8 us slower together.
+    const uint64_t weight_bytes = static_cast<uint64_t>(tiles) * p.sb_total * (int4 ? 1024 : 2048) * (pair ? 2 : 1);
+    const bool wide = !pair && p.m == 1 && p.k >= 4096 && weight_bytes > (24ull << 20) &&
+                      tiles <= 4 * compute_units();
+    const int waves = p.k >= 8192 || p.m * p.k > max_elems(8) || wide ? 16 : 8;
     const uint32_t threads = static_cast<uint32_t>(waves) * kWave;
     const uint32_t wpt = f.epilogue == kFusedPair ? waves / 2 : waves;
     const uint32_t sb_per_group = p.group >= 128 ? p.group / 128 : 1;
@@ -761,7 +768,6 @@ hipError_t launch_qgemv_fused(const QgemvFused& f, hipStream_t s) {
     // even shares, for more loads in flight. (Measured on MI355X, M = 1:
     // the q/k/v launch [6144 x 4096] gains 1 us from one block per CU, the
     // gate/up pair [2 x 14336 x 4096] loses 0.5 us.)
-    const uint64_t weight_bytes = static_cast<uint64_t>(tiles) * p.sb_total * (int4 ? 1024 : 2048) * (pair ? 2 : 1);
     uint32_t blocks, per_block;
     const uint32_t per_cap = 4096 / (16 * p.m);
     if (slices > 1) {

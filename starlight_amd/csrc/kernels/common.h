@@ -135,6 +135,68 @@ __device__ __forceinline__ float lane_xor32(float v) {
     return __uint_as_float((threadIdx.x & 32) ? s[0] : s[1]);
 }
 
+// N wave reductions at once (N = 2, 4 or 8 values per lane, as bit
+// patterns; OP combines two, commutatively). Each level of a butterfly
+// pairs two of a lane's values and exchanges half of them: at distance 32,
+// v_permlane32_swap(a, b) leaves a's lower half with b's lower half, and b
+// with both upper halves, so one combine of the two results reduces a in
+// the lower lanes and b in the upper ones; at distance 16 v_permlane16_swap
+// does the same for 16-lane rows; at distance 8 a DPP row rotate by 8. The
+// one value left is then reduced within groups of 64 / N lanes on the DPP
+// network. Lane l ends with the total of value l / (64 / N), every lane of a
+// group holding the same bits: 7 exchanges and 3-5 DPP steps for N = 8,
+// against 8 separate reductions of 4 DPP steps and 4 readlanes each. All 64
+// lanes must be active.
+template <int N, typename Op>
+__device__ __forceinline__ uint32_t lane_reduce_bits(const uint32_t (&v)[N], Op op) {
+    static_assert(N == 2 || N == 4 || N == 8, "two, four or eight values per lane");
+    uint32_t b[N / 2];
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {  // pairs (i, i + N / 2): lanes 0-31 keep i, 32-63 i + N / 2
+        const auto s = __builtin_amdgcn_permlane32_swap(v[i], v[i + N / 2], false, false);
+        b[i] = op(s[0], s[1]);
+    }
+    uint32_t r;
+    if constexpr (N == 2) {
+        r = b[0];
+    } else {
+        uint32_t c[N / 4];
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {  // 16-lane rows 0, 1, 2, 3 keep slots i, i + N / 4 (lower, upper)
+            const auto s = __builtin_amdgcn_permlane16_swap(b[i], b[i + N / 4], false, false);
+            c[i] = op(s[0], s[1]);
+        }
+        if constexpr (N == 4) {
+            r = c[0];
+        } else {  // the 8-lane halves of each row keep c[0] and c[1]
+            const bool upper = (threadIdx.x & 8) != 0;
+            const uint32_t keep = upper ? c[1] : c[0], give = upper ? c[0] : c[1];
+            r = op(keep, static_cast<uint32_t>(dpp_i<kDppRowRor8>(static_cast<int>(give))));
+        }
+    }
+    r = op(r, static_cast<uint32_t>(dpp_i<kDppXor1>(static_cast<int>(r))));
+    r = op(r, static_cast<uint32_t>(dpp_i<kDppXor2>(static_cast<int>(r))));
+    r = op(r, static_cast<uint32_t>(dpp_i<kDppHalfMirror>(static_cast<int>(r))));
+    if constexpr (N <= 4) r = op(r, static_cast<uint32_t>(dpp_i<kDppMirror>(static_cast<int>(r))));
+    if constexpr (N == 2) {
+        const auto s = __builtin_amdgcn_permlane16_swap(r, r, false, false);
+        r = op(r, (threadIdx.x & 16) ? s[0] : s[1]);
+    }
+    return r;
+}
+template <int N>
+__device__ __forceinline__ float lane_reduce_sum(const float (&v)[N]) {
+    uint32_t bits[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) bits[i] = __float_as_uint(v[i]);
+    return __uint_as_float(lane_reduce_bits<N>(
+        bits, [](uint32_t a, uint32_t b) { return __float_as_uint(__uint_as_float(a) + __uint_as_float(b)); }));
+}
+template <int N>
+__device__ __forceinline__ uint32_t lane_reduce_max_u32(const uint32_t (&v)[N]) {
+    return lane_reduce_bits<N>(v, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+
 // Pulls the first BYTES of the kernel's argument segment into the scalar
 // cache with one batch of independent loads (one word per 64-byte line) and
 // waits for them once. Left to itself the compiler fetches arguments as

@@ -408,6 +408,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
         if (static_cast<uint32_t>(wave) * kWave + kThreads * u >= total4) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
 
     if (gamma != nullptr) {
+        // each run's sum of squares over the wave: the F4 runs reduced
+        // together, lane l ending with run l / (64 / F4)'s
+        float ssq[F4];
 #pragma unroll
         for (int u = 0; u < F4; ++u) {
             float ss = 0.f;
@@ -415,8 +418,14 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
             ss = fmaf(v[u].y, v[u].y, ss);
             ss = fmaf(v[u].z, v[u].z, ss);
             ss = fmaf(v[u].w, v[u].w, ss);
-            ss = wave_sum(ss);
-            if (lane == 0) red[u][wave] = ss;
+            ssq[u] = ss;
+        }
+        if constexpr (F4 == 1) {
+            const float ss = wave_sum(ssq[0]);
+            if (lane == 0) red[0][wave] = ss;
+        } else {
+            const float ss = lane_reduce_sum<F4>(ssq);
+            if (lane % (kWave / F4) == 0) red[lane / (kWave / F4)][wave] = ss;
         }
         // Each wave sums the rows w, w + W over the (u, wave) partials of
         // their runs in a fixed order, and stores the row's 1 / rms.
@@ -459,19 +468,29 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     // whose operands are the signed bytes 16 q).
     const uint32_t chunks = K / 256;
     int8_t* const limb_lane = limbs + 4 * lane;  // this lane's word of a limb row's run
+    // max|x| of each run's chunk as a bit pattern (non-negative floats order
+    // as unsigned integers): the F4 runs reduced together, lane l ending
+    // with run l / (64 / F4)'s (F4 > 1)
+    uint32_t lmax[F4];
+#pragma unroll
+    for (int u = 0; u < F4; ++u)
+        lmax[u] = __float_as_uint(fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+    uint32_t rmax;
+    if constexpr (F4 == 1) rmax = wave_max_u32(lmax[0]);
+    else rmax = lane_reduce_max_u32<F4>(lmax);
 #pragma unroll
     for (int u = 0; u < F4; ++u) {
         const uint32_t fb = static_cast<uint32_t>(wave) * kWave + kThreads * u;
         if (fb >= total4) continue;  // whole wave past the end
         const uint32_t r = ru[u];
-        // max|x| of the chunk as a bit pattern (non-negative floats order as
-        // unsigned integers) and ex = its biased exponent - 126: frexp's
-        // exponent, max|x| < 2^ex. A zero or subnormal maximum gives -126:
-        // the chunk's X are then its values in units of 2^-148 (|X| < 2^22),
-        // which drops at most the last bit of a subnormal, and its factor
-        // 2^(ex-22) is itself subnormal (zero for INT4).
-        const uint32_t mb = wave_max_u32(__float_as_uint(
-            fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w)))));
+        // ex = the chunk maximum's biased exponent - 126: frexp's exponent,
+        // max|x| < 2^ex. A zero or subnormal maximum gives -126: the chunk's
+        // X are then its values in units of 2^-148 (|X| < 2^22), which drops
+        // at most the last bit of a subnormal, and its factor 2^(ex-22) is
+        // itself subnormal (zero for INT4).
+        const uint32_t mb = F4 == 1 ? rmax
+                                    : static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rmax),
+                                                                                      u * (kWave / F4)));
         const int ex = static_cast<int>(mb >> 23) - 126;
         const int shift = 22 - ex;
         if (lane == 0) cfac[r * chunks + cb[u] / 64] = ldexpf(1.0f, ex - 22 - (BITS == 4 ? 4 : 0));

@@ -546,7 +546,10 @@ def test_swiglu_parity(hip, quantized, rows, hidden, inter):
 
 @pytest.mark.parametrize("quantized", [False, True])
 @pytest.mark.parametrize("rows,hidden,out_f", [(1, 1, 1), (3, 7, 5), (2, 33, 17), (4, 256, 384), (1, 4096, 1024),
-                                               (3, 512, 640)])
+                                               (3, 512, 640),
+                                               # the fused GEMV's prologue at 2, 4 and 8 float4 of
+                                               # activations per thread (its runs' sums reduced together)
+                                               (2, 4096, 512), (8, 4096, 256), (1, 8192, 256)])
 def test_rms_norm_matmul_parity(hip, quantized, rows, hidden, out_f):
     if quantized and hidden % 128:
         pytest.skip("group size 128 needs hidden multiple of 128")

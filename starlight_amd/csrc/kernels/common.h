@@ -144,9 +144,9 @@ __device__ __forceinline__ float lane_xor32(float v) {
 // does the same for 16-lane rows; at distance 8 a DPP row rotate by 8. The
 // one value left is then reduced within groups of 64 / N lanes on the DPP
 // network. Lane l ends with the total of value l / (64 / N), every lane of a
-// group holding the same bits: 7 exchanges and 3-5 DPP steps for N = 8,
-// against 8 separate reductions of 4 DPP steps and 4 readlanes each. All 64
-// lanes must be active.
+// group holding the same bits. For N = 8 that is 7 exchanges (4 + 2 + 1)
+// and 3 DPP steps, against 8 separate reductions of 4 DPP steps and 4
+// readlanes each. All 64 lanes must be active.
 template <int N, typename Op>
 __device__ __forceinline__ uint32_t lane_reduce_bits(const uint32_t (&v)[N], Op op) {
     static_assert(N == 2 || N == 4 || N == 8, "two, four or eight values per lane");

@@ -549,7 +549,9 @@ def test_swiglu_parity(hip, quantized, rows, hidden, inter):
                                                (3, 512, 640),
                                                # the fused GEMV's prologue at 2, 4 and 8 float4 of
                                                # activations per thread (its runs' sums reduced together)
-                                               (2, 4096, 512), (8, 4096, 256), (1, 8192, 256)])
+                                               (2, 4096, 512), (8, 4096, 256), (1, 8192, 256),
+                                               # rows ending inside a thread's runs, and runs past the input
+                                               (3, 4096, 256), (6, 4096, 128), (12, 2048, 256)])
 def test_rms_norm_matmul_parity(hip, quantized, rows, hidden, out_f):
     if quantized and hidden % 128:
         pytest.skip("group size 128 needs hidden multiple of 128")

@@ -658,6 +658,9 @@ constexpr int kMergeMaxParts = 64;
 // The leading (preloaded) arguments locate the partials: the workspace,
 // P partials per row, head_dim, R = group * seq rows per KV head, and the
 // KV heads; the loads go out while the argument block is fetched.
+// KP > 0: partials per thread, at least ceil(P / T); KP == 0: up to
+// kMergeMaxParts / 4 per thread.
+template <int KP>
 __global__ __launch_bounds__(256) void attn_decode_merge(const float* ws, uint32_t P, uint32_t head_dim, uint32_t R,
                                                          uint32_t kv_heads, Geo g) {
     __shared__ float coef[kMergeMaxParts];
@@ -671,13 +674,21 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* ws, uint32
     const uint32_t T = 256 / D4;  // threads per slot: 4 .. 16
     const uint32_t c = tid % D4, q = tid / D4;  // q >= T (head_dim 192): idle
     const bool mine = q < T;
-    constexpr int kPer = kMergeMaxParts / 4;  // partials per thread at most
+    constexpr int kPer = KP > 0 ? KP : kMergeMaxParts / 4;
     float4 v[kPer];
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-        const uint32_t pp = q + u * T;
-        v[u] = mine && pp < P ? reinterpret_cast<const float4*>(base + (pp * R + r) * row_stride + kDecodePartStride)[c]
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (KP > 0) {
+            // unconditional (partials past P re-read the last one and are
+            // skipped below), so no load waits at a branch's join
+            const uint32_t pp = min(q + u * T, P - 1);
+            v[u] = reinterpret_cast<const float4*>(base + (pp * R + r) * row_stride + kDecodePartStride)[c];
+        } else {
+            const uint32_t pp = q + u * T;
+            v[u] = mine && pp < P
+                       ? reinterpret_cast<const float4*>(base + (pp * R + r) * row_stride + kDecodePartStride)[c]
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     }
     if (tid < kWave) {
         const bool on = static_cast<uint32_t>(lane) < P;
@@ -1107,8 +1118,16 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
 #undef SL_DECODE_LONG
 #undef SL_DECODE_K
 #undef SL_DECODE_ARGS
-    attn_decode_merge<<<dim3(g.kv_heads * static_cast<unsigned>(rows), static_cast<unsigned>(a.batch)), 256, 0, s>>>(
-        g.ws, static_cast<uint32_t>(parts), g.head_dim, static_cast<uint32_t>(rows), g.kv_heads, g);
+    // one partial per merge thread (T = 256 / (head_dim / 4) threads per
+    // float4 slot, each over every T-th partial): the unconditional-load
+    // form; more: the guarded form
+    const bool one = parts <= 256 / (a.head_dim / 4);
+    const dim3 mgrid(g.kv_heads * static_cast<unsigned>(rows), static_cast<unsigned>(a.batch));
+#define SL_MERGE(KP) \
+    attn_decode_merge<KP><<<mgrid, 256, 0, s>>>(g.ws, static_cast<uint32_t>(parts), g.head_dim, static_cast<uint32_t>(rows), g.kv_heads, g)
+    if (one) SL_MERGE(1);
+    else SL_MERGE(0);
+#undef SL_MERGE
     return hipGetLastError();
 }
 

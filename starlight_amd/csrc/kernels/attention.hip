@@ -674,6 +674,13 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* ws, uint32
     const uint32_t T = 256 / D4;  // threads per slot: 4 .. 16
     const uint32_t c = tid % D4, q = tid / D4;  // q >= T (head_dim 192): idle
     const bool mine = q < T;
+    // (m, l) of partial `lane` (lanes past P re-read the last one), loaded
+    // first: wave 0's weights below wait on these loads alone, while the
+    // partial rows are still in flight
+    const bool on = static_cast<uint32_t>(lane) < P;
+    const float2 ml = *reinterpret_cast<const float2*>(
+        base + static_cast<uint64_t>(min(static_cast<uint32_t>(lane), P - 1) * R + r) * row_stride);
+    __builtin_amdgcn_sched_barrier(0);  // kept ahead of the row loads
     constexpr int kPer = KP > 0 ? KP : kMergeMaxParts / 4;
     float4 v[kPer];
 #pragma unroll
@@ -691,10 +698,8 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* ws, uint32
         }
     }
     if (tid < kWave) {
-        const bool on = static_cast<uint32_t>(lane) < P;
-        const float* pr = base + (static_cast<uint64_t>(on ? lane : 0) * R + r) * row_stride;
-        const float mp = on ? pr[0] : -INFINITY;
-        const float lp = on ? pr[1] : 0.f;
+        const float mp = on ? ml.x : -INFINITY;
+        const float lp = on ? ml.y : 0.f;
         const float mx = wave_max(mp);
         const float e = mp == -INFINITY ? 0.f : expf(mp - mx);
         const float total = wave_sum(lp * e);
@@ -1118,14 +1123,16 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
 #undef SL_DECODE_LONG
 #undef SL_DECODE_K
 #undef SL_DECODE_ARGS
-    // one partial per merge thread (T = 256 / (head_dim / 4) threads per
-    // float4 slot, each over every T-th partial): the unconditional-load
-    // form; more: the guarded form
-    const bool one = parts <= 256 / (a.head_dim / 4);
+    // partials per merge thread (T = 256 / (head_dim / 4) threads per float4
+    // slot, each over every T-th partial): up to four, the unconditional
+    // form with exactly that many loads; more, the guarded form
+    const uint64_t T = 256 / (a.head_dim / 4), per = (parts + T - 1) / T;
     const dim3 mgrid(g.kv_heads * static_cast<unsigned>(rows), static_cast<unsigned>(a.batch));
 #define SL_MERGE(KP) \
     attn_decode_merge<KP><<<mgrid, 256, 0, s>>>(g.ws, static_cast<uint32_t>(parts), g.head_dim, static_cast<uint32_t>(rows), g.kv_heads, g)
-    if (one) SL_MERGE(1);
+    if (per <= 1) SL_MERGE(1);
+    else if (per <= 2) SL_MERGE(2);
+    else if (per <= 4) SL_MERGE(4);
     else SL_MERGE(0);
 #undef SL_MERGE
     return hipGetLastError();

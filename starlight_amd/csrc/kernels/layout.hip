@@ -11,28 +11,46 @@
 namespace slhip {
 namespace {
 
-// Copies `rows` rows of `width` floats: dst row r <- src row map(r).
-// Mapping kinds: gather (src row = ids[r]), fixed stride pairs.
+// One row of n > 0 elements (T = float4 or float) copied by a 256-thread
+// block, U elements per thread and pass: each pass issues all of its loads
+// before its first store, so a row of up to 256 U elements costs one memory
+// round trip, not U of them. Loads and stores are unconditional (a guarded
+// store pulls its load into the guard, and a load under a branch is waited
+// for at the join): indices past the row re-read its last element and store
+// it again, unchanged. The launcher picks U = ceil(n / 256) up to 4, so only
+// a row's last 255 or fewer positions are ever re-read.
+template <int U, typename T>
+__device__ __forceinline__ void copy_row(const T* __restrict__ src, T* __restrict__ dst, uint64_t n) {
+    for (uint64_t c0 = threadIdx.x; c0 < n; c0 += U * 256) {
+        T v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = src[min(c0 + u * 256, n - 1)];
+#pragma unroll
+        for (int u = 0; u < U; ++u) dst[min(c0 + u * 256, n - 1)] = v[u];
+    }
+}
+
+// Gather: dst row r <- table row ids[r].
+template <int U>
 __global__ __launch_bounds__(256) void gather_rows(const float* __restrict__ table, const uint32_t* __restrict__ ids,
                                                    float* __restrict__ out, uint64_t hidden, bool vec) {
     const uint64_t r = blockIdx.x;
     const uint64_t src = static_cast<uint64_t>(ids[r]) * hidden;
     const uint64_t dst = r * hidden;
-    if (vec) {
-        const float4* s4 = reinterpret_cast<const float4*>(table + src);
-        float4* d4 = reinterpret_cast<float4*>(out + dst);
-        for (uint64_t c = threadIdx.x; c < hidden / 4; c += blockDim.x) d4[c] = s4[c];
-    } else {
-        for (uint64_t c = threadIdx.x; c < hidden; c += blockDim.x) out[dst + c] = table[src + c];
-    }
+    if (vec)
+        copy_row<U>(reinterpret_cast<const float4*>(table + src), reinterpret_cast<float4*>(out + dst), hidden / 4);
+    else
+        copy_row<U>(table + src, out + dst, hidden);
 }
 
+template <int U>
 __global__ __launch_bounds__(256) void last_token_rows(const float* __restrict__ in, float* __restrict__ out,
-                                                       uint64_t seq, uint64_t hidden, uint64_t position) {
+                                                       uint64_t seq, uint64_t hidden, uint64_t position, bool vec) {
     const uint64_t b = blockIdx.x;
     const float* src = in + (b * seq + position) * hidden;
     float* dst = out + b * hidden;
-    for (uint64_t c = threadIdx.x; c < hidden; c += blockDim.x) dst[c] = src[c];
+    if (vec) copy_row<U>(reinterpret_cast<const float4*>(src), reinterpret_cast<float4*>(dst), hidden / 4);
+    else copy_row<U>(src, dst, hidden);
 }
 
 // [B, S, H, D] <-> [B, H, S, D]: one thread per output element group of VEC.
@@ -120,18 +138,34 @@ __global__ __launch_bounds__(256) void paged_store_rows(const float* __restrict_
 
 }  // namespace
 
+// elements per thread and pass of copy_row for a row of n elements
+static int copy_per_thread(uint64_t n) { return n <= 256 ? 1 : n <= 512 ? 2 : n <= 768 ? 3 : 4; }
+
 hipError_t launch_gather(const float* table, const uint32_t* ids, float* out, uint64_t rows,
                          uint64_t hidden, hipStream_t s) {
     if (rows == 0 || hidden == 0) return hipSuccess;
     const bool vec = hidden % 4 == 0 && aligned16(table) && aligned16(out);
-    gather_rows<<<static_cast<unsigned>(rows), 256, 0, s>>>(table, ids, out, hidden, vec);
+    const dim3 grid(static_cast<unsigned>(rows));
+    switch (copy_per_thread(vec ? hidden / 4 : hidden)) {
+        case 1: gather_rows<1><<<grid, 256, 0, s>>>(table, ids, out, hidden, vec); break;
+        case 2: gather_rows<2><<<grid, 256, 0, s>>>(table, ids, out, hidden, vec); break;
+        case 3: gather_rows<3><<<grid, 256, 0, s>>>(table, ids, out, hidden, vec); break;
+        default: gather_rows<4><<<grid, 256, 0, s>>>(table, ids, out, hidden, vec); break;
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_last_token(const float* in, float* out, uint64_t batch, uint64_t seq, uint64_t hidden,
                              uint64_t seq_len, hipStream_t s) {
     if (batch == 0 || hidden == 0) return hipSuccess;
-    last_token_rows<<<static_cast<unsigned>(batch), 256, 0, s>>>(in, out, seq, hidden, seq_len - 1);
+    const bool vec = hidden % 4 == 0 && aligned16(in) && aligned16(out);
+    const dim3 grid(static_cast<unsigned>(batch));
+    switch (copy_per_thread(vec ? hidden / 4 : hidden)) {
+        case 1: last_token_rows<1><<<grid, 256, 0, s>>>(in, out, seq, hidden, seq_len - 1, vec); break;
+        case 2: last_token_rows<2><<<grid, 256, 0, s>>>(in, out, seq, hidden, seq_len - 1, vec); break;
+        case 3: last_token_rows<3><<<grid, 256, 0, s>>>(in, out, seq, hidden, seq_len - 1, vec); break;
+        default: last_token_rows<4><<<grid, 256, 0, s>>>(in, out, seq, hidden, seq_len - 1, vec); break;
+    }
     return hipGetLastError();
 }
 
@@ -189,7 +223,7 @@ hipError_t launch_paged_store(const float* state, float* pool, const uint32_t* t
 // that needs it (about 1-2 ms each, more for large objects).
 hipError_t load_code_layout() {
     hipFuncAttributes attr;
-    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&gather_rows));
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&gather_rows<4>));
 }
 
 }  // namespace slhip

@@ -157,7 +157,11 @@ def test_rope_parity(hip, variant, batch, heads, seq, hd, theta, rank3):
 # ----------------------------------------------------------------- layout --
 
 
-@pytest.mark.parametrize("vocab,hidden,rows", [(10, 5, 3), (1, 1, 1), (4, 7, 0), (13, 9, 6), (1000, 4096, 37)])
+# rows of one pass (<= 1024 float4 or floats per 256 threads), of several,
+# and of a pass that ends inside a thread's four loads
+@pytest.mark.parametrize("vocab,hidden,rows", [(10, 5, 3), (1, 1, 1), (4, 7, 0), (13, 9, 6), (1000, 4096, 37),
+                                               (20, 2048, 4), (50, 8192, 3), (9, 6000, 2), (7, 1025, 2),
+                                               (5, 4099, 3)])
 def test_gather_parity(hip, vocab, hidden, rows):
     r = rng(vocab + rows)
     table = r.standard_normal(vocab * hidden).astype(np.float32)
@@ -174,7 +178,9 @@ def test_gather_parity(hip, vocab, hidden, rows):
         assert np.array_equal(read(hip, orf), oracle.gather(table, ids, vocab, hidden, rows))
 
 
-@pytest.mark.parametrize("batch,seq,hidden,seq_len", [(1, 1, 3, 1), (3, 5, 4, 5), (2, 4, 7, 2), (2, 64, 4096, 40)])
+@pytest.mark.parametrize("batch,seq,hidden,seq_len", [(1, 1, 3, 1), (3, 5, 4, 5), (2, 4, 7, 2), (2, 64, 4096, 40),
+                                                     (1, 1, 4096, 1), (1, 1, 2048, 1), (2, 3, 8192, 3),
+                                                     (3, 2, 1030, 1), (2, 2, 6004, 2)])
 def test_last_token_parity(hip, batch, seq, hidden, seq_len):
     x = rng(seq).standard_normal(batch * seq * hidden).astype(np.float32)
     _, xr = put(hip, x)

@@ -621,9 +621,10 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
             d->stats.fused_commands += used;
             return used;
         }
-        // Many rows (prefill): the norm on its own, then the projections as
-        // one q-GEMM launch over the normed rows (one activation split for
-        // all of them), a residual Add in its epilogue. The split copies the
+        // Many rows (prefill): the projections as one q-GEMM launch over one
+        // activation split for all of them, a residual Add in its epilogue.
+        // The norm runs inside the split when nothing after the unit reads
+        // its output, else on its own first. The split copies the
         // activations into the workspace before the GEMM starts, so the
         // Add's output may reuse their space.
         if (rows <= 16) return 0;  // few rows the fused GEMV did not take: one launch each
@@ -637,10 +638,15 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
         if (residual) ++used;
         // the product itself, when nothing after the Add reads it, is not written
         if (residual && dead_after(d, i + used, outs[0])) f.out[0] = nullptr;
-        e = norm ? launch_rms_norm(f.a, f.gamma, f.normed, rows, k, f.eps, d->stream) : hipSuccess;
+        // (dead from the command after its last reader on: the unit's Add,
+        // which may overwrite it, counts)
+        const bool norm_in_split = norm && qgemm_norm_takes(k, f.gamma) && qgemm_mfma_takes(f.a, f.w, cnt, rows, ws) &&
+                                   dead_after(d, j + cnt, norm->out);
+        e = norm && !norm_in_split ? launch_rms_norm(f.a, f.gamma, f.normed, rows, k, f.eps, d->stream) : hipSuccess;
         if (e == hipSuccess)
-            e = launch_qgemm_multi(a, f.w, f.out, cnt, rows, ws, d->stream, nullptr, residual ? f.resid : nullptr,
-                                   residual ? f.out2 : nullptr);
+            e = launch_qgemm_multi(norm_in_split ? f.a : a, f.w, f.out, cnt, rows, ws, d->stream, nullptr,
+                                   residual ? f.resid : nullptr, residual ? f.out2 : nullptr,
+                                   norm_in_split ? f.gamma : nullptr, f.eps);
         *err = e;
         d->stats.fused_commands += used;
         return used;
@@ -675,6 +681,9 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
             // before its products run, so the Add's output may reuse their
             // space, unless it is shifted against them and a later chunk
             // still reads rows an earlier chunk's Add wrote.
+            // The norm runs inside the gate/up split when nothing after the
+            // unit reads its output and every row chunk takes that route
+            // (launch_swiglu then launches nothing else first), else on its own.
             size_t used = (j - i) + 1;
             const Logged* add = j + 1 < n ? &d->log[j + 1] : nullptr;
             const sl_buffer_ref x_ref = norm ? norm->out : c1.in[0];
@@ -682,15 +691,28 @@ size_t try_fuse(Device* d, size_t i, hipError_t* err) {
             if (other >= 0 && overlaps(add->out, x_ref) && !same_ref(add->out, x_ref) &&
                 swiglu_chunk_rows(d->workspace_floats, inter) < rows)
                 other = -1;
-            e = norm ? launch_rms_norm(f.a, f.gamma, f.normed, rows, hidden, f.eps, d->stream) : hipSuccess;
-            if (e == hipSuccess)
-                e = launch_swiglu(norm ? f.normed : f.a, weight_ref(d, c1.in[1], c1.plan.quant[1]),
-                                  weight_ref(d, c1.in[2], c1.plan.quant[2]), weight_ref(d, c1.in[3], c1.plan.quant[3]),
-                                  fptr(d, c1.out), rows, hidden, inter,
-                                  Workspace{d->workspace, d->workspace_floats},
-                                  d->stream, other >= 0 ? fptr(d, add->in[other]) : nullptr,
-                                  other >= 0 ? fptr(d, add->out) : nullptr,
-                                  other >= 0 && dead_after(d, i + used + 1, c1.out));
+            // with the norm in the split, the chunks read its input instead
+            // (its output is dead from the command after the SwiGlu on: the
+            // unit's Add, which may overwrite it, counts)
+            const bool fold = norm && !(other >= 0 && overlaps(add->out, norm->in[0]) &&
+                                        !same_ref(add->out, norm->in[0]) &&
+                                        swiglu_chunk_rows(d->workspace_floats, inter) < rows) &&
+                              dead_after(d, j + 1, norm->out);
+            const auto run = [&](bool in_split) {
+                return launch_swiglu(in_split ? f.a : norm ? f.normed : f.a, weight_ref(d, c1.in[1], c1.plan.quant[1]),
+                                     weight_ref(d, c1.in[2], c1.plan.quant[2]),
+                                     weight_ref(d, c1.in[3], c1.plan.quant[3]), fptr(d, c1.out), rows, hidden, inter,
+                                     Workspace{d->workspace, d->workspace_floats}, d->stream,
+                                     other >= 0 ? fptr(d, add->in[other]) : nullptr,
+                                     other >= 0 ? fptr(d, add->out) : nullptr,
+                                     other >= 0 && dead_after(d, i + used + 1, c1.out), in_split ? f.gamma : nullptr,
+                                     f.eps);
+            };
+            e = fold ? run(true) : hipErrorNotSupported;
+            if (e == hipErrorNotSupported) {
+                e = norm ? launch_rms_norm(f.a, f.gamma, f.normed, rows, hidden, f.eps, d->stream) : hipSuccess;
+                if (e == hipSuccess) e = run(false);
+            }
             if (other >= 0) ++used;
             *err = e;
             d->stats.fused_commands += used;

@@ -30,7 +30,8 @@ uint64_t swiglu_chunk_rows(uint64_t ws_floats, uint64_t inter) {
 
 hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up, const WeightRef& down,
                          float* out, uint64_t rows, uint64_t hidden, uint64_t inter, const Workspace& ws,
-                         hipStream_t s, const float* resid, float* out2, bool out_dead) {
+                         hipStream_t s, const float* resid, float* out2, bool out_dead, const float* gamma,
+                         float eps) {
     if (rows == 0) return hipSuccess;
     const uint64_t budget = ws.floats / 2;
     uint64_t chunk = swiglu_chunk_rows(ws.floats, inter);
@@ -40,7 +41,19 @@ hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef&
     float* g = ws.data;
     float* u = ws.data + u_off;
     const Workspace rest = ws.after(budget);
-    if (rows <= 16 && gate.quantized() && up.quantized()) {
+    const QuantWeight* gate_up[2] = {&gate.quant, &up.quant};
+    if (gamma != nullptr) {
+        // the norm exists only inside the gate/up split: every chunk (the
+        // full ones and the last) must take the q-GEMM route
+        const uint64_t tail = rows % chunk;
+        const auto takes = [&](uint64_t rc) {
+            return rc > 16 && qgemm_mfma_takes(x, gate_up, 2, rc, rest);
+        };
+        if (!gate.quantized() || !up.quantized() || !qgemm_norm_takes(hidden, gamma) || !takes(chunk) ||
+            (tail != 0 && !takes(tail)))
+            return hipErrorNotSupported;
+    }
+    if (rows <= 16 && gate.quantized() && up.quantized() && gamma == nullptr) {
         // gate and up tiles in one launch with the silu * up epilogue
         QgemvFused f{};
         f.a = x;
@@ -58,7 +71,6 @@ hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef&
         }
         if (e != hipErrorNotSupported) return e;
     }
-    const QuantWeight* gate_up[2] = {&gate.quant, &up.quant};
     float* gu_out[2] = {g, u};
     for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
         const uint64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
@@ -66,7 +78,7 @@ hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef&
         hipError_t e;
         if (gate.quantized() && up.quantized() && rc > 16 && qgemm_mfma_takes(xr, gate_up, 2, rc, rest)) {
             // many rows: gate and up in one launch over one activation split
-            e = launch_qgemm_multi(xr, gate_up, gu_out, 2, rc, rest, s);
+            e = launch_qgemm_multi(xr, gate_up, gu_out, 2, rc, rest, s, nullptr, nullptr, nullptr, gamma, eps);
         } else {
             e = launch_linear(xr, gate, g, rc, inter, hidden, rest, s);
             if (e == hipSuccess) e = launch_linear(xr, up, u, rc, inter, hidden, rest, s);
@@ -115,11 +127,20 @@ hipError_t launch_rms_norm_matmul(const float* x, const float* weight, const Wei
         hipError_t e = launch_qgemv_fused(f, s);
         if (e != hipErrorNotSupported) return e;
     }
+    const QuantWeight* wq[1] = {&w.quant};
     for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
         const uint64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
-        hipError_t e = launch_rms_norm(x + r0 * hidden, weight, y, rc, hidden, eps, s);
-        if (e == hipSuccess)
-            e = launch_linear(y, w, out + r0 * out_features, rc, out_features, hidden, ws.after(budget), s);
+        const float* xr = x + r0 * hidden;
+        float* outs[1] = {out + r0 * out_features};
+        hipError_t e;
+        if (w.quantized() && rc > 16 && qgemm_norm_takes(hidden, weight) &&
+            qgemm_mfma_takes(xr, wq, 1, rc, ws.after(budget))) {
+            // many rows: the norm inside the q-GEMM's activation split
+            e = launch_qgemm_multi(xr, wq, outs, 1, rc, ws.after(budget), s, nullptr, nullptr, nullptr, weight, eps);
+        } else {
+            e = launch_rms_norm(xr, weight, y, rc, hidden, eps, s);
+            if (e == hipSuccess) e = launch_linear(y, w, outs[0], rc, out_features, hidden, ws.after(budget), s);
+        }
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -232,12 +232,17 @@ hipError_t launch_qgemm_mfma(const float* a, const QuantWeight& w, float* out, u
 // a * dequant(w[i])^T. With u, the activations are silu(a) * u (SwiGlu's
 // down projection, elementwise); with out2[i] set, also out2[i] = resid[i]
 // + out[i] (a residual Add), and out[i] may then be null (the product
-// itself not written, when nothing reads it). qgemm_mfma_takes says whether
-// a launch would run.
+// itself not written, when nothing reads it). With gamma (and no u), the
+// activations are RMSNorm(a) * gamma (epsilon eps), formed by the
+// activation split bit-identical to launch_rms_norm's vectorised kernel (the
+// normalised rows are not written anywhere); qgemm_norm_takes says whether
+// k and gamma allow it. qgemm_mfma_takes says whether a launch would run.
 bool qgemm_mfma_takes(const float* a, const QuantWeight* const* w, uint32_t nseg, uint64_t m, const Workspace& ws);
+bool qgemm_norm_takes(uint64_t k, const float* gamma);
 hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float* const* out, uint32_t nseg,
                               uint64_t m, const Workspace& ws, hipStream_t s, const float* u = nullptr,
-                              const float* const* resid = nullptr, float* const* out2 = nullptr);
+                              const float* const* resid = nullptr, float* const* out2 = nullptr,
+                              const float* gamma = nullptr, float eps = 0.f);
 hipError_t launch_qmatmul(const float* a, const QuantWeight& w, float* out, uint64_t m, const Workspace& ws,
                           hipStream_t s);
 // The MFMA decode path (m <= 16, Mfma layout); returns hipErrorNotSupported
@@ -288,10 +293,14 @@ uint64_t swiglu_chunk_rows(uint64_t ws_floats, uint64_t inter);
 // SwiGlu (reference/swiglu.rs): out = (silu(x Wg^T) * (x Wu^T)) Wd^T.
 // With out2, also out2 = resid + out (a residual Add after the SwiGlu);
 // out_dead: nothing reads out afterwards, so the q-GEMM route may skip it.
+// With gamma, x is normalised first (RMSNorm, epsilon eps) inside the gate/up
+// q-GEMM's activation split; hipErrorNotSupported, before anything is
+// launched, unless every row chunk takes that route.
 hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef& up,
                          const WeightRef& down, float* out, uint64_t rows, uint64_t hidden,
                          uint64_t inter, const Workspace& ws, hipStream_t s, const float* resid = nullptr,
-                         float* out2 = nullptr, bool out_dead = false);
+                         float* out2 = nullptr, bool out_dead = false, const float* gamma = nullptr,
+                         float eps = 0.f);
 // gate/up epilogue: h = silu(g) * u, elementwise over n values.
 hipError_t launch_silu_mul(const float* g, const float* u, float* h, uint64_t n, hipStream_t s);
 // RmsNormMatMul (reference/fused.rs): out = rms_norm(x, weight) W^T.

@@ -71,14 +71,16 @@ __device__ __forceinline__ float4 act4(const float4* row, const float4* urow, ui
 __device__ constexpr int kPerm8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
 
 // Row r: E with max |a| < 2^E (0 for an all-zero row), then hi/lo of
-// a * 2^(15 - E); with u, of silu(a) * u. k % 8 == 0 and rows 16-byte
-// aligned. NP > 0: the row's values stay in registers between the two
-// passes (thread t holds the 8-element groups t + 256 j, j < NP, so k <=
-// 2048 NP), and a and u are read once; NP == 0 reads the row twice.
+// a * 2^(15 - E); with u, of silu(a) * u; with gamma (NP > 0, k <= 8192,
+// no u), of RMSNorm(a) * gamma. k % 8 == 0 and rows 16-byte aligned.
+// NP > 0: the row's values stay in registers between the two passes
+// (thread t holds the 8-element groups t + 256 j, j < NP, so k <= 2048 NP),
+// and a and u are read once; NP == 0 reads the row twice.
 template <int NP>
 __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, const float* __restrict__ u,
                                                   _Float16* __restrict__ hi, _Float16* __restrict__ lo,
-                                                  int* __restrict__ row_exp, uint32_t k) {
+                                                  int* __restrict__ row_exp, uint32_t k,
+                                                  const float* __restrict__ gamma, float eps) {
     __shared__ float scratch[4];
     const uint64_t r = blockIdx.x;
     const float4* row = reinterpret_cast<const float4*>(a + r * k);
@@ -88,15 +90,58 @@ __global__ __launch_bounds__(256) void split_rows(const float* __restrict__ a, c
     float4 keep[NP > 0 ? 2 * NP : 1];
     float mx = 0.f;
     if constexpr (NP > 0) {
+        if (gamma != nullptr) {
+            // RMSNorm first. Its sum of squares runs in the standalone
+            // kernel's order (rms_norm_vec: thread t over float4 columns t +
+            // 256 i, ascending, then block_sum), from a second set of loads
+            // of the row, so the normalised values are bit-identical to that
+            // kernel's output. Every load is unconditional (clamped indices;
+            // columns past the row count as zeros, which leave the sum
+            // unchanged) and issued before any of them is used.
+            const float4* g4 = reinterpret_cast<const float4*>(gamma);
+            float4 xv[2 * NP], gv[2 * NP];
 #pragma unroll
-        for (int j = 0; j < NP; ++j) {
-            const uint32_t i = threadIdx.x + 256 * j;
-            if (i < groups) {
-                keep[2 * j] = act4(row, urow, 2 * i);
-                keep[2 * j + 1] = act4(row, urow, 2 * i + 1);
-                const float4 v0 = keep[2 * j], v1 = keep[2 * j + 1];
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))));
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+            for (int j = 0; j < NP; ++j) {
+                const uint32_t i = min(threadIdx.x + 256u * j, groups - 1);
+                keep[2 * j] = row[2 * i];
+                keep[2 * j + 1] = row[2 * i + 1];
+                gv[2 * j] = g4[2 * i];
+                gv[2 * j + 1] = g4[2 * i + 1];
+            }
+#pragma unroll
+            for (int i = 0; i < 2 * NP; ++i) xv[i] = row[min(threadIdx.x + 256u * i, k4 - 1)];
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < 2 * NP; ++i) {
+                const float4 v = threadIdx.x + 256u * i < k4 ? xv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+            ss = block_sum(ss, scratch);
+            const float inv = 1.0f / sqrtf(ss / static_cast<float>(k) + eps);
+#pragma unroll
+            for (int j = 0; j < 2 * NP; ++j) {
+                float4& v = keep[j];
+                v.x = (v.x * inv) * gv[j].x;
+                v.y = (v.y * inv) * gv[j].y;
+                v.z = (v.z * inv) * gv[j].z;
+                v.w = (v.w * inv) * gv[j].w;
+                // groups past the row repeat the last one: the maximum is unchanged
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NP; ++j) {
+                const uint32_t i = threadIdx.x + 256 * j;
+                if (i < groups) {
+                    keep[2 * j] = act4(row, urow, 2 * i);
+                    keep[2 * j + 1] = act4(row, urow, 2 * i + 1);
+                    const float4 v0 = keep[2 * j], v1 = keep[2 * j + 1];
+                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))));
+                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+                }
             }
         }
     } else {
@@ -482,21 +527,25 @@ bool qgemm_mfma_takes(const float* a, const QuantWeight* const* w, uint32_t nseg
     return blocks <= 0xffffffffull && split_layout(m, w0.k).floats <= ws.floats;
 }
 
+bool qgemm_norm_takes(uint64_t k, const float* gamma) { return gamma != nullptr && aligned16(gamma) && k <= 2048 * 4; }
+
 hipError_t launch_qgemm_multi(const float* a, const QuantWeight* const* w, float* const* out, uint32_t nseg,
                               uint64_t m, const Workspace& ws, hipStream_t s, const float* u,
-                              const float* const* resid, float* const* out2) {
+                              const float* const* resid, float* const* out2, const float* gamma, float eps) {
     if (!qgemm_mfma_takes(a, w, nseg, m, ws)) return hipErrorNotSupported;
     const QuantWeight& w0 = *w[0];
+    if (gamma != nullptr && (u != nullptr || !qgemm_norm_takes(w0.k, gamma))) return hipErrorNotSupported;
     const SplitLayout lay = split_layout(m, w0.k);
     _Float16* hi = reinterpret_cast<_Float16*>(ws.data);
     _Float16* lo = reinterpret_cast<_Float16*>(ws.data + lay.lo_at);
     int* row_exp = reinterpret_cast<int*>(ws.data + lay.exp_at);
     // rows of up to 32768 elements stay in registers between the passes
     const uint32_t kk = static_cast<uint32_t>(w0.k);
-    if (w0.k <= 2048 * 4) split_rows<4><<<static_cast<unsigned>(m), 256, 0, s>>>(a, u, hi, lo, row_exp, kk);
-    else if (w0.k <= 2048 * 8) split_rows<8><<<static_cast<unsigned>(m), 256, 0, s>>>(a, u, hi, lo, row_exp, kk);
-    else if (w0.k <= 2048 * 16) split_rows<16><<<static_cast<unsigned>(m), 256, 0, s>>>(a, u, hi, lo, row_exp, kk);
-    else split_rows<0><<<static_cast<unsigned>(m), 256, 0, s>>>(a, u, hi, lo, row_exp, kk);
+    const dim3 sgrid(static_cast<unsigned>(m));
+    if (w0.k <= 2048 * 4) split_rows<4><<<sgrid, 256, 0, s>>>(a, u, hi, lo, row_exp, kk, gamma, eps);
+    else if (w0.k <= 2048 * 8) split_rows<8><<<sgrid, 256, 0, s>>>(a, u, hi, lo, row_exp, kk, nullptr, 0.f);
+    else if (w0.k <= 2048 * 16) split_rows<16><<<sgrid, 256, 0, s>>>(a, u, hi, lo, row_exp, kk, nullptr, 0.f);
+    else split_rows<0><<<sgrid, 256, 0, s>>>(a, u, hi, lo, row_exp, kk, nullptr, 0.f);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     GemmArgs p{};

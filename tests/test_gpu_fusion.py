@@ -523,6 +523,87 @@ def test_prefill_norm_and_projections_run_as_one_gemm(hip, fmt_name):
         assert_normwise(got[i], want[i])
 
 
+@pytest.mark.parametrize("fmt_name,k", [("INT4", 512), ("INT4", 4096), ("INT8", 2048)])
+def test_prefill_norm_inside_the_activation_split(hip, fmt_name, k):
+    """RmsNorm at 64 rows whose output nothing reads after its projections
+    (a later command overwrites it): the norm runs inside the q-GEMM's
+    activation split and its output is never written. Two units: q/k/v
+    (three MatMulNT as one launch), and a SwiGlu with the residual Add of
+    the norm's input after it (h2 = h + ffn(norm(h))), once also with h2
+    written over the norm output by the unit's own Add. Each result
+    is bit-identical to the same commands with the norm output left live
+    (the norm then runs as its own launch first), and matches the oracle
+    normwise per row (1e-4)."""
+    from starlight_amd import quant
+    from starlight_amd.ir import QuantFormat
+
+    fmt = QuantFormat[fmt_name]
+    r = np.random.default_rng(k + len(fmt_name))
+    rows, nq, nkv, inter = 64, 256, 128, 384
+    x = r.standard_normal((rows, k)).astype(np.float32)
+    gamma = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+
+    def qw(n, cols):
+        w = (r.standard_normal((n, cols)) * 0.05).astype(np.float32)
+        words, scales = quant.quantize(w, 128, fmt)
+        wb, sb = hip.upload_new_u32(words), hip.upload_new_f32(scales)
+        hip.bind_quantized(wb, sb, fmt, 128, n, cols)
+        return (BufferRef(wb, 0, words.size), Value.quantized([n, cols], fmt, 128),
+                quant.dequantize(words, scales, n, cols, 128, fmt))
+
+    wq, wk, wv = qw(nq, k), qw(nkv, k), qw(nkv, k)
+    g, u, d = qw(inter, k), qw(inter, k), qw(k, inter)
+    G = BufferRef(hip.upload_new_f32(gamma), 0, k)
+    xv, gv = Value.f32([1, rows, k]), Value.f32([k], ValueRole.PARAM)
+    normed = oracle.rms_norm(x.ravel(), gamma, rows, k, 1e-5)
+
+    def run(dead, add_into_norm=False):
+        X = BufferRef(hip.upload_new_f32(x.ravel()), 0, rows * k)
+        N = BufferRef(hip.allocate_f32(rows * k, 256), 0, rows * k)
+        W = BufferRef(hip.upload_new_f32(np.ones(rows * k, np.float32)), 0, rows * k)
+        outs = {name: BufferRef(hip.allocate_f32(rows * n, 256), 0, rows * n) for name, n in
+                (("q", nq), ("k", nkv), ("v", nkv))}
+        before = hip.stats()
+        hip.dispatch(Op.rms_norm(1e-5), [X, G], [xv, gv], [N], [xv])
+        for name, w, n in (("q", wq, nq), ("k", wk, nkv), ("v", wv, nkv)):
+            hip.dispatch(Op.matmul_nt(), [N, w[0]], [xv, w[1]], [outs[name]], [Value.f32([1, rows, n])])
+        if dead:
+            hip.dispatch(Op.scale_by(2.0), [W], [xv], [N], [xv])
+        hip.synchronize()
+        assert hip.stats()["fused_commands"] - before["fused_commands"] == 4
+        got = {name: hip.read_f32(o.buffer, o.len) for name, o in outs.items()}
+        if dead:
+            np.testing.assert_array_equal(hip.read_f32(N.buffer, rows * k), np.full(rows * k, 2, np.float32))
+        # the feed-forward half of a layer: h2 = h + SwiGlu(norm(h))
+        # (add_into_norm: the Add's output takes the norm output's place, as
+        # a memory plan reuses it once the SwiGlu has read it)
+        Y = BufferRef(hip.allocate_f32(rows * k, 256), 0, rows * k)
+        H2 = N if add_into_norm else BufferRef(hip.allocate_f32(rows * k, 256), 0, rows * k)
+        before = hip.stats()
+        hip.dispatch(Op.rms_norm(1e-5), [X, G], [xv, gv], [N], [xv])
+        hip.dispatch(Op.swiglu(), [N, g[0], u[0], d[0]], [xv, g[1], u[1], d[1]], [Y], [xv])
+        hip.dispatch(Op.add(), [Y, X], [xv, xv], [H2], [xv])
+        if dead and not add_into_norm:
+            hip.dispatch(Op.scale_by(2.0), [W], [xv], [N], [xv])
+        hip.synchronize()
+        assert hip.stats()["fused_commands"] - before["fused_commands"] == 3
+        got["h"] = hip.read_f32(H2.buffer, rows * k)
+        return got
+
+    folded, separate, overwritten = run(True), run(False), run(True, add_into_norm=True)
+    for name in ("q", "k", "v", "h"):
+        np.testing.assert_array_equal(folded[name], separate[name])
+    np.testing.assert_array_equal(overwritten["h"], separate["h"])
+    for name, w, n in (("q", wq, nq), ("k", wk, nkv), ("v", wv, nkv)):
+        want = oracle.matmul_nt(normed, w[2], 1, rows, k, n).reshape(rows, n)
+        for i in range(rows):
+            assert_normwise(folded[name].reshape(rows, n)[i], want[i])
+    ffn = oracle.swiglu(normed, g[2], u[2], d[2], rows, k, inter).reshape(rows, k)
+    h = folded["h"].reshape(rows, k)
+    for i in range(rows):
+        assert_normwise(h[i] - x[i], ffn[i])
+
+
 @pytest.mark.parametrize("fmt_name,residual", [("INT4", True), ("INT4", False), ("INT8", True)])
 def test_long_k_gemv_with_many_rows(hip, fmt_name, residual):
     """A quantized MatMulNT with 8 rows of k = 14336 (the down projection at

@@ -558,7 +558,11 @@ def test_swiglu_parity(hip, quantized, rows, hidden, inter):
                                                # activations per thread (its runs' sums reduced together)
                                                (2, 4096, 512), (8, 4096, 256), (1, 8192, 256),
                                                # rows ending inside a thread's runs, and runs past the input
-                                               (3, 4096, 256), (6, 4096, 128), (12, 2048, 256)])
+                                               (3, 4096, 256), (6, 4096, 128), (12, 2048, 256),
+                                               # many rows: the norm inside the q-GEMM's activation split
+                                               # (up to 8192 wide), or on its own past that
+                                               (64, 4096, 256), (40, 2048, 384), (100, 8192, 128),
+                                               (33, 12288, 128)])
 def test_rms_norm_matmul_parity(hip, quantized, rows, hidden, out_f):
     if quantized and hidden % 128:
         pytest.skip("group size 128 needs hidden multiple of 128")

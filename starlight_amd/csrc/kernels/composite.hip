@@ -80,6 +80,8 @@ hipError_t launch_swiglu(const float* x, const WeightRef& gate, const WeightRef&
             // many rows: gate and up in one launch over one activation split
             e = launch_qgemm_multi(xr, gate_up, gu_out, 2, rc, rest, s, nullptr, nullptr, nullptr, gamma, eps);
         } else {
+            // (never with gamma: the check above covers every chunk)
+            if (gamma != nullptr) return hipErrorInvalidValue;
             e = launch_linear(xr, gate, g, rc, inter, hidden, rest, s);
             if (e == hipSuccess) e = launch_linear(xr, up, u, rc, inter, hidden, rest, s);
         }

@@ -17,8 +17,9 @@ namespace {
 // round trip, not U of them. Loads and stores are unconditional (a guarded
 // store pulls its load into the guard, and a load under a branch is waited
 // for at the join): indices past the row re-read its last element and store
-// it again, unchanged. The launcher picks U = ceil(n / 256) up to 4, so only
-// a row's last 255 or fewer positions are ever re-read.
+// it again, unchanged. The launcher picks U = ceil(n / 256) up to 4, so a
+// row of up to 1024 elements has at most 255 such slots; a longer row's last
+// pass has up to 1023.
 template <int U, typename T>
 __device__ __forceinline__ void copy_row(const T* __restrict__ src, T* __restrict__ dst, uint64_t n) {
     for (uint64_t c0 = threadIdx.x; c0 < n; c0 += U * 256) {

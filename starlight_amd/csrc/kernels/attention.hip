@@ -1056,16 +1056,20 @@ Geo make_geo(const AttentionArgs& a, const Workspace& ws) {
     return g;
 }
 
-// Partials per (row, KV head): one per 128 positions of max_seq, at most
-// kMergeMaxParts, and no more than keep the grid near kDecodeGridBlocks
-// blocks. Each block's share is latency-bound (one or two 16-key tiles per
-// wave), so a batch of many sequences is better served by fewer, longer
-// partials than by rounds of short blocks (8B, batch 8: 2,022 tok/s at 512
-// blocks, 2,006 at 1024, 1,946 with 32 partials as at batch 1). Shapes only:
-// the grid never depends on past_len.
+// Partials per (row, KV head): one per 128 positions of max_seq (64 for
+// head_dim 64, whose waves then take 8-key tiles), at most kMergeMaxParts,
+// and no more than keep the grid near kDecodeGridBlocks blocks. Each
+// block's share is latency-bound (one or two tiles per wave), so a batch of
+// many sequences is better served by fewer, longer partials than by rounds
+// of short blocks (8B, batch 8: 2,022 tok/s at 512 blocks, 2,006 at 1024,
+// 1,946 with 32 partials as at batch 1). Half the positions per partial and
+// 8-key tiles at head_dim 64: 1B decode 1,860-1,881 -> 1,884-1,897 tok/s;
+// the same at head_dim 128: 8B 670-674 -> 665-668. Shapes only: the grid
+// never depends on past_len.
 constexpr uint64_t kDecodeGridBlocks = 512;
+uint64_t decode_part_span(const AttentionArgs& a) { return a.head_dim == 64 ? 64 : 128; }
 uint64_t decode_parts(const AttentionArgs& a) {
-    uint64_t parts = (a.max_seq + 127) / 128;
+    uint64_t parts = (a.max_seq + decode_part_span(a) - 1) / decode_part_span(a);
     const uint64_t rows = a.batch * a.kv_heads;
     const uint64_t by_grid = rows ? (kDecodeGridBlocks + rows - 1) / rows : 1;
     if (parts > by_grid) parts = by_grid;
@@ -1101,10 +1105,11 @@ hipError_t launch_decode(const AttentionArgs& a, Geo g, const Workspace& ws, hip
                     : attn_decode<DVv, RTv, true, false, K><<<grid, 256, lds, s>>>(SL_DECODE_ARGS))   \
      : paged ? attn_decode<DVv, RTv, false, true, K><<<grid, 256, lds, s>>>(SL_DECODE_ARGS)           \
              : attn_decode<DVv, RTv, false, false, K><<<grid, 256, lds, s>>>(SL_DECODE_ARGS))
-    // 8-key tiles where the partials were capped by the grid size (batch 8,
-    // 8B: 2,617-2,624 -> 2,689-2,690 tok/s; at batch 1 they cost 642-644 ->
-    // 629-634 tok/s), for head_dim 64 and 128
-    const bool short_tiles = parts < (a.max_seq + 127) / 128 && dv <= 2;
+    // 8-key tiles at head_dim 64, and at 128 where the partials were capped
+    // by the grid size (batch 8, 8B: 2,617-2,624 -> 2,689-2,690 tok/s; at
+    // batch 1, with the partials unchanged, they cost 642-644 -> 629-634)
+    const bool short_tiles =
+        dv == 1 || (dv == 2 && parts < (a.max_seq + decode_part_span(a) - 1) / decode_part_span(a));
 #define SL_DECODE(DVv, RTv) (short_tiles ? SL_DECODE_K(DVv, RTv, 2) : SL_DECODE_K(DVv, RTv, 4))
 #define SL_DECODE_LONG(DVv, RTv) SL_DECODE_K(DVv, RTv, 4)
     switch (dv * 100 + rt) {

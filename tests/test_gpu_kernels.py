@@ -218,7 +218,8 @@ ATT_SHAPES = [
     (1, 1, 0, 3, 1, 1, 2, 4, 3),
     (1, 2, 1, 32, 8, 1, 1000, 128, 1100),   # 8B-shaped decode step
     (1, 1, 0, 32, 8, 1, 300, 64, 512),      # 1B-shaped decode step
-    (1, 1, 0, 32, 8, 1, 1500, 64, 2048),    # 1B-shaped, 16 partials: one per merge thread
+    (1, 1, 0, 32, 8, 1, 1500, 64, 2048),    # 1B-shaped: 32 partials of 64 positions, 8-key tiles
+    (1, 1, 0, 32, 8, 1, 3990, 64, 4096),    # head_dim 64 at 4096 positions: 64 partials, four per merge thread
     (8, 1, 0, 32, 8, 1, 77, 128, 128),      # batch-8 decode
     (1, 1, 0, 32, 8, 100, 0, 128, 128),     # prefill, tiled path
     (1, 2, 0, 32, 8, 70, 30, 64, 128),      # chunked prefill after a prefix, tiled path

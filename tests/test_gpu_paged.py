@@ -29,22 +29,23 @@ def upload(hip, a):
     return BufferRef(b, 0, a.size)
 
 
-def run_step(hip, cache, pool_host, layer, rng, batch):
+def run_step(hip, cache, pool_host, layer, rng, batch, h=H, hkv=HKV, d=D):
     """One decode step on the GPU and the oracle; returns the oracle pool."""
-    q = rng.uniform(-1, 1, batch * H * D).astype(np.float32)
-    k = rng.uniform(-1, 1, batch * HKV * D).astype(np.float32)
-    v = rng.uniform(-1, 1, batch * HKV * D).astype(np.float32)
-    out = hip.allocate_f32(batch * H * D, 256)
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    q = rng.uniform(-1, 1, batch * h * d).astype(np.float32)
+    k = rng.uniform(-1, 1, batch * hkv * d).astype(np.float32)
+    v = rng.uniform(-1, 1, batch * hkv * d).astype(np.float32)
+    out = hip.allocate_f32(batch * h * d, 256)
     cache.sync()
-    cache.attention(Op.causal_attention(layer, H, HKV, D, SCALE), upload(hip, q), upload(hip, k), upload(hip, v),
-                    BufferRef(out, 0, batch * H * D), batch)
-    got = hip.read_f32(out, batch * H * D)
+    cache.attention(Op.causal_attention(layer, h, hkv, d, scale), upload(hip, q), upload(hip, k), upload(hip, v),
+                    BufferRef(out, 0, batch * h * d), batch)
+    got = hip.read_f32(out, batch * h * d)
     p = cache.pool
     want, new_pool = oracle.paged_attention_decode(q, k, v, pool_host, p.tables()[:batch].ravel(),
                                                    p.seq_lens()[:batch], batch, LAYERS, layer, p.num_pages,
-                                                   p.page_size, p.pages_per_seq, H, HKV, D, SCALE)
-    for i in range(batch * H):
-        assert_normwise(got[i * D:(i + 1) * D], want[i * D:(i + 1) * D])
+                                                   p.page_size, p.pages_per_seq, h, hkv, d, scale)
+    for i in range(batch * h):
+        assert_normwise(got[i * d:(i + 1) * d], want[i * d:(i + 1) * d])
     return new_pool
 
 
@@ -61,6 +62,26 @@ def test_mixed_lengths_shuffled_pages(hip):
         pool.admit(seq)
         pool.set_length(seq, n)
     want_pool = run_step(hip, cache, host, 1, rng, 4)
+    np.testing.assert_array_equal(hip.read_f32(cache.pool_buffer, cache.pool_elements), want_pool)
+
+
+@pytest.mark.parametrize("lengths", [[0, 300, 550, 2040], [1500]])
+def test_mixed_lengths_head_dim_64(hip, lengths):
+    """The 1B decode geometry (32 query heads over 8 KV heads of 64, 8-key
+    tiles, one partial per 64 positions of a row's 2048-position capacity up
+    to the grid's cap): four rows at 0-2040 positions, and one row alone at
+    1500 (32 partials)."""
+    rng = np.random.default_rng(51 + len(lengths))
+    b = len(lengths)
+    pool = PagePool(num_pages=b * 128 + 8, page_size=16, pages_per_seq=128, max_batch=b)
+    rng.shuffle(pool.free)
+    cache = PagedKvCache(hip, LAYERS, 8, 64, pool)
+    host = rng.uniform(-1, 1, cache.pool_elements).astype(np.float32)
+    hip.upload_f32(cache.pool_buffer, host)
+    for seq, n in enumerate(lengths):
+        pool.admit(seq)
+        pool.set_length(seq, n)
+    want_pool = run_step(hip, cache, host, 0, rng, b, h=32, hkv=8, d=64)
     np.testing.assert_array_equal(hip.read_f32(cache.pool_buffer, cache.pool_elements), want_pool)
 
 

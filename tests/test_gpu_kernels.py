@@ -586,3 +586,24 @@ def test_rms_norm_matmul_parity(hip, quantized, rows, hidden, out_f):
     got = read(hip, orf).reshape(rows, out_f)
     for i in range(rows):
         assert_normwise(got[i], want[i])
+
+
+@pytest.mark.parametrize("rows,hidden,out_f", [(64, 4096, 256), (17, 2048, 128), (48, 8192, 64)])
+def test_rms_norm_matmul_int4_many_rows(hip, rows, hidden, out_f):
+    """RmsNormMatMul on INT4 weights at more than 16 rows: the norm inside the
+    q-GEMM's activation split. Normwise per row against the oracle (1e-4)."""
+    r = rng(rows * 3 + hidden)
+    x = r.uniform(-2, 2, rows * hidden).astype(np.float32)
+    wt = r.uniform(0.5, 1.5, hidden).astype(np.float32)
+    w = (r.standard_normal((out_f, hidden)) * 0.1).astype(np.float32)
+    _, xr = put(hip, x)
+    _, wtr = put(hip, wt)
+    wr, wv, w = quant_weight(hip, w, QuantFormat.INT4, 128)
+    _, orf = out_buf(hip, rows * out_f)
+    hip.dispatch(Op.rms_norm_matmul(1e-5), [xr, wtr, wr],
+                 [Value.f32([rows, hidden]), Value.f32([hidden], ValueRole.PARAM), wv], [orf],
+                 [Value.f32([rows, out_f])])
+    want = oracle.rms_norm_matmul(x, wt, w, rows, hidden, out_f, 1e-5).reshape(rows, out_f)
+    got = read(hip, orf).reshape(rows, out_f)
+    for i in range(rows):
+        assert_normwise(got[i], want[i])
